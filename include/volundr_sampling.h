@@ -1,0 +1,117 @@
+/* volundr_sampling.h - C ABI of the MI355X token-selection library (libvolundr_sampling.so).
+ *
+ * The library replaces the token-selection hot path of volundr-mlx:
+ *   - vs_sample_batch   : Sampler.sample for a batch of rows (volundr-mlx/sampler.py:100-156), called per row
+ *                         by scheduler.py:424 / session.py:615 through Sampler.choose (sampler.py:83-98);
+ *   - vs_verify_greedy  : the greedy verify step of speculative decoding: first-max argmax over the valid
+ *                         vocabulary and the accept prefix (volundr-mlx/spec/specdec.py:326-336 for B=1,
+ *                         volundr-mlx/scheduler.py:462-470 for B<=4), plus the chosen-token logprob.
+ * The reference has no function boundary for these (NumPy and inline MLX ops); the Python host in
+ * volundr-mlx_amd/volundr_amd keeps sampler.py's call surface on top of these entry points.
+ *
+ * Conventions: every pointer argument except `ws` and `params` host-side arrays is a DEVICE pointer; all work is
+ * stream-ordered on `stream` (a hipStream_t; 0 = the null stream); nothing is allocated inside the hot calls.
+ * Return codes: 0 = OK; VS_EINVAL = bad argument; VS_EWORKSPACE = workspace too small; VS_EHIP = a HIP runtime
+ * call failed. vs_last_error() describes the last failure of the calling thread.
+ * Workspaces must be zeroed once (vs_workspace_init) before first use; the kernels leave them zeroed again.
+ * Calls that share one workspace must be ordered on one stream.
+ */
+#ifndef VOLUNDR_SAMPLING_H
+#define VOLUNDR_SAMPLING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vs_stream_t; /* hipStream_t, declared without the HIP headers */
+
+enum { VS_OK = 0, VS_EINVAL = -1, VS_EWORKSPACE = -2, VS_EHIP = -3 };
+
+/* Logit element types. bf16 and f16 rows are widened to float32 exactly, as sampler.py:94 does with
+ * logits.astype(mx.float32). */
+enum { VS_F32 = 0, VS_BF16 = 1, VS_F16 = 2 };
+
+/* vs_row_params.flags */
+enum {
+  VS_ROW_GREEDY = 1u /* Sampling.greedy (session.py:466-467): top_k == 1 or temperature < 1e-6 -> np.argmax of the
+                        processed row over the full vocabulary, first maximum (sampler.py:127-128) */
+};
+
+/* out_flags bits */
+enum {
+  VS_OUT_DRAW_BOUNDARY = 1u << 0, /* the scaled draw u*z lies within 1e-6*z of a CDF boundary */
+  VS_OUT_TOPP_BOUNDARY = 1u << 1, /* the top-p cut lies within 1e-6 of a cumulative boundary */
+  VS_OUT_GREEDY = 1u << 3,        /* the row took the greedy argmax */
+  VS_OUT_NOFINITE = 1u << 4,      /* no finite logit: np.argmax of the row (sampler.py:131-132) */
+  VS_OUT_COOP = 1u << 5,          /* the distribution was resolved by the row-cooperative radix select */
+  VS_OUT_GATHER = 1u << 6,        /* the distribution was resolved in one workgroup after a gather */
+  VS_OUT_TIMEOUT = 1u << 31       /* an inter-workgroup wait hit its spin limit: results of this row are invalid */
+};
+
+/* Per-row sampling parameters (the fields of session.py:439-456 that Sampler.sample reads, sampler.py:100-156).
+ * 80 bytes, 8-byte aligned. Index ranges are [begin, end) into the shared arrays of vs_sample_batch. */
+typedef struct vs_row_params {
+  float temperature;        /* sampler.py:129 t = float32(temperature) */
+  float top_p;              /* sampler.py:145; >= 1 disables */
+  float min_p;              /* sampler.py:149; <= 0 disables */
+  float repetition_penalty; /* sampler.py:118-120; 1 disables */
+  float frequency_penalty;  /* sampler.py:121 */
+  float presence_penalty;   /* sampler.py:121 */
+  int32_t top_k;            /* sampler.py:133; 0 = off (None and 0 both mean off) */
+  uint32_t flags;           /* VS_ROW_GREEDY */
+  double u;                 /* the uniform draw in [0,1) (sampler.py:154 self.uniform()) */
+  int64_t hist_begin, hist_end; /* token history (the multiset behind Sampler.counts, sampler.py:77-78) */
+  int32_t bias_begin, bias_end; /* additive biases, ids sorted ascending, equal ids in application order
+                                   (budget extra then logit_bias, sampler.py:104-109) */
+  int32_t supp_begin, supp_end; /* suppressed ids, sorted: -inf before the penalties (sampler.py:110-112) */
+  int32_t stop_begin, stop_end; /* stop ids masked while produced < min_new_tokens, sorted: -inf after the
+                                   penalties (sampler.py:123-126); the host passes an empty range otherwise */
+} vs_row_params;
+
+/* Sampler.sample for B rows of logits (row r starts at element r*ld; ld >= V).
+ *   params     : device array [B] of vs_row_params
+ *   hist       : device int32 token ids, indexed by params[r].hist_begin..hist_end (may be NULL if all empty);
+ *                ids outside [0, V) are ignored
+ *   bias_ids/bias_vals, mask_ids : device arrays indexed by the bias / supp / stop ranges (may be NULL if empty)
+ *   out_ids    : int32 [B] token ids
+ *   out_logprob: float32 [B] log(pr[j]/z) of the drawn token (greedy rows: log-softmax of the processed row)
+ *   out_flags  : uint32 [B] VS_OUT_* bits (may be NULL)
+ *   out_keep   : int32 [B] size of the distribution drawn from (may be NULL)
+ *   ws         : device workspace of at least vs_sample_workspace_bytes(B, V) bytes, zeroed once beforehand
+ * Replaces: volundr-mlx/sampler.py:100-156 (Sampler.sample), applied per row as scheduler.py:416-425 does. */
+int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                    const int32_t* hist, const int32_t* bias_ids, const float* bias_vals, const int32_t* mask_ids,
+                    int32_t* out_ids, float* out_logprob, uint32_t* out_flags, int32_t* out_keep, void* ws,
+                    size_t ws_bytes, vs_stream_t stream);
+
+size_t vs_sample_workspace_bytes(int B, int V);
+
+/* Greedy speculative verify over logits [B, T, V] (row (b,t) starts at element (b*T + t)*ld).
+ *   drafts     : int32 [B, T-1], the draft tokens inp[:, 1:] of the verify input
+ *   out_argmax : int32 [B, T], first-max argmax over [0, vocab_valid)
+ *   out_accept : int32 [B], nacc = sum(cumprod(drafts == argmax[:, :-1]))
+ *   out_logprob: float32 [B, T], x[argmax] - logsumexp(x[:vocab_valid]) (may be NULL)
+ * Replaces: volundr-mlx/spec/specdec.py:326-327 and volundr-mlx/scheduler.py:462-463 (tok, nacc). */
+int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t ld, int vocab_valid,
+                     const int32_t* drafts, int32_t* out_argmax, int32_t* out_accept, float* out_logprob, void* ws,
+                     size_t ws_bytes, vs_stream_t stream);
+
+size_t vs_verify_workspace_bytes(int B, int T, int V);
+
+/* Zero a workspace (stream-ordered). */
+int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
+
+/* Text of the calling thread's last error ("" if none). */
+const char* vs_last_error(void);
+
+/* Library ABI version (increments on any signature or struct change). */
+int vs_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOLUNDR_SAMPLING_H */
