@@ -1,0 +1,189 @@
+"""Benchmark of the token-selection hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+A step is one vs_sample_batch call over the B=16 x V=163840 mixed-parameter batch (configuration C3, the one
+BASELINE.json's metric names), with logits, parameters and histories already resident in HBM. Logits rotate over
+`--slots` device buffers (> 256 MB in total by default), so every step reads them from HBM and not from the 256 MB
+Infinity Cache. Printed (one JSON line on stdout):
+  value       end-to-end microseconds per step (host-issued launches back to back, HIP events on the launch stream)
+  roofline    algorithmic bytes per launch / average kernel duration (event pairs around each launch) vs 8 TB/s
+  cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
+The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "volundr-mlx_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "sampling step latency µs + HBM GB/s at B=16, V=163840 on 1 MI355X"
+PEAK_GBPS = 8000.0
+V = 163840
+
+
+def algo_bytes_sample(d, B):
+    """Logits read once + histories read once + per-row params + outputs (ids, logprob, flags, keep)."""
+    x = d["logits"]
+    h = 0 if d["hists"] is None else d["hists"].size * 4
+    return x.size * 4 + h + B * 88 + B * 16
+
+
+def algo_bytes_verify(d):
+    B, T, _ = d["logits_bf16"].shape
+    return d["logits_bf16"].size * 2 + d["drafts"].size * 4 + B * T * 8 + B * 4
+
+
+def time_calls(torch, call, nslots, steps, warmup):
+    """-> (end-to-end us per step, average kernel us from per-launch event pairs)."""
+    for i in range(warmup):
+        call(i % nslots)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        call(i % nslots)
+    t1.record()
+    torch.cuda.synchronize()
+    e2e = t0.elapsed_time(t1) * 1000.0 / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        call(i % nslots)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    kern = sum(a.elapsed_time(b) for a, b in ev) * 1000.0 / steps
+    return e2e, kern
+
+
+def bench_sample(torch, dev, d, steps, warmup, nslots):
+    from volundr_amd import ops
+
+    B = d["logits"].shape[0]
+    x = torch.from_numpy(d["logits"]).to(dev)
+    slots = [x] + [x.clone() for _ in range(nslots - 1)]
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
+    call = ops.PreparedSample(slots, rows)
+    cold = time_calls(torch, call, nslots, steps, warmup)
+    warm = time_calls(torch, call, 1, steps, warmup)
+    flags = call.out.flags.cpu().numpy()
+    assert not any((int(f) & 0xFFFFFFFF) >> 31 for f in flags), "timeout flag set"
+    return cold, warm, algo_bytes_sample(d, B)
+
+
+def bench_verify(torch, dev, d, steps, warmup, nslots):
+    import numpy as np
+
+    from volundr_amd import ops
+
+    x = torch.from_numpy(d["logits_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
+    slots = [x] + [x.clone() for _ in range(nslots - 1)]
+    call = ops.PreparedVerify(slots, torch.from_numpy(d["drafts"]).to(dev))
+    cold = time_calls(torch, call, nslots, steps, warmup)
+    warm = time_calls(torch, call, 1, steps, warmup)
+    acc = call.out.accept.cpu().numpy()
+    return cold, warm, algo_bytes_verify(d), int(acc.sum() + len(acc))
+
+
+def cpu_baseline(d, budget_s=10.0):
+    """The oracle (NumPy restatement of sampler.py) row by row, single-threaded, for about budget_s seconds."""
+    from oracle import sampler_ref as S
+
+    B = d["logits"].shape[0]
+    counts = [S.counts_from_history(h) for h in d["hists"]] if d["hists"] is not None else [{}] * B
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for i in range(B):
+            S.sample(d["logits"][i], d["params"][i], float(d["u"][i]), counts[i])
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(dt * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"{n} passes over the {B} rows of the same synthetic batch (counts built outside the timed "
+                      f"loop), NumPy oracle of sampler.py:100-156, os.cpu_count()={os.cpu_count()}",
+            "tokens_per_s": round(B / dt, 1)}
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/traffic_<name>.json)."""
+    p = ROOT / "profiles" / f"traffic_{name}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--slots", type=int, default=32, help="rotating logits buffers (cold-HBM measurement)")
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-others", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the token-selection path is per-row and needs no collectives; "
+              "run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from volundr_amd import synth
+
+    dev = torch.device("cuda:0")
+    d = synth.CONFIGS[a.config](seed=0)
+    B = d["logits"].shape[0]
+    (e2e, kern), (e2e_w, kern_w), algo = bench_sample(torch, dev, d, a.steps, a.warmup, a.slots)
+    others = {}
+    if not a.no_others:
+        for name in ("c1", "c5"):
+            if name == a.config:
+                continue
+            dd = synth.CONFIGS[name](seed=0)
+            (oe, ok), (we, wk), ab = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others[name] = {"us_per_step": round(oe, 2), "kernel_us": round(ok, 2), "warm_us_per_step": round(we, 2),
+                            "warm_kernel_us": round(wk, 2), "algo_bytes": ab,
+                            "hbm_gbps": round(ab / (ok * 1e-6) / 1e9, 1),
+                            "tokens_per_s": round(dd["logits"].shape[0] / (oe * 1e-6), 1)}
+        for name in ("c2", "c4"):
+            dd = synth.CONFIGS[name](seed=0)
+            (oe, ok), (we, wk), ab, ntok = bench_verify(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others[name] = {"us_per_step": round(oe, 2), "kernel_us": round(ok, 2), "warm_us_per_step": round(we, 2),
+                            "warm_kernel_us": round(wk, 2), "algo_bytes": ab,
+                            "hbm_gbps": round(ab / (ok * 1e-6) / 1e9, 1),
+                            "tokens_per_s": round(ntok / (oe * 1e-6), 1)}
+    cpu = None if a.no_cpu else cpu_baseline(d)
+    ach = algo / (kern * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(e2e, 2), "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(e2e / 1000.0, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{a.config.upper()}: B={B} V={V} fp32 mixed-parameter sampling (BASELINE configs[2])",
+                   "B": B, "V": V, "history_len": None if d["hists"] is None else int(d["hists"].shape[1]),
+                   "logit_slots": a.slots},
+        "tokens_per_s": round(B / (e2e * 1e-6), 1),
+        "hbm_gbps": round(algo / (e2e * 1e-6) / 1e9, 1),
+        "kernel_us": round(kern, 2), "warm_us_per_step": round(e2e_w, 2), "warm_kernel_us": round(kern_w, 2),
+        "kernels_per_step": 1,
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_GBPS, 4), "traffic": load_traffic(a.config),
+                     "algo_bytes": algo},
+        "cpu_baseline": cpu,
+        "other_configs": others,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

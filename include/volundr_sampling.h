@@ -9,7 +9,7 @@
  * The reference has no function boundary for these (NumPy and inline MLX ops); the Python host in
  * volundr-mlx_amd/volundr_amd keeps sampler.py's call surface on top of these entry points.
  *
- * Conventions: every pointer argument except `ws` and `params` host-side arrays is a DEVICE pointer; all work is
+ * Conventions: every pointer argument is a DEVICE pointer (ws included); all work is
  * stream-ordered on `stream` (a hipStream_t; 0 = the null stream); nothing is allocated inside the hot calls.
  * Return codes: 0 = OK; VS_EINVAL = bad argument; VS_EWORKSPACE = workspace too small; VS_EHIP = a HIP runtime
  * call failed. vs_last_error() describes the last failure of the calling thread.
@@ -52,19 +52,20 @@ enum {
 };
 
 /* Per-row sampling parameters (the fields of session.py:439-456 that Sampler.sample reads, sampler.py:100-156).
- * 80 bytes, 8-byte aligned. Index ranges are [begin, end) into the shared arrays of vs_sample_batch. */
+ * 88 bytes, 8-byte aligned. Index ranges are [begin, end) into the shared arrays of vs_sample_batch.
+ * top_p and min_p stay float64 because the reference compares them with float64 sums (sampler.py:146,150). */
 typedef struct vs_row_params {
   float temperature;        /* sampler.py:129 t = float32(temperature) */
-  float top_p;              /* sampler.py:145; >= 1 disables */
-  float min_p;              /* sampler.py:149; <= 0 disables */
-  float repetition_penalty; /* sampler.py:118-120; 1 disables */
-  float frequency_penalty;  /* sampler.py:121 */
-  float presence_penalty;   /* sampler.py:121 */
-  int32_t top_k;            /* sampler.py:133; 0 = off (None and 0 both mean off) */
+  float repetition_penalty; /* sampler.py:118-120 (float32); 1 disables */
+  float frequency_penalty;  /* sampler.py:121 (float32) */
+  float presence_penalty;   /* sampler.py:121 (float32) */
+  int32_t top_k;            /* sampler.py:133-134; 0 = off (None and 0 both mean off); the host maps k < 0 to 1 */
   uint32_t flags;           /* VS_ROW_GREEDY */
+  double top_p;             /* sampler.py:145; >= 1 disables */
+  double min_p;             /* sampler.py:149; <= 0 disables */
   double u;                 /* the uniform draw in [0,1) (sampler.py:154 self.uniform()) */
   int64_t hist_begin, hist_end; /* token history (the multiset behind Sampler.counts, sampler.py:77-78) */
-  int32_t bias_begin, bias_end; /* additive biases, ids sorted ascending, equal ids in application order
+  int32_t bias_begin, bias_end; /* additive float32 biases, ids sorted ascending, equal ids in application order
                                    (budget extra then logit_bias, sampler.py:104-109) */
   int32_t supp_begin, supp_end; /* suppressed ids, sorted: -inf before the penalties (sampler.py:110-112) */
   int32_t stop_begin, stop_end; /* stop ids masked while produced < min_new_tokens, sorted: -inf after the

@@ -70,7 +70,7 @@ def seed_state(seed: int) -> int:
 def counts_from_history(hist) -> dict:
     """The `counts` dict that Sampler.accept builds (sampler.py:77-78) from a token history, in first-seen order."""
     c: dict = {}
-    for t in hist:
+    for t in (() if hist is None else hist):
         t = int(t)
         c[t] = c.get(t, 0) + 1
     return c

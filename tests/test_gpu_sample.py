@@ -1,0 +1,173 @@
+"""GPU parity of vs_sample_batch (through the C ABI via volundr_amd.ops) against the NumPy oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_ref as S
+from parity import check_sample
+from volundr_amd import sample_batch, synth
+from volundr_amd._lib import OUT_COOP, OUT_GATHER, OUT_GREEDY, OUT_NOFINITE
+from volundr_amd.session import Sampling
+
+pytestmark = pytest.mark.gpu
+
+
+def run(dev, x, params, u, hists=None, produced=None, dtype=torch.float32, label=""):
+    xt = torch.from_numpy(x).to(dev).to(dtype)
+    xr = xt.float().cpu().numpy()  # the oracle sees exactly the widened values the kernel reads
+    print(f"[{label}] B={x.shape[0]} V={x.shape[1]} dtype={dtype}", flush=True)
+    out = sample_batch(xt, params, u, hists, produced)
+    torch.cuda.synchronize()
+    refs = [S.sample(xr[i], params[i], float(u[i]), S.counts_from_history(hists[i]) if hists is not None else {},
+                     0 if produced is None else produced[i]) for i in range(x.shape[0])]
+    nb = check_sample(out, refs, label)
+    return out, refs, nb
+
+
+def rand_params(rng, n, V):
+    ps = []
+    for _ in range(n):
+        ps.append(Sampling(temperature=float(rng.choice([0.0, 0.5, 0.9, 1.0, 1.6])),
+                           top_k=int(rng.choice([0, 1, 2, 7, 20, 50, 300])),
+                           top_p=float(rng.choice([1.0, 0.95, 0.8, 0.3])),
+                           min_p=float(rng.choice([0.0, 0.0, 0.05])),
+                           repetition_penalty=float(rng.choice([1.0, 1.1, 1.3])),
+                           presence_penalty=float(rng.choice([0.0, 0.3])),
+                           frequency_penalty=float(rng.choice([0.0, 0.1]))))
+    return ps
+
+
+@pytest.mark.parametrize("V", [1000, 5003, 40000])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_mix(dev, V, seed):
+    rng = np.random.default_rng(100 + seed)
+    B = 12
+    x = (rng.standard_normal((B, V)) * rng.choice([0.2, 1.0, 3.0], size=(B, 1))).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    hists = [rng.integers(0, V, size=int(rng.integers(0, 300))) for _ in range(B)]
+    run(dev, x, ps, rng.random(B), hists, label=f"mix V{V} s{seed}")
+
+
+def test_bf16_rows(dev):
+    rng = np.random.default_rng(7)
+    B, V = 6, 30000
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    run(dev, x, ps, rng.random(B), dtype=torch.bfloat16, label="bf16")  # many exact ties after rounding
+
+
+def test_coop_path_near_flat(dev):
+    rng = np.random.default_rng(11)
+    B, V = 4, 50000
+    x = (rng.standard_normal((B, V)) * 0.1).astype(np.float32)
+    ps = [Sampling(top_p=0.95), Sampling(top_p=1.0), Sampling(top_p=0.5, min_p=0.9), Sampling(top_k=3000, top_p=0.9)]
+    out, refs, _ = run(dev, x, ps, rng.random(B), label="coop")
+    fl = out.flags.cpu().numpy()
+    assert all(f & OUT_COOP for f in fl)
+
+
+def test_gather_path(dev):
+    rng = np.random.default_rng(12)
+    B, V = 3, 20000
+    x = (rng.standard_normal((B, V)) * 30).astype(np.float32)  # exp(-40) filter keeps a few dozen
+    ps = [Sampling(top_k=0, top_p=p, temperature=1.0) for p in (1.0, 0.9, 0.5)]
+    out, refs, _ = run(dev, x, ps, rng.random(B), label="gather")
+    assert all(f & OUT_GATHER for f in out.flags.cpu().numpy())
+
+
+def test_small_n_no_filter(dev):
+    # <= 4096 finite tokens: no exp(-40) filter (sampler.py:137), kept = all finite (gather or coop)
+    rng = np.random.default_rng(13)
+    V = 4000
+    x = (rng.standard_normal((2, V)) * 0.5).astype(np.float32)
+    x[1, 1500:] = -np.inf
+    run(dev, x, [Sampling(top_p=0.99), Sampling()], rng.random(2), label="n<=4096")
+
+
+def test_edits(dev):
+    rng = np.random.default_rng(14)
+    B, V = 5, 9000
+    x = (rng.standard_normal((B, V))).astype(np.float32)
+    ps = [Sampling(logit_bias=[(5, 20.0), (5, 1.5), (V + 3, 1.0)], top_k=10),
+          Sampling(suppress_tokens=[int(np.argmax(x[1]))], top_k=5, repetition_penalty=0.5),
+          Sampling(stop_token_ids=[int(np.argmax(x[2]))], min_new_tokens=3, top_k=1),
+          Sampling(logit_bias=[(-1, 30.0)], top_p=0.7),
+          Sampling(frequency_penalty=0.7, presence_penalty=-0.2, repetition_penalty=1.4, top_k=0, top_p=0.9)]
+    hists = [None, [int(np.argmax(x[1]))] * 3, [], [1, 2, 3], list(np.argsort(-x[4])[:40]) * 3]
+    out, refs, _ = run(dev, x, ps, rng.random(B), hists, produced=[0, 0, 1, 0, 0], label="edits")
+    assert out.ids[0].item() == 5 and out.ids[3].item() == V - 1
+
+
+def test_nonfinite_rows(dev):
+    V = 3000
+    x = np.zeros((5, V), np.float32)
+    x[0, :] = -np.inf
+    x[1, :] = -np.inf
+    x[1, 7] = np.inf
+    x[2, 100] = np.nan
+    x[2, 50] = 4.0
+    x[3, :] = np.nan
+    x[4, :] = -np.inf
+    x[4, 2999] = 1.0
+    ps = [Sampling(), Sampling(top_k=5), Sampling(top_k=1), Sampling(top_k=0), Sampling(top_p=0.5)]
+    out, refs, _ = run(dev, x, ps, [0.3] * 5, label="nonfinite")
+    fl = out.flags.cpu().numpy()
+    assert fl[0] & OUT_NOFINITE and fl[1] & OUT_NOFINITE and fl[2] & OUT_GREEDY
+    assert out.ids.cpu().tolist() == [0, 7, 100, 0, 2999]
+
+
+def test_signed_zero_and_ties(dev):
+    V = 600
+    x = np.zeros((3, V), np.float32)
+    x[:, 10] = -0.0
+    x[0, 20:30] = 2.0
+    x[1, ::2] = -0.0
+    ps = [Sampling(top_k=1), Sampling(top_k=4), Sampling(top_k=7, temperature=0.5)]
+    run(dev, x, ps, [0.1, 0.99, 0.5], label="ties")
+
+
+def test_strided_rows_and_many_launches(dev):
+    rng = np.random.default_rng(15)
+    B, V = 100, 2500
+    big = torch.from_numpy((rng.standard_normal((B, V + 13)) * 2).astype(np.float32)).to(dev)
+    xt = big[:, :V]  # ld = V + 13: scalar-load path
+    ps = rand_params(rng, B, V)
+    u = rng.random(B)
+    out = sample_batch(xt, ps, u)
+    xr = xt.cpu().numpy()
+    refs = [S.sample(xr[i], ps[i], float(u[i])) for i in range(B)]
+    check_sample(out, refs, "strided B100")
+
+
+def test_deterministic(dev):
+    d = synth.c5(seed=3, B=4, H=1000)
+    xt = torch.from_numpy(d["logits"][:4]).to(dev)
+    a = sample_batch(xt, d["params"][:4], d["u"][:4], d["hists"][:4])
+    b = sample_batch(xt, d["params"][:4], d["u"][:4], d["hists"][:4])
+    assert torch.equal(a.ids, b.ids) and torch.equal(a.keep, b.keep)
+
+
+@pytest.mark.parametrize("name", ["c1", "c3", "c5"])
+def test_configs_full_size(dev, name):
+    d = synth.CONFIGS[name](seed=0)
+    out, refs, nb = run(dev, d["logits"], d["params"], d["u"], d["hists"], label=name)
+    print(f"{name}: {len(refs)} rows, {nb} CDF-boundary rows", flush=True)
+
+
+def test_sampler_shim_sequence(dev):
+    from volundr_amd.sampler import Sampler
+
+    rng = np.random.default_rng(16)
+    V = 7000
+    sp = Sampling(temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.2, presence_penalty=0.3, seed=99)
+    smp = Sampler(sp, vocab_valid=V)
+    counts, st, produced = {}, S.seed_state(99), 0
+    for step in range(12):
+        x = (rng.standard_normal(V) * 2).astype(np.float32)
+        tok = smp.choose(torch.from_numpy(x).to(dev))
+        st, u = S.xorshift64s_next(st)
+        ref = S.sample(x, sp, u, counts, produced)
+        assert tok == ref.token or ref.draw_boundary
+        counts[ref.token] = counts.get(ref.token, 0) + 1
+        produced += 1
+    assert smp.counts == counts

@@ -1,0 +1,64 @@
+"""GPU parity of vs_verify_greedy against the NumPy oracle: argmax and accept bit-exact, logprob within 1e-5."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import verify_ref as VR
+from volundr_amd import synth, verify_greedy
+
+pytestmark = pytest.mark.gpu
+
+
+def check(dev, bits_or_f32, drafts, vv, dtype, label):
+    B, T, V = bits_or_f32.shape
+    if bits_or_f32.dtype == np.uint16:
+        xt = torch.from_numpy(bits_or_f32.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(bits_or_f32).to(dev).to(dtype)
+    print(f"[{label}] B={B} T={T} V={V} vv={vv} {xt.dtype}", flush=True)
+    ref_in = xt.float().cpu().numpy()
+    dt = torch.from_numpy(drafts).to(dev) if T > 1 else None
+    o = verify_greedy(xt, dt, vv)
+    torch.cuda.synchronize()
+    tok, acc, lp = VR.verify(ref_in, drafts, vv)
+    assert np.array_equal(o.argmax.cpu().numpy(), tok), label
+    assert np.array_equal(o.accept.cpu().numpy(), acc), label
+    g = o.logprobs.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(g - lp) <= 1e-5 * np.abs(lp) + 1e-10), (label, np.max(np.abs(g - lp)))
+    return o
+
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+def test_configs(dev, name):
+    d = synth.CONFIGS[name](seed=0, tie_frac=0.2)
+    o = check(dev, d["logits_bf16"], d["drafts"], 163840, torch.bfloat16, name)
+    assert np.array_equal(o.accept.cpu().numpy(), d["accept"])
+
+
+def test_ties_and_vocab_valid(dev):
+    rng = np.random.default_rng(5)
+    x = rng.integers(-4, 5, size=(3, 6, 5000)).astype(np.float32)  # heavy ties: first max must win
+    drafts = np.argmax(x[..., :4990], -1)[:, :5].astype(np.int32)
+    drafts[1, 2] += 1
+    check(dev, x, drafts, 4990, torch.float32, "ties f32")
+    check(dev, x, drafts, 4990, torch.bfloat16, "ties bf16")
+    check(dev, x, drafts, 4990, torch.float16, "ties f16")
+
+
+def test_single_position_and_odd_sizes(dev):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((5, 1, 12345)).astype(np.float32)
+    check(dev, x, np.zeros((5, 0), np.int32), 12345, torch.float32, "T=1")
+    x = rng.standard_normal((2, 9, 777)).astype(np.float32)
+    d = np.argmax(x, -1)[:, :8].astype(np.int32)
+    check(dev, x, d, 777, torch.float32, "odd")
+
+
+def test_nonfinite(dev):
+    x = np.zeros((1, 3, 300), np.float32)
+    x[0, 0, 5] = np.nan
+    x[0, 1, :] = -np.inf
+    x[0, 2, 9] = np.inf
+    x[0, 2, 10] = np.inf
+    o = verify_greedy(torch.from_numpy(x).to(dev), torch.tensor([[5, 0]], dtype=torch.int32, device=dev), 300)
+    assert o.argmax.cpu().tolist() == [[5, 0, 9]] and o.accept.item() == 2

@@ -1,0 +1,81 @@
+"""CPU checks of the boundary: the C-ABI library loads and exports every symbol the header declares; host packing
+follows sampler.py's parameter semantics. No device calls."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from volundr_amd import _lib, pack_rows
+from volundr_amd.session import Sampling
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_header_symbols_exported():
+    L = _lib.load()
+    hdr = (ROOT / "include" / "volundr_sampling.h").read_text()
+    names = set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(vs_\w+)\s*\(", hdr, re.M))
+    assert names == set(_lib.EXPORTS)
+    for n in names:
+        assert hasattr(L, n)
+    assert L.vs_version() == 1
+    assert L.vs_sample_workspace_bytes(16, 163840) > 0
+
+
+def test_row_struct_size_matches_header():
+    hdr = (ROOT / "include" / "volundr_sampling.h").read_text()
+    assert "88 bytes" in hdr and _lib.ROW_DTYPE.itemsize == 88
+
+
+def test_errors_without_device_calls():
+    L = _lib.load()
+    assert L.vs_sample_batch(0, 0, -1, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
+    assert b"B < 0" in L.vs_last_error()
+    assert L.vs_sample_batch(0, 0, 0, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_OK
+    assert L.vs_verify_greedy(0, 0, 1, 0, 10, 10, 10, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
+
+
+def test_pack_rows_semantics():
+    sps = [Sampling(top_k=None, temperature=0.7, logit_bias=[(3, 1.0), (1, 2.0), (3, 0.5), (99, 1.0)],
+                    suppress_tokens=[4, 4, 50, -1], stop_token_ids=[2], min_new_tokens=1),
+           Sampling(top_k=-3, temperature=1e-7)]
+    p = pack_rows(sps, [0.25, 0.5], V=10, histories=[[1, 1, 2], None], produced=[0, 5], extras=[[(3, -1.0)], None])
+    r0, r1 = p.params
+    assert r0["top_k"] == 0 and r0["flags"] == 0 and r0["temperature"] == np.float32(0.7)
+    assert r1["top_k"] == 1 and r1["flags"] == _lib.VS_ROW_GREEDY  # temperature < 1e-6 -> greedy
+    # biases sorted by id, equal ids in application order (extra first), ids >= V dropped
+    b = slice(r0["bias_begin"], r0["bias_end"])
+    assert p.bias_ids[b].tolist() == [1, 3, 3, 3] and p.bias_vals[b].tolist() == [2.0, -1.0, 1.0, 0.5]
+    assert p.mask_ids[r0["supp_begin"]:r0["supp_end"]].tolist() == [4, 9]   # -1 wraps to V-1
+    assert p.mask_ids[r0["stop_begin"]:r0["stop_end"]].tolist() == [2]
+    assert r1["stop_end"] == r1["stop_begin"]
+    assert p.hist[r0["hist_begin"]:r0["hist_end"]].tolist() == [1, 1, 2] and r1["hist_end"] == r1["hist_begin"]
+    with pytest.raises(ValueError):
+        pack_rows([Sampling()], [0.1, 0.2], V=10)
+
+
+def test_no_cpu_fallback():
+    import torch
+
+    from volundr_amd import sample_batch, verify_greedy
+
+    with pytest.raises(ValueError):
+        sample_batch(torch.zeros(1, 10), [Sampling()], [0.5])
+    with pytest.raises(ValueError):
+        verify_greedy(torch.zeros(1, 2, 10), torch.zeros(1, 1, dtype=torch.int32))
+
+
+def test_budget_logic():
+    from volundr_amd.sampler import Budget
+
+    b = Budget(4, 0.0, [1, 2, 7], 7, 8)   # <think>=7 open in the prompt tail
+    assert b.open == 0
+    assert [b.act(i)[0] for i in range(4)] == ["none"] * 4
+    assert b.act(4) == ("force", 8)
+    assert b.act(5) == ("bias", [(7, -np.inf)])
+    b = Budget(10, 1.5, [7, 8], 7, 8)     # closed in the prompt: never opens
+    assert b.open is None and b.act(20) == ("none", None)
+    b = Budget(10, 1.5, [], 7, 8)
+    b.accept(0, 7)
+    assert b.open == 1 and b.act(9) == ("bias", [(8, 1.5)]) and b.act(5) == ("none", None)

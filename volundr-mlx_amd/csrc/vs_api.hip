@@ -1,0 +1,65 @@
+// vs_api.hip - library-wide C entry points: error text, workspace zeroing, version; cached device properties.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/volundr_sampling.h"
+#include "vs_host.h"
+
+namespace vs {
+
+static thread_local std::string g_err;
+unsigned long long* g_trace = nullptr;
+
+void set_error(const std::string& msg) { g_err = msg; }
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+int hip_fail(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return VS_EHIP;
+}
+
+static std::mutex g_mu;
+static DevInfo g_dev[64];
+static bool g_have[64];
+
+const DevInfo* dev_info() {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_have[d]) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, d) != hipSuccess) return nullptr;
+    g_dev[d].device = d;
+    g_dev[d].cus = p.multiProcessorCount;
+    g_dev[d].lds_per_block = p.sharedMemPerBlock;
+    g_dev[d].coop = p.cooperativeLaunch;
+    g_have[d] = true;
+  }
+  return &g_dev[d];
+}
+
+}  // namespace vs
+
+extern "C" {
+
+const char* vs_last_error(void) { return vs::g_err.c_str(); }
+
+int vs_version(void) { return 1; }
+
+#ifdef VS_TRACE
+void vs_debug_set_trace(void* p) { vs::g_trace = (unsigned long long*)p; }
+#endif
+
+int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream) {
+  if (!ws && bytes) return vs::fail(VS_EINVAL, "vs_workspace_init: null workspace");
+  if (!bytes) return VS_OK;
+  hipError_t e = hipMemsetAsync(ws, 0, bytes, (hipStream_t)stream);
+  if (e != hipSuccess) return vs::hip_fail(e, "vs_workspace_init: hipMemsetAsync");
+  return VS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,1340 @@
+// vs_sample.hip - batched Sampler.sample (volundr-mlx/sampler.py:100-156) as one cooperative HIP kernel for gfx950.
+//
+// Layout: row r of the batch is split into G contiguous vocabulary chunks, one 512-thread workgroup each
+// (split-vocab, so that B <= 16 rows still occupy the 256 CUs). A workgroup reads its chunk from HBM exactly once
+// with 16-byte loads and keeps it in VGPRs (<= 24 values per lane) for every later pass. The G workgroups of a
+// row sit on one XCD (blockIdx -> row mapping below) and talk through a per-row control block in the workspace.
+//
+// Per row, by class (decided from the row's parameters, identically in every workgroup):
+//   GREEDY  (Sampling.greedy)        local first-max argmax + logsumexp partials -> last workgroup merges.
+//   TOPK    (1 <= top_k <= kcap)     local top-k by 64-bit key -> last workgroup sorts the G*k candidates and runs
+//                                    softmax / top-p / min-p / draw on the k survivors in one wave, in the order
+//                                    sampler.py:140-156 uses.
+//   FULL    (top-k off or large)     row max + finite count over a spin barrier; the kept set (sampler.py:
+//                                    133-139) gets a mass histogram; if it has <= 1024 members they are gathered
+//                                    and one workgroup finishes as for TOPK, otherwise top-p and the draw are
+//                                    resolved by a row-cooperative radix select on the keys, weighted by
+//                                    fixed-point probability mass (deterministic integer sums).
+// No full-vocabulary sort happens anywhere.
+#include "vs_common.h"
+#include "vs_host.h"
+
+#pragma clang fp contract(off)
+
+namespace vs {
+
+constexpr int SNT = 512;         // threads per workgroup
+constexpr int SNW = SNT / WAVE;  // waves per workgroup
+constexpr int EPT_MAX = 24;      // logits per lane kept in VGPRs
+constexpr int NBIN = 256;        // radix digit = 8 bits
+constexpr int MAX_ROUNDS = 24;   // histogram slots per row (8 count rounds + 1 + 7 + 7 mass rounds)
+constexpr int GMAX = 64;         // workgroups per row
+constexpr int GCAP = 1024;       // gather capacity of the FULL path
+constexpr int SORT_MAX = 1024;   // largest in-workgroup sort
+constexpr int KEYS_CAP = 4096;   // LDS key area (32 KB)
+constexpr int KCAP = 256;        // largest top_k of the TOPK class
+constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
+
+enum RowClass { CLS_GREEDY = 0, CLS_TOPK = 1, CLS_FULL = 2 };
+
+// Per-row control block; all zero between calls.
+struct RowCtl {
+  uint32_t bar;     // spin-barrier arrivals
+  uint32_t done;    // workgroups finished
+  uint32_t nfin;    // finite count of the row
+  uint32_t mkey;    // ord32 of the largest finite logit
+  u64 amkey;        // np.argmax key of the row
+  uint32_t gcount;  // gather reservations
+  uint32_t mcnt;    // min-p kept count
+  u64 mfix;         // min-p kept fixed-point mass
+  double mf64;      // min-p kept float64 mass
+  uint32_t err;     // a workgroup of the row timed out
+  uint32_t pad[3];
+};
+static_assert(sizeof(RowCtl) == 64, "RowCtl layout");
+
+struct Part {  // one per workgroup, written with device-coherent stores
+  u64 amkey;
+  uint32_t nfin;
+  uint32_t kc;
+  float mf;
+  uint32_t pad;
+  double se;
+};
+static_assert(sizeof(Part) == 32, "Part layout");
+
+struct HistSlot {
+  uint32_t cnt[NBIN];
+  u64 fix[NBIN];
+  double f64[NBIN];
+  u64 mk[NBIN];
+};
+
+constexpr size_t OFF_PART = sizeof(RowCtl);
+constexpr size_t OFF_CAND = OFF_PART + sizeof(Part) * GMAX;
+constexpr size_t OFF_GATHER = OFF_CAND + sizeof(u64) * KEYS_CAP;
+constexpr size_t OFF_HIST = OFF_GATHER + sizeof(u64) * GCAP;
+constexpr size_t ROW_WS = OFF_HIST + sizeof(HistSlot) * MAX_ROUNDS;
+
+struct SampleArgs {
+  const void* logits;
+  int64_t ld;
+  int B;     // rows in this launch
+  int row0;  // first batch row of this launch
+  int V;
+  int G;
+  int CH;
+  int NV;      // vector loads per lane
+  int vec_ok;  // 16-byte loads allowed
+  int has_hist;
+  int lds_ch;  // chunk length the LDS areas are sized for
+  int kcap;    // TOPK class bound for this launch
+  uint32_t spin_limit;
+  double fix_scale;  // probability -> fixed point
+  const vs_row_params* params;
+  const int32_t* hist;
+  const int32_t* bias_ids;
+  const float* bias_vals;
+  const int32_t* mask_ids;
+  int32_t* out_ids;
+  float* out_lp;
+  uint32_t* out_flags;
+  int32_t* out_keep;
+  char* ws;
+  unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
+};
+
+// LDS layout (dynamic): [R0: max(CH*4 + GCAP*8, KEYS_CAP*8)] [tk: SNT u64] [hist] [scratch]
+// R0 holds, in turn: the penalty counts (cnt, CH u32); then either the TOPK/merge keys (keys, <= KEYS_CAP u64) or,
+// for FULL rows, the processed chunk (xv, CH floats) followed by the gather keys (fkeys, <= GCAP u64).
+struct Smem {
+  uint32_t* cnt;  // penalty counts
+  float* xv;      // FULL rows: the processed chunk
+  u64* fkeys;     // FULL rows: gathered keys
+  u64* keys;
+  u64* tk;
+  uint32_t* hc;
+  u64* hfix;
+  double* hf64;
+  u64* hmk;
+  u64* red64;
+  double* redf;
+  int* redi;
+  int* misc;
+};
+
+__host__ __device__ inline size_t xv_bytes(int CH) { return ((size_t)CH * 4 + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t region0(int CH) {
+  const size_t a = xv_bytes(CH) + (size_t)GCAP * 8, b = (size_t)KEYS_CAP * 8;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ Smem carve(char* base, int CH) {
+  Smem s;
+  s.cnt = (uint32_t*)base;
+  s.xv = (float*)base;
+  s.fkeys = (u64*)(base + xv_bytes(CH));
+  s.keys = (u64*)base;
+  char* p = base + region0(CH);
+  s.tk = (u64*)p;
+  p += SNT * 8;
+  s.hfix = (u64*)p;
+  p += NBIN * 8;
+  s.hf64 = (double*)p;
+  p += NBIN * 8;
+  s.hmk = (u64*)p;
+  p += NBIN * 8;
+  s.hc = (uint32_t*)p;
+  p += NBIN * 4;
+  s.red64 = (u64*)p;
+  p += SNW * 8;
+  s.redf = (double*)p;
+  p += SNW * 8;
+  s.redi = (int*)p;
+  p += SNW * 4;
+  s.misc = (int*)p;
+  return s;
+}
+static size_t smem_bytes(int CH) { return region0(CH) + SNT * 8 + NBIN * (8 + 8 + 8 + 4) + SNW * (8 + 8 + 4) + 64 * 4; }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Histogram scan. One wave walks the 256 bins: lane L owns digits 255-4L .. 252-4L (descending key order), so the
+// bins are visited in rank order with one wave-wide scan and a ballot. Finds the first digit whose bin is non-empty
+// and whose inclusive cumulative weight reaches `target`; when none does (a target above the total by rounding) the
+// lowest non-empty digit, i.e. the last element. Weight = count (count mode) or fixed-point mass. Also returns the
+// cumulative sums of all higher digits. The caller has synchronised after filling the bins.
+// ---------------------------------------------------------------------------------------------------------------
+struct ScanOut {
+  int digit;
+  u64 cnt_before, fix_before;
+  double f64_before;
+  u64 cnt, fix;
+  double f64;
+  u64 mk;
+};
+
+__device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, double target) {
+  if (threadIdx.x < WAVE) {
+    const int L = threadIdx.x;
+    u64 c[4], w[4];
+    double f[4];
+    u64 lc = 0, lw = 0;
+    double lf = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = NBIN - 1 - (4 * L + i);
+      c[i] = s.hc[d];
+      w[i] = count_mode ? c[i] : s.hfix[d];
+      f[i] = s.hf64[d];
+      lc += c[i];
+      lw += w[i];
+      lf += f[i];
+    }
+    const u64 iw = wave_scan(lw), ic = wave_scan(lc);
+    const double iff = wave_scan(lf);
+    u64 cw = iw - lw, cc = ic - lc;
+    double cf = iff - lf;
+    int hit = -1, last = -1;
+    u64 hw = 0, hc2 = 0;
+    double hf = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (c[i] > 0) last = i;
+      if (hit < 0 && c[i] > 0 && (double)(cw + w[i]) >= target) {
+        hit = i;
+        hw = cw;
+        hc2 = cc;
+        hf = cf;
+      }
+      cw += w[i];
+      cc += c[i];
+      cf += f[i];
+    }
+    const unsigned long long hb = __ballot(hit >= 0);
+    int lane_sel, i_sel;
+    if (hb) {
+      lane_sel = __ffsll((long long)hb) - 1;
+      i_sel = lane_bcast(hit, lane_sel);
+    } else {
+      const unsigned long long lb = __ballot(last >= 0);
+      lane_sel = lb ? 63 - __clzll((long long)lb) : 0;
+      i_sel = lb ? lane_bcast(last, lane_sel) : 0;
+      if (i_sel < 0) i_sel = 0;
+    }
+    if (L == lane_sel) {
+      if (!hb) {
+        hw = iw - lw;
+        hc2 = ic - lc;
+        hf = iff - lf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (i < i_sel) {
+            hw += w[i];
+            hc2 += c[i];
+            hf += f[i];
+          }
+        }
+      }
+      const int d = NBIN - 1 - (4 * L + i_sel);
+      s.misc[0] = d;
+      s.red64[0] = hc2;
+      s.red64[1] = hw;
+      s.redf[0] = hf;
+      s.red64[2] = s.hc[d];
+      s.red64[3] = s.hfix[d];
+      s.redf[1] = s.hf64[d];
+      s.red64[4] = s.hmk[d];
+    }
+  }
+  __syncthreads();
+  ScanOut o;
+  o.digit = s.misc[0];
+  o.cnt_before = s.red64[0];
+  o.fix_before = count_mode ? 0 : s.red64[1];
+  o.f64_before = s.redf[0];
+  o.cnt = s.red64[2];
+  o.fix = s.red64[3];
+  o.f64 = s.redf[1];
+  o.mk = s.red64[4];
+  __syncthreads();
+  return o;
+}
+
+__device__ __forceinline__ void hist_clear(const Smem& s) {
+  const int t = threadIdx.x;
+  if (t < NBIN) {
+    s.hc[t] = 0;
+    s.hfix[t] = 0;
+    s.hf64[t] = 0.0;
+    s.hmk[t] = 0;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void hist_add(const Smem& s, u64 key, int shift, u64 fx, double f) {
+  const int d = (int)((key >> shift) & 0xFF);
+  atomicAdd(&s.hc[d], 1u);
+  if (fx) atomicAdd(&s.hfix[d], fx);
+  if (f != 0.0) unsafeAtomicAdd(&s.hf64[d], f);
+  atomicMax(&s.hmk[d], key);
+}
+
+__device__ __forceinline__ bool prefix_match(u64 key, int shift, u64 prefix) {
+  return shift >= 56 ? true : ((key >> (shift + 8)) == prefix);
+}
+
+// k-th largest of n unique keys in LDS (1 <= k <= n): returns T with |{keys >= T}| == k. Radix select, 8-bit
+// digits from the top, stopping as soon as a bin is taken whole.
+__device__ __forceinline__ u64 block_kth(const Smem& s, const u64* keys, int n, int k) {
+  u64 prefix = 0;
+  int shift = 56;
+  int krem = k;
+  for (;;) {
+    hist_clear(s);
+    for (int i = threadIdx.x; i < n; i += SNT) {
+      const u64 key = keys[i];
+      if (prefix_match(key, shift, prefix)) atomicAdd(&s.hc[(key >> shift) & 0xFF], 1u);
+    }
+    __syncthreads();
+    const ScanOut o = hist_scan(s, true, (double)krem);
+    const int need = krem - (int)o.cnt_before;
+    const u64 np = (prefix << 8) | (u64)o.digit;
+    if ((int)o.cnt == need || shift == 0) return np << shift;
+    krem = need;
+    prefix = np;
+    shift -= 8;
+  }
+}
+
+// Bitonic compare-exchange of the element at position i with its partner i^j in stage (k, j), descending overall.
+__device__ __forceinline__ u64 bitonic_keep(u64 mine, u64 other, int i, int j, int k) {
+  const bool desc = (i & k) == 0;
+  const bool lower = (i & j) == 0;
+  const u64 mx = mine > other ? mine : other, mn = mine > other ? other : mine;
+  return (desc == lower) ? mx : mn;
+}
+
+// Sort a[0..n) descending (n <= SORT_MAX) in place, zero-padded to a power of two >= 64. Thread t holds positions t
+// and t+512 in registers; partners within a wave are exchanged with cross-lane moves, partners in other waves
+// through LDS, so most of the network needs no barrier. `a` must have room for the padded length (and >= SNT).
+__device__ __forceinline__ void block_sort_desc(u64* a, int n) {
+  int P = 64;
+  while (P < n) P <<= 1;
+  const int t = threadIdx.x;
+  __syncthreads();
+  u64 e0 = t < n ? a[t] : 0;
+  u64 e1 = (P > SNT && t + SNT < n) ? a[t + SNT] : 0;
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= SNT) {
+        const bool desc = (t & k) == 0;
+        const u64 mx = e0 > e1 ? e0 : e1, mn = e0 > e1 ? e1 : e0;
+        e0 = desc ? mx : mn;
+        e1 = desc ? mn : mx;
+      } else if (j >= WAVE) {
+        __syncthreads();
+        a[t] = e0;
+        if (P > SNT) a[t + SNT] = e1;
+        __syncthreads();
+        const u64 p0 = a[t ^ j];
+        e0 = bitonic_keep(e0, p0, t, j, k);
+        if (P > SNT) {
+          const u64 p1 = a[(t + SNT) ^ j];
+          e1 = bitonic_keep(e1, p1, t + SNT, j, k);
+        }
+      } else {
+        const u64 p0 = lane_xor_rt(e0, j);
+        e0 = bitonic_keep(e0, p0, t, j, k);
+        if (P > SNT) {
+          const u64 p1 = lane_xor_rt(e1, j);
+          e1 = bitonic_keep(e1, p1, t + SNT, j, k);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (t < P) a[t] = e0;
+  if (P > SNT && t + SNT < P) a[t + SNT] = e1;
+  __syncthreads();
+}
+
+struct Final {
+  int32_t token;
+  float lp;
+  uint32_t flags;
+  int32_t keep;
+};
+
+// sampler.py:141-156 on n <= SORT_MAX keys sorted descending in LDS (a[0] is the row maximum), in one wave: lane L
+// owns positions [L*E, L*E+E), so every sum and prefix is a lane-sequential loop plus one wave scan. The result is
+// broadcast to the whole workgroup.
+__device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n, const vs_row_params& P) {
+  constexpr int EM = SORT_MAX / WAVE;
+  if (threadIdx.x < WAVE) {
+    const int L = threadIdx.x;
+    const int E = (n + WAVE - 1) / WAVE;
+    const int i0 = L * E;
+    const float tt = P.temperature;
+    const float xs0 = key_value(a[0]) / tt;  // sampler.py:141 xs[0]
+    double pr[EM];
+    double ls = 0.0;
+#pragma unroll
+    for (int q = 0; q < EM; ++q) {
+      pr[q] = 0.0;
+      if (q < E && i0 + q < n) {
+        const float xs = key_value(a[i0 + q]) / tt;
+        const float d = xs - xs0;  // float32 subtraction (:142)
+        pr[q] = exp((double)d);    // float64 exp
+        ls += pr[q];
+      }
+    }
+    const double S = wave_sum(ls);  // :143
+    double lp = 0.0;
+#pragma unroll
+    for (int q = 0; q < EM; ++q) {
+      pr[q] = pr[q] / S;
+      lp += pr[q];
+    }
+    const double base = wave_scan(lp) - lp;  // cumulative mass before this lane's first position
+    int keep = n;
+    uint32_t flags = 0;
+    if (P.top_p < 1.0) {  // :145-148 first position with cumsum >= top_p
+      const double tp = P.top_p;
+      double c = base;
+      int hit = -1;
+      int fb = 0;
+#pragma unroll
+      for (int q = 0; q < EM; ++q) {
+        if (q < E && i0 + q < n) {
+          const double prev = c;
+          c += pr[q];
+          if (hit < 0 && c >= tp) {
+            hit = i0 + q;
+            fb = fabs(c - tp) < 1e-6 || fabs(prev - tp) < 1e-6;
+          }
+        }
+      }
+      const unsigned long long hb = __ballot(hit >= 0);
+      if (hb) {
+        const int ls2 = __ffsll((long long)hb) - 1;
+        keep = lane_bcast(hit, ls2) + 1;
+        if (lane_bcast(fb, ls2)) flags |= VS_OUT_TOPP_BOUNDARY;
+      }
+    }
+    if (P.min_p > 0.0) {  // :149-152 first position with pr < pr[0] * min_p
+      const double thr = lane_bcast(pr[0], 0) * P.min_p;
+      int hit = -1;
+#pragma unroll
+      for (int q = 0; q < EM; ++q)
+        if (hit < 0 && q < E && i0 + q < n && pr[q] < thr) hit = i0 + q;
+      const unsigned long long hb = __ballot(hit >= 0);
+      int cnt = hb ? lane_bcast(hit, __ffsll((long long)hb) - 1) : n;
+      cnt = cnt > 1 ? cnt : 1;
+      keep = keep < cnt ? keep : cnt;
+    }
+    double lz = 0.0;
+#pragma unroll
+    for (int q = 0; q < EM; ++q)
+      if (q < E && i0 + q < keep) lz += pr[q];
+    const double z = wave_sum(lz);  // :153
+    const double uz = P.u * z;      // :154
+    double c = base;
+    int hit = -1;
+    double hp = 0.0, hc = 0.0;
+#pragma unroll
+    for (int q = 0; q < EM; ++q) {
+      if (q < E && i0 + q < keep) {
+        c += pr[q];
+        if (hit < 0 && c >= uz) {
+          hit = i0 + q;
+          hp = pr[q];
+          hc = c;
+        }
+      }
+    }
+    const unsigned long long hb = __ballot(hit >= 0);
+    int j;
+    if (hb) {  // :155 searchsorted(cumsum, u*z, 'left')
+      const int ls2 = __ffsll((long long)hb) - 1;
+      j = lane_bcast(hit, ls2);
+      hp = lane_bcast(hp, ls2);
+      hc = lane_bcast(hc, ls2);
+    } else {  // :156 min(j, keep-1): the last kept position
+      j = keep - 1;
+      const int owner = j / E, qq = j - owner * E;
+      double cc = base, pp = 0.0;
+#pragma unroll
+      for (int q = 0; q < EM; ++q)
+        if (q <= qq && q < E) {
+          cc += pr[q];
+          pp = pr[q];
+        }
+      hp = lane_bcast(pp, owner);
+      hc = lane_bcast(cc, owner);
+    }
+    if (L == 0) {
+      const double tol = 1e-6 * z;
+      if (fabs(hc - uz) < tol || (j >= 1 && fabs(hc - hp - uz) < tol)) flags |= VS_OUT_DRAW_BOUNDARY;
+      s.misc[1] = (int)key_index(a[j]);
+      s.misc[2] = keep;
+      s.misc[3] = (int)flags;
+      s.redf[0] = log(hp / z);
+    }
+  }
+  __syncthreads();
+  Final f;
+  f.token = s.misc[1];
+  f.keep = s.misc[2];
+  f.flags = (uint32_t)s.misc[3];
+  f.lp = (float)s.redf[0];
+  __syncthreads();
+  return f;
+}
+
+__device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Final& f) {
+  if (threadIdx.x == 0) {
+    const int r = A.row0 + row;
+    A.out_ids[r] = f.token;
+    A.out_lp[r] = f.lp;
+    if (A.out_flags) A.out_flags[r] = f.flags;
+    if (A.out_keep) A.out_keep[r] = f.keep;
+  }
+}
+
+// Sorted-id range search: first position in ids[b, e) with ids[p] >= x.
+__device__ __forceinline__ int lower_bound_ids(const int32_t* ids, int b, int e, int32_t x) {
+  while (b < e) {
+    const int m = (b + e) >> 1;
+    if (ids[m] < x)
+      b = m + 1;
+    else
+      e = m;
+  }
+  return b;
+}
+
+template <int DT>
+struct DTraits;
+template <>
+struct DTraits<VS_F32> {
+  typedef float LT;
+  static constexpr int VEC = 4;
+  __device__ static float cv(LT v) { return v; }
+};
+template <>
+struct DTraits<VS_BF16> {
+  typedef uint16_t LT;
+  static constexpr int VEC = 8;
+  __device__ static float cv(LT v) { return bf16_to_f32(v); }
+};
+template <>
+struct DTraits<VS_F16> {
+  typedef uint16_t LT;
+  static constexpr int VEC = 8;
+  __device__ static float cv(LT v) { return f16_to_f32(v); }
+};
+
+// Count the history tokens that fall in [lo, hi) into cnt[tok - lo] (the counts Sampler.accept keeps,
+// sampler.py:77-78). Four 16-byte loads per lane are in flight per iteration.
+__device__ __forceinline__ void count_history(const int32_t* h, int64_t b, int64_t e, int lo, int hi, uint32_t* cnt) {
+  const int t = threadIdx.x;
+  int64_t a = (b + 3) & ~(int64_t)3;  // first 16-byte aligned position
+  if (a > e) a = e;
+  for (int64_t i = b + t; i < a; i += SNT) {
+    const int32_t tok = h[i];
+    if (tok >= lo && tok < hi) atomicAdd(&cnt[tok - lo], 1u);
+  }
+  const int64_t nv = (e - a) >> 2;  // whole int4 vectors
+  const int4* hv = (const int4*)(h + a);
+  constexpr int U = 4;
+  for (int64_t v0 = t; v0 < nv; v0 += (int64_t)SNT * U) {
+    int4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t vi = v0 + (int64_t)u * SNT;
+      r[u] = vi < nv ? hv[vi] : make_int4(-1, -1, -1, -1);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t tk[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (tk[q] >= lo && tk[q] < hi) atomicAdd(&cnt[tk[q] - lo], 1u);
+    }
+  }
+  for (int64_t i = a + nv * 4 + t; i < e; i += SNT) {
+    const int32_t tok = h[i];
+    if (tok >= lo && tok < hi) atomicAdd(&cnt[tok - lo], 1u);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
+  typedef DTraits<DT> TR;
+  typedef typename TR::LT LT;
+  constexpr int VEC = TR::VEC;
+  constexpr int NVMAX = EPT_MAX / VEC;
+  extern __shared__ __align__(16) char smem_raw[];
+  const Smem s = carve(smem_raw, A.lds_ch);
+  const int t = threadIdx.x;
+  const int G = A.G;
+
+  // blockIdx -> (row, chunk): consecutive workgroups are dealt round-robin to the 8 XCDs, so workgroups with equal
+  // blockIdx % 8 share an XCD (and its L2). Give each row G workgroups of one XCD when the grid allows it.
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+  const int row = l / G, g = l % G;
+  const int grow = A.row0 + row;
+  const vs_row_params P = A.params[grow];
+  char* rws = A.ws + (size_t)row * ROW_WS;
+  RowCtl* ctl = (RowCtl*)rws;
+  Part* parts = (Part*)(rws + OFF_PART);
+  u64* cand = (u64*)(rws + OFF_CAND);
+  u64* gather = (u64*)(rws + OFF_GATHER);
+  HistSlot* hslots = (HistSlot*)(rws + OFF_HIST);
+
+  const int V = A.V;
+  const int lo = g * A.CH;
+  const int hi = min(V, lo + A.CH);
+  const int NV = A.NV;
+  VS_TR(A, 0);
+  VS_TRC(A, 30);
+
+  // ---- load the chunk into VGPRs (one HBM read) ----
+  float v[EPT_MAX];
+  const LT* rowp = (const LT*)A.logits + (int64_t)grow * A.ld;
+#pragma unroll
+  for (int j = 0; j < NVMAX; ++j) {
+    if (j < NV) {
+      const int base = lo + (j * SNT + t) * VEC;
+      if (A.vec_ok && base + VEC <= hi) {
+        const uint4 raw = *(const uint4*)(rowp + base);
+        const LT* e = (const LT*)&raw;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) v[j * VEC + q] = TR::cv(e[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) v[j * VEC + q] = (base + q < hi) ? TR::cv(rowp[base + q]) : __builtin_nanf("");
+      }
+    }
+  }
+#define ELEM(j, q) (lo + ((j) * SNT + t) * VEC + (q))
+#define FOR_ELEMS(BODY)                                 \
+  _Pragma("unroll") for (int j = 0; j < NVMAX; ++j) {   \
+    if (j < NV) {                                       \
+      _Pragma("unroll") for (int q = 0; q < VEC; ++q) { \
+        const int e = ELEM(j, q);                       \
+        if (e < hi) {                                   \
+          float& x = v[j * VEC + q];                    \
+          (void)x;                                      \
+          BODY                                          \
+        }                                               \
+      }                                                 \
+    }                                                   \
+  }
+  VS_TR(A, 1);
+
+  // ---- logit edits and penalties (sampler.py:104-126), float32 throughout ----
+  const bool has_bias = P.bias_end > P.bias_begin;
+  const bool has_supp = P.supp_end > P.supp_begin;
+  const bool has_stop = P.stop_end > P.stop_begin;
+  const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
+  const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
+  if (has_pen) {
+    for (int i = t; i < A.CH; i += SNT) s.cnt[i] = 0;
+    __syncthreads();
+    count_history(A.hist, P.hist_begin, P.hist_end, lo, hi, s.cnt);
+    __syncthreads();
+  }
+  if (has_bias || has_supp || has_pen || has_stop) {
+    FOR_ELEMS({
+      if (has_bias) {  // sampler.py:104-109, equal ids applied in list order
+        int p = lower_bound_ids(A.bias_ids, P.bias_begin, P.bias_end, e);
+        while (p < P.bias_end && A.bias_ids[p] == e) {
+          x = x + A.bias_vals[p];
+          ++p;
+        }
+      }
+      if (has_supp) {  // :110-112
+        const int p = lower_bound_ids(A.mask_ids, P.supp_begin, P.supp_end, e);
+        if (p < P.supp_end && A.mask_ids[p] == e) x = -__builtin_inff();
+      }
+      if (has_pen) {  // :113-122
+        const uint32_t c = s.cnt[e - lo];
+        if (c) {
+          float y = x;
+          if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
+          const float cf = (float)c;
+          const float fc = fpen * cf;
+          const float sub = fc + ppen;
+          y = y - sub;
+          x = y;
+        }
+      }
+      if (has_stop) {  // :123-126
+        const int p = lower_bound_ids(A.mask_ids, P.stop_begin, P.stop_end, e);
+        if (p < P.stop_end && A.mask_ids[p] == e) x = -__builtin_inff();
+      }
+    })
+    __syncthreads();  // the count area is reused below
+  }
+  VS_TR(A, 2);
+
+  const int top_k = P.top_k;
+  const int cls = (P.flags & VS_ROW_GREEDY) ? CLS_GREEDY : ((top_k >= 1 && top_k <= A.kcap) ? CLS_TOPK : CLS_FULL);
+  int slot = 0;  // histogram slots used by this row (identical in all its workgroups)
+  uint32_t nbar = 0;
+  bool ok = true;
+
+  // Arrive at the row's done counter; true in the last workgroup of the row.
+  auto arrive_done = [&]() -> bool { return block_arrive(&ctl->done, (uint32_t*)&s.misc[8]) == (uint32_t)(G - 1); };
+  auto cleanup = [&](int nrounds) {
+    // Only the last workgroup of the row gets here: restore the all-zero state of the row's workspace.
+    for (int r = 0; r < nrounds; ++r) {
+      HistSlot* hs = hslots + r;
+      if (t < NBIN) {
+        st_dev(&hs->cnt[t], 0u);
+        st_dev(&hs->fix[t], (u64)0);
+        st_dev(&hs->f64[t], 0.0);
+        st_dev(&hs->mk[t], (u64)0);
+      }
+    }
+    if (t < (int)(sizeof(RowCtl) / 4)) st_dev(&((uint32_t*)ctl)[t], 0u);
+  };
+  auto put_part = [&](u64 am, uint32_t nf, uint32_t kc, float mf, double se) {
+    if (t == 0) {
+      st_dev(&parts[g].amkey, am);
+      st_dev(&parts[g].nfin, nf);
+      st_dev(&parts[g].kc, kc);
+      st_dev(&parts[g].mf, mf);
+      st_dev(&parts[g].se, se);
+    }
+  };
+
+  if (cls == CLS_GREEDY) {
+    // ---- sampler.py:127-128: np.argmax(x), first maximum; logprob = log-softmax of the processed row ----
+    u64 am = 0;
+    float mf = -__builtin_inff();
+    FOR_ELEMS({
+      const u64 k = amkey64(x, (uint32_t)e);
+      am = k > am ? k : am;
+      if (is_finite(x)) mf = x > mf ? x : mf;
+    })
+    am = block_max<SNT>(am, s.red64);
+    mf = block_max<SNT>(mf, (float*)s.redf);
+    double se = 0.0;
+    if (is_finite(mf)) {
+      FOR_ELEMS({
+        if (is_finite(x)) se += exp((double)x - (double)mf);
+      })
+    }
+    se = block_sum<SNT>(se, s.redf);
+    put_part(am, 0, 0, mf, se);
+    VS_TR(A, 3);
+    if (arrive_done()) {
+      VS_TR(A, 4);
+      // last workgroup of the row: merge the G partials in one wave (G <= 64)
+      if (t < WAVE) {
+        u64 k = 0;
+        float m = -__builtin_inff();
+        double e = 0.0;
+        if (t < G) {
+          k = ld_dev(&parts[t].amkey);
+          m = ld_dev(&parts[t].mf);
+          e = ld_dev(&parts[t].se);
+        }
+        const u64 bam = wave_max(k);
+        const float M = wave_max(m);
+        const double S = wave_sum((e > 0.0 && is_finite(M)) ? e * exp((double)m - (double)M) : 0.0);
+        if (t == 0) {
+          const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
+          const int r = A.row0 + row;
+          A.out_ids[r] = (int32_t)key_index(bam);
+          A.out_lp[r] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
+          if (A.out_flags) A.out_flags[r] = VS_OUT_GREEDY;
+          if (A.out_keep) A.out_keep[r] = 0;
+        }
+      }
+      cleanup(0);
+    }
+    return;
+  }
+
+  if (cls == CLS_TOPK) {
+    // ---- local top-k by key among finite logits (sampler.py:133-136, ties toward the lower index) ----
+    const int k = top_k;
+    u64 tmax = 0, am = 0;
+    int nf = 0;
+    FOR_ELEMS({
+      const u64 ka = amkey64(x, (uint32_t)e);
+      am = ka > am ? ka : am;
+      if (is_finite(x)) {
+        ++nf;
+        const u64 kk = key64(x, (uint32_t)e);
+        tmax = kk > tmax ? kk : tmax;
+      }
+    })
+    const int nb_fin = block_sum<SNT>(nf, s.redi);
+    const int nz = block_sum<SNT>(tmax != 0 ? 1 : 0, s.redi);
+    am = block_max<SNT>(am, s.red64);
+    VS_TR(A, 10);
+    int kc = 0;
+    if (nb_fin > 0) {
+      // Lower bound L for the k-th largest key: the k-th largest lane maximum (the k lanes above it each hold a
+      // distinct key >= it). Only keys >= L can be in the local top-k.
+      u64 L = 1;
+      if (nb_fin > k && nz > k) {
+        s.tk[t] = tmax;
+        block_sort_desc(s.tk, SNT);
+        L = s.tk[k - 1];
+        __syncthreads();
+      }
+      VS_TR(A, 11);
+      if (t == 0) s.misc[4] = 0;
+      __syncthreads();
+      FOR_ELEMS({
+        if (is_finite(x)) {
+          const u64 kk = key64(x, (uint32_t)e);
+          if (kk >= L) {
+            const int p = atomicAdd(&s.misc[4], 1);
+            if (p < KEYS_CAP) s.keys[p] = kk;
+          }
+        }
+      })
+      __syncthreads();
+      const int C = s.misc[4];
+      __syncthreads();
+      VS_TR(A, 12);
+#ifdef VS_TRACE
+      if (t == 0 && A.trace) A.trace[(size_t)blockIdx.x * 32 + 19] = C;
+#endif
+      if (C <= SORT_MAX) {
+        block_sort_desc(s.keys, C);
+        VS_TR(A, 13);
+        kc = C < k ? C : k;
+        if (t < kc) st_dev(&cand[g * A.kcap + t], s.keys[t]);
+      } else {
+        // Many keys above the bound (few lanes hold finite values): radix select over the VGPR-resident chunk.
+        u64 prefix = 0;
+        int shift = 56, krem = k;
+        u64 T = 0;
+        for (;;) {
+          hist_clear(s);
+          FOR_ELEMS({
+            if (is_finite(x)) {
+              const u64 kk = key64(x, (uint32_t)e);
+              if (prefix_match(kk, shift, prefix)) atomicAdd(&s.hc[(kk >> shift) & 0xFF], 1u);
+            }
+          })
+          __syncthreads();
+          const ScanOut o = hist_scan(s, true, (double)krem);
+          const int need = krem - (int)o.cnt_before;
+          const u64 np = (prefix << 8) | (u64)o.digit;
+          if ((int)o.cnt == need || shift == 0) {
+            T = np << shift;
+            break;
+          }
+          krem = need;
+          prefix = np;
+          shift -= 8;
+        }
+        if (t == 0) s.misc[5] = 0;
+        __syncthreads();
+        FOR_ELEMS({
+          if (is_finite(x)) {
+            const u64 kk = key64(x, (uint32_t)e);
+            if (kk >= T) {
+              const int p = atomicAdd(&s.misc[5], 1);
+              if (p < A.kcap) st_dev(&cand[g * A.kcap + p], kk);
+            }
+          }
+        })
+        __syncthreads();
+        kc = min(s.misc[5], A.kcap);
+      }
+    }
+    put_part(am, (uint32_t)nb_fin, (uint32_t)kc, 0.0f, 0.0);
+    VS_TR(A, 3);
+    VS_TRC(A, 31);
+    if (arrive_done()) {
+      VS_TR(A, 4);
+      // ---- merge: the last workgroup of the row (partials read by one wave, G <= 64) ----
+      int* offs = (int*)s.tk;  // [2*G]: candidate offset and count per workgroup (tk is free until the sort)
+      if (t < WAVE) {
+        int c = 0, nf2 = 0;
+        u64 k2 = 0;
+        if (t < G) {
+          c = (int)ld_dev(&parts[t].kc);
+          nf2 = (int)ld_dev(&parts[t].nfin);
+          k2 = ld_dev(&parts[t].amkey);
+        }
+        const int incl = wave_scan(c);
+        const int tot = wave_sum(c);
+        const int nn = wave_sum(nf2);
+        const u64 bam2 = wave_max(k2);
+        if (t < G) {
+          offs[2 * t] = incl - c;
+          offs[2 * t + 1] = c;
+        }
+        if (t == 0) {
+          s.misc[6] = tot;
+          s.misc[7] = nn;
+          s.red64[0] = bam2;
+        }
+      }
+      __syncthreads();
+      const int C = s.misc[6];
+      const int n = s.misc[7];
+      const u64 bam = s.red64[0];
+      __syncthreads();
+      if (n == 0) {  // sampler.py:131-132
+        Final f;
+        f.token = (int32_t)key_index(bam);
+        f.lp = 0.0f;
+        f.flags = VS_OUT_NOFINITE;
+        f.keep = 0;
+        write_out(A, row, f);
+      } else {
+        for (int idx = t; idx < G * A.kcap; idx += SNT) {
+          const int i = idx / A.kcap, q = idx - i * A.kcap;
+          if (q < offs[2 * i + 1]) s.keys[offs[2 * i] + q] = ld_dev(&cand[idx]);
+        }
+        __syncthreads();
+        int keff = k < n ? k : n;  // sampler.py:133-134
+        if (keff < 1) keff = 1;
+        VS_TR(A, 5);
+        const u64* sorted;
+        if (C <= SORT_MAX) {
+          block_sort_desc(s.keys, C);  // sampler.py:140 on the candidates; the first keff are the top-k
+          sorted = s.keys;
+        } else {
+          const u64 T = block_kth(s, s.keys, C, keff);
+          if (t == 0) s.misc[9] = 0;
+          __syncthreads();
+          for (int i = t; i < C; i += SNT) {
+            const u64 kk = s.keys[i];
+            if (kk >= T) {
+              const int p = atomicAdd(&s.misc[9], 1);
+              if (p < SNT) s.tk[p] = kk;
+            }
+          }
+          __syncthreads();
+          block_sort_desc(s.tk, keff);
+          sorted = s.tk;
+        }
+        VS_TR(A, 6);
+        const Final f = wave_sample(s, sorted, keff, P);
+        VS_TR(A, 7);
+        write_out(A, row, f);
+      }
+      cleanup(0);
+    }
+    return;
+  }
+
+  // =================================== FULL class ===================================
+  // The chunk moves to LDS (xv): every later pass of this class reads it from there, so the 24 VGPRs of the
+  // chunk are free for the selection state.
+  FOR_ELEMS({ s.xv[e - lo] = x; })
+  __syncthreads();
+#define FOR_XV(BODY)                              \
+  for (int i_ = t; i_ < hi - lo; i_ += SNT) {     \
+    const int e = lo + i_;                        \
+    const float x = s.xv[i_];                     \
+    BODY                                          \
+  }
+  // ---- row statistics: finite count, largest finite logit, np.argmax key ----
+  {
+    int nf = 0;
+    uint32_t mk = 0;
+    u64 am = 0;
+    FOR_XV({
+      const u64 ka = amkey64(x, (uint32_t)e);
+      am = ka > am ? ka : am;
+      if (is_finite(x)) {
+        ++nf;
+        const uint32_t o = ord32(x);
+        mk = o > mk ? o : mk;
+      }
+    })
+    nf = block_sum<SNT>(nf, s.redi);
+    mk = block_max<SNT>(mk, (uint32_t*)s.redi);
+    am = block_max<SNT>(am, s.red64);
+    if (t == 0) {
+      if (nf) atomicAdd(&ctl->nfin, (uint32_t)nf);
+      if (mk) atomicMax(&ctl->mkey, mk);
+      atomicMax(&ctl->amkey, am);
+    }
+  }
+  ++nbar;
+  ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+  VS_TR(A, 3);
+  Final fin;
+  fin.token = -1;
+  fin.lp = 0.0f;
+  fin.flags = VS_OUT_TIMEOUT;
+  fin.keep = 0;
+  if (ok) {
+    const int n = (int)ld_relaxed(&ctl->nfin);
+    const uint32_t mkey = ld_relaxed(&ctl->mkey);
+    const u64 amk = ld_relaxed64(&ctl->amkey);
+    if (n == 0) {  // sampler.py:131-132
+      fin.token = (int32_t)key_index(amk);
+      fin.flags = VS_OUT_NOFINITE;
+    } else {
+      int k = top_k > 0 ? (top_k < n ? top_k : n) : n;  // sampler.py:133-134
+      if (k < 1) k = 1;
+      const float tt = P.temperature;
+      const float xmax = inv_ord32(mkey);
+      const float xs0 = xmax / tt;  // xs[0]: the maximum always survives
+      int mode = 0;                 // 0 all finite, 1 key >= Tk, 2 exp(-40) filter
+      u64 Tk = 0;
+      float thr = 0.0f;
+      if (k < n) {
+        // top-k with k beyond the TOPK class: cooperative count-weighted radix select (sampler.py:135-136)
+        mode = 1;
+        u64 prefix = 0;
+        int shift = 56;
+        int krem = k;
+        for (;;) {
+          hist_clear(s);
+          FOR_XV({
+            if (is_finite(x)) {
+              const u64 kk = key64(x, (uint32_t)e);
+              if (prefix_match(kk, shift, prefix)) atomicAdd(&s.hc[(kk >> shift) & 0xFF], 1u);
+            }
+          })
+          __syncthreads();
+          HistSlot* hs = hslots + slot;
+          if (t < NBIN && s.hc[t]) atomicAdd(&hs->cnt[t], s.hc[t]);
+          ++nbar;
+          ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+          if (!ok) break;
+          if (t < NBIN) {
+            s.hc[t] = ld_relaxed(&hs->cnt[t]);
+            s.hfix[t] = 0;
+            s.hf64[t] = 0.0;
+            s.hmk[t] = 0;
+          }
+          __syncthreads();
+          ++slot;
+          const ScanOut o = hist_scan(s, true, (double)krem);
+          const int need = krem - (int)o.cnt_before;
+          const u64 np = (prefix << 8) | (u64)o.digit;
+          if ((int)o.cnt == need || shift == 0) {
+            Tk = np << shift;
+            break;
+          }
+          krem = need;
+          prefix = np;
+          shift -= 8;
+        }
+      } else if (n > 4096) {
+        mode = 2;  // sampler.py:137-139: keep x/t >= m/t - 40 (float32)
+        thr = xs0 - 40.0f;
+      }
+      if (ok) {
+#define IS_CAND(x, kk) (is_finite(x) && (mode == 0 || (mode == 1 ? (kk) >= Tk : ((x) / tt) >= thr)))
+        const double scale = A.fix_scale;
+        VS_TR(A, 4);
+        // ---- mass histogram of the kept set (top digit) + bounded gather ----
+        hist_clear(s);
+        int cb = 0;
+        FOR_XV({
+          const u64 kk = key64(x, (uint32_t)e);
+          if (IS_CAND(x, kk)) {
+            ++cb;
+            const float d = x / tt - xs0;
+            const double pr = exp((double)d);
+            hist_add(s, kk, 56, (u64)(pr * scale + 0.5), pr);
+          }
+        })
+        cb = block_sum<SNT>(cb, s.redi);
+        if (t == 0) {
+          s.misc[9] = (int)atomicAdd(&ctl->gcount, (uint32_t)cb);
+          s.misc[10] = 0;
+        }
+        __syncthreads();
+        const int gbase = s.misc[9];
+        if (gbase + cb <= GCAP) {
+          FOR_XV({
+            const u64 kk = key64(x, (uint32_t)e);
+            if (IS_CAND(x, kk)) st_dev(&gather[gbase + atomicAdd(&s.misc[10], 1)], kk);
+          })
+        }
+        const int s1 = slot++;
+        {
+          HistSlot* hs = hslots + s1;
+          if (t < NBIN && s.hc[t]) {
+            atomicAdd(&hs->cnt[t], s.hc[t]);
+            atomicAdd(&hs->fix[t], s.hfix[t]);
+            unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
+            atomicMax(&hs->mk[t], s.hmk[t]);
+          }
+        }
+        ++nbar;
+        ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+        if (ok) {
+          const int total = (int)ld_relaxed(&ctl->gcount);
+          VS_TR(A, 5);
+          if (total <= GCAP) {
+            // ---- small kept set: one workgroup finishes exactly as for TOPK ----
+            if (g == 0) {
+              for (int i = t; i < total; i += SNT) s.fkeys[i] = ld_dev(&gather[i]);
+              __syncthreads();
+              block_sort_desc(s.fkeys, total);
+              fin = wave_sample(s, s.fkeys, total, P);
+              fin.flags |= VS_OUT_GATHER;
+            }
+          } else {
+            // ---- large kept set: cooperative mass-weighted radix select ----
+            HistSlot* h1 = hslots + s1;
+            auto load_slot = [&](HistSlot* hs) {
+              if (t < NBIN) {
+                s.hc[t] = ld_relaxed(&hs->cnt[t]);
+                s.hfix[t] = ld_relaxed64(&hs->fix[t]);
+                s.hf64[t] = ld_relaxed_f64(&hs->f64[t]);
+                s.hmk[t] = ld_relaxed64(&hs->mk[t]);
+              }
+              __syncthreads();
+            };
+            load_slot(h1);
+            const u64 Sfix = block_sum<SNT>(t < NBIN ? s.hfix[t] : (u64)0, s.red64);
+            const double Sf = block_sum<SNT>(t < NBIN ? s.hf64[t] : 0.0, s.redf);
+            // select: the first key (descending) whose inclusive cumulative mass reaches target
+            struct Sel {
+              u64 key, cnt_before, fix_before, fix;
+              double f64_before, f64;
+            };
+            auto select = [&](double target) -> Sel {
+              Sel r;
+              r.key = 0;
+              r.cnt_before = r.fix_before = r.fix = 0;
+              r.f64_before = r.f64 = 0.0;
+              load_slot(h1);
+              u64 prefix = 0;
+              int shift = 56;
+              for (;;) {
+                const ScanOut o = hist_scan(s, false, target - (double)r.fix_before);
+                r.cnt_before += o.cnt_before;
+                r.fix_before += o.fix_before;
+                r.f64_before += o.f64_before;
+                if (o.cnt <= 1 || shift == 0) {
+                  r.key = o.mk;
+                  r.fix = o.fix;
+                  r.f64 = o.f64;
+                  return r;
+                }
+                prefix = (prefix << 8) | (u64)o.digit;
+                shift -= 8;
+                // next digit: histogram of the candidates under this prefix
+                hist_clear(s);
+                FOR_XV({
+                  const u64 kk = key64(x, (uint32_t)e);
+                  if (IS_CAND(x, kk) && (kk >> (shift + 8)) == prefix) {
+                    const float d = x / tt - xs0;
+                    const double pr = exp((double)d);
+                    hist_add(s, kk, shift, (u64)(pr * scale + 0.5), pr);
+                  }
+                })
+                __syncthreads();
+                HistSlot* hs = hslots + slot;
+                ++slot;
+                if (t < NBIN && s.hc[t]) {
+                  atomicAdd(&hs->cnt[t], s.hc[t]);
+                  atomicAdd(&hs->fix[t], s.hfix[t]);
+                  unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
+                  atomicMax(&hs->mk[t], s.hmk[t]);
+                }
+                ++nbar;
+                ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+                if (!ok) return r;
+                load_slot(hs);
+              }
+            };
+            int keep = total;
+            u64 zfix = Sfix;
+            double zf = Sf;
+            uint32_t flags = VS_OUT_COOP;
+            if (P.top_p < 1.0) {  // sampler.py:145-148
+              const double tgt = P.top_p * (double)Sfix;
+              const Sel a = select(tgt);
+              if (ok) {
+                keep = (int)a.cnt_before + 1;
+                zfix = a.fix_before + a.fix;
+                zf = a.f64_before + a.f64;
+                const double tol = 1e-6 * (double)Sfix;
+                if (fabs((double)a.fix_before - tgt) < tol || fabs((double)zfix - tgt) < tol)
+                  flags |= VS_OUT_TOPP_BOUNDARY;
+              }
+            }
+            VS_TR(A, 6);
+            if (ok && P.min_p > 0.0) {  // sampler.py:149-152
+              const double pthr = (1.0 / Sf) * P.min_p;
+              int mc = 0;
+              u64 mfx = 0;
+              double mff = 0.0;
+              FOR_XV({
+                const u64 kk = key64(x, (uint32_t)e);
+                if (IS_CAND(x, kk)) {
+                  const float d = x / tt - xs0;
+                  const double pr = exp((double)d);
+                  if (!(pr / Sf < pthr)) {
+                    ++mc;
+                    mfx += (u64)(pr * scale + 0.5);
+                    mff += pr;
+                  }
+                }
+              })
+              mc = block_sum<SNT>(mc, s.redi);
+              mfx = block_sum<SNT>(mfx, s.red64);
+              mff = block_sum<SNT>(mff, s.redf);
+              if (t == 0) {
+                atomicAdd(&ctl->mcnt, (uint32_t)mc);
+                atomicAdd(&ctl->mfix, mfx);
+                unsafeAtomicAdd(&ctl->mf64, mff);
+              }
+              ++nbar;
+              ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+              if (ok) {
+                const int cm = (int)ld_relaxed(&ctl->mcnt);
+                const int km = cm > 1 ? cm : 1;
+                if (km < keep) {
+                  keep = km;
+                  if (cm >= 1) {
+                    zfix = ld_relaxed64(&ctl->mfix);
+                    zf = ld_relaxed_f64(&ctl->mf64);
+                  } else {
+                    zfix = (u64)(scale + 0.5);
+                    zf = 1.0;
+                  }
+                }
+              }
+            }
+            VS_TR(A, 7);
+            if (ok) {  // sampler.py:153-156
+              const double tgt = P.u * (double)zfix;
+              const Sel bsel = select(tgt);
+              if (ok) {
+                const float xb = key_value(bsel.key);
+                const float d = xb / tt - xs0;
+                fin.token = (int32_t)key_index(bsel.key);
+                fin.lp = (float)((double)d - log(zf));
+                fin.keep = keep;
+                const double tol = 1e-6 * (double)zfix;
+                if (fabs((double)bsel.fix_before - tgt) < tol ||
+                    fabs((double)(bsel.fix_before + bsel.fix) - tgt) < tol)
+                  flags |= VS_OUT_DRAW_BOUNDARY;
+                fin.flags = flags;
+              }
+            }
+          }
+        }
+#undef IS_CAND
+      }
+    }
+  }
+#undef FOR_XV
+  VS_TR(A, 9);
+  // In the gather case only workgroup 0 computed `fin`; in every other case all workgroups agree.
+  if (g == 0) write_out(A, row, fin);
+  if (!ok && t == 0) atomicOr(&ctl->err, 1u);  // a timed-out row clears every histogram slot
+  if (arrive_done()) {
+    const bool err = ld_relaxed(&ctl->err) != 0;
+    cleanup(err ? MAX_ROUNDS : slot);
+  }
+#undef FOR_ELEMS
+#undef ELEM
+}
+
+}  // namespace vs
+
+// =================================================================================================================
+// Host entry points
+// =================================================================================================================
+using namespace vs;
+
+extern "C" size_t vs_sample_workspace_bytes(int B, int V) {
+  (void)V;
+  const int rows = B < 1 ? 1 : (B > RPL_MAX ? RPL_MAX : B);
+  return (size_t)rows * ROW_WS;
+}
+
+extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                               const int32_t* hist, const int32_t* bias_ids, const float* bias_vals,
+                               const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
+                               int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
+  if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
+  if (B == 0) return VS_OK;
+  if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
+  if (ld < V) return fail(VS_EINVAL, "vs_sample_batch: ld < V");
+  if (dtype != VS_F32 && dtype != VS_BF16 && dtype != VS_F16) return fail(VS_EINVAL, "vs_sample_batch: bad dtype");
+  if (!logits || !params || !out_ids || !out_logprob || !ws)
+    return fail(VS_EINVAL, "vs_sample_batch: null logits/params/out_ids/out_logprob/ws");
+  const DevInfo* dv = dev_info();
+  if (!dv) return fail(VS_EHIP, "vs_sample_batch: no HIP device");
+  const int VEC = dtype == VS_F32 ? 4 : 8;
+  const int unit = SNT * VEC;
+  const int chmax = (EPT_MAX / VEC) * unit;
+  const int rows_target = B < RPL_MAX ? B : RPL_MAX;
+  const int gmin = (V + chmax - 1) / chmax;
+  if (gmin > GMAX) return fail(VS_EINVAL, "vs_sample_batch: V too large for one launch row");
+  int G = dv->cus / rows_target;
+  if (G < 1) G = 1;
+  if (G > GMAX) G = GMAX;
+  if (G < gmin) G = gmin;
+  int CH = (V + G - 1) / G;
+  CH = (CH + unit - 1) / unit * unit;
+  G = (V + CH - 1) / CH;
+  const int NV = CH / unit;
+  const int has_hist = hist != nullptr;
+  const int lds_ch = CH;
+  const size_t lds = smem_bytes(lds_ch);
+  if (lds > dv->lds_per_block) return fail(VS_EINVAL, "vs_sample_batch: LDS need exceeds the device limit");
+  const void* kfn = dtype == VS_F32    ? (const void*)vs_sample_kernel<VS_F32>
+                    : dtype == VS_BF16 ? (const void*)vs_sample_kernel<VS_BF16>
+                                       : (const void*)vs_sample_kernel<VS_F16>;
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, SNT, lds);
+  if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: occupancy query");
+  const int maxres = per_cu * dv->cus;
+  int RB = maxres / G;
+  if (RB > rows_target) RB = rows_target;
+  if (RB < 1) return fail(VS_EINVAL, "vs_sample_batch: a row does not fit on the device at once");
+  if (ws_bytes < (size_t)RB * ROW_WS) return fail(VS_EWORKSPACE, "vs_sample_batch: workspace too small");
+  int kcap = KEYS_CAP / G;
+  if (kcap > KCAP) kcap = KCAP;
+  int bits = 0;
+  while ((1ll << bits) < (long long)V) ++bits;
+  SampleArgs a;
+  a.logits = logits;
+  a.ld = ld;
+  a.V = V;
+  a.G = G;
+  a.CH = CH;
+  a.NV = NV;
+  a.vec_ok = ((uintptr_t)logits % 16 == 0) && (ld % VEC == 0);
+  a.has_hist = has_hist;
+  a.lds_ch = lds_ch;
+  a.kcap = kcap;
+  a.spin_limit = 1u << 21;
+  a.fix_scale = ldexp(1.0, 63 - bits);
+  a.params = params;
+  a.hist = hist;
+  a.bias_ids = bias_ids;
+  a.bias_vals = bias_vals;
+  a.mask_ids = mask_ids;
+  a.out_ids = out_ids;
+  a.out_lp = out_logprob;
+  a.out_flags = out_flags;
+  a.out_keep = out_keep;
+  a.ws = (char*)ws;
+  a.trace = g_trace;
+  for (int r0 = 0; r0 < B; r0 += RB) {
+    a.row0 = r0;
+    a.B = (B - r0) < RB ? (B - r0) : RB;
+    void* kargs[] = {&a};
+    e = hipLaunchCooperativeKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: cooperative launch");
+  }
+  return VS_OK;
+}

@@ -1,0 +1,260 @@
+// vs_verify.hip - greedy speculative verify for gfx950: first-max argmax over the valid vocabulary, the accept
+// prefix, and the chosen-token logprob, in one pass over [B, T, V] logits.
+//
+// Reference: tok = argmax(logits[..., :vv]) (volundr-mlx/spec/specdec.py:326, scheduler.py:462);
+//            nacc = sum(cumprod(inp[:, 1:] == tok[:, :-1])) (specdec.py:327, scheduler.py:463);
+//            logprob = x[tok] - logsumexp(x[:vv]) (log-softmax form of spec/check_verify.py:27-30; build-defined).
+//
+// Each (b, t) row is split into G chunks, one 256-thread workgroup each, so B*T = 17..68 rows still fill the
+// 256 CUs. A workgroup reads its chunk once with 16-byte loads into VGPRs, reduces (first-max key, finite max) with
+// wave64 reductions, then sum(exp(x - max)); the last workgroup of a row (done counter) merges the G partials, and
+// the last row of a request computes the accept length. No workgroup ever waits for another.
+#include "vs_common.h"
+#include "vs_host.h"
+
+#pragma clang fp contract(off)
+
+namespace vs {
+
+constexpr int VNT = 256;
+constexpr int VNW = VNT / WAVE;
+constexpr int VNV_MAX = 64;  // 16-byte loads per lane (streamed, not held)
+constexpr int VGMAX = 64;
+constexpr int VRMAX = 8192;  // rows (B*T) per call: the counters live at fixed offsets so any call finds them zero
+
+struct VPart {
+  u64 amkey;
+  float mf;
+  uint32_t pad;
+  double se;
+  u64 pad2;
+};
+static_assert(sizeof(VPart) == 32, "VPart layout");
+
+struct VerifyArgs {
+  const void* logits;
+  int64_t ld;
+  int B, T, V, vv;
+  int G, CH, NV, vec_ok;
+  const int32_t* drafts;
+  int32_t* out_argmax;
+  int32_t* out_accept;
+  float* out_lp;
+  char* ws;  // [VRMAX] row counters | [VRMAX] request counters | [R*G] VPart
+  unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
+};
+
+template <int DT>
+struct VTraits;
+template <>
+struct VTraits<VS_F32> {
+  static constexpr int VEC = 4;
+  __device__ static float get(const uint4& r, int q) { return ((const float*)&r)[q]; }
+  __device__ static float one(const void* p, int64_t i) { return ((const float*)p)[i]; }
+};
+template <>
+struct VTraits<VS_BF16> {
+  static constexpr int VEC = 8;
+  __device__ static float get(const uint4& r, int q) { return bf16_to_f32(((const uint16_t*)&r)[q]); }
+  __device__ static float one(const void* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
+};
+template <>
+struct VTraits<VS_F16> {
+  static constexpr int VEC = 8;
+  __device__ static float get(const uint4& r, int q) { return f16_to_f32(((const uint16_t*)&r)[q]); }
+  __device__ static float one(const void* p, int64_t i) { return f16_to_f32(((const uint16_t*)p)[i]); }
+};
+
+template <int DT>
+__global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
+  typedef VTraits<DT> TR;
+  constexpr int VEC = TR::VEC;
+  constexpr int U = 4;  // 16-byte loads in flight per lane
+  __shared__ u64 red64[VNW];
+  __shared__ float redf[VNW];
+  __shared__ double redd[VNW];
+  __shared__ uint32_t flag;
+  const int t = threadIdx.x;
+  const int G = A.G;
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+  const int row = l / G, g = l % G;
+  uint32_t* rowdone = (uint32_t*)A.ws;
+  uint32_t* reqdone = rowdone + VRMAX;
+  VPart* parts = (VPart*)(A.ws + 8 * VRMAX);
+
+  const int lo = g * A.CH;
+  const int hi = min(A.vv, lo + A.CH);
+  const char* rowp = (const char*)A.logits + (int64_t)row * A.ld * (DT == VS_F32 ? 4 : 2);
+  VS_TR(A, 0);
+
+  // One streaming pass: first-max key (np.argmax order, NaN first), running finite maximum m and
+  // s = sum(exp(x - m)) rescaled whenever m grows (float32 exp per element, float64 accumulation).
+  u64 am = 0;
+  float m = -__builtin_inff();
+  double se = 0.0;
+  for (int j0 = 0; j0 < A.NV; j0 += U) {
+    uint4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int base = lo + ((j0 + u) * VNT + t) * VEC;
+      raw[u] = make_uint4(0, 0, 0, 0);
+      if (j0 + u < A.NV && A.vec_ok && base + VEC <= hi) raw[u] = *(const uint4*)(rowp + (int64_t)base * (DT == VS_F32 ? 4 : 2));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u >= A.NV) continue;
+      const int base = lo + ((j0 + u) * VNT + t) * VEC;
+      const bool full = A.vec_ok && base + VEC <= hi;
+      float xs[VEC];
+#pragma unroll
+      for (int q = 0; q < VEC; ++q)
+        xs[q] = full ? TR::get(raw[u], q) : (base + q < hi ? TR::one(rowp, base + q) : -__builtin_inff());
+      float vm = -__builtin_inff();
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        if (base + q < hi) {
+          const u64 k = amkey64(xs[q], (uint32_t)(base + q));
+          am = k > am ? k : am;
+          if (is_finite(xs[q])) vm = xs[q] > vm ? xs[q] : vm;
+        }
+      }
+      if (vm > m) {
+        if (se > 0.0) se *= exp((double)m - (double)vm);
+        m = vm;
+      }
+      if (is_finite(m)) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+          if (base + q < hi && is_finite(xs[q])) acc += expf(xs[q] - m);
+        se += (double)acc;
+      }
+    }
+  }
+  VS_TR(A, 1);
+  // workgroup merge of (m, se) pairs and the key
+  am = block_max<VNT>(am, red64);
+  const float mb = block_max<VNT>(m, redf);
+  const double sc = (se > 0.0 && is_finite(mb)) ? se * exp((double)m - (double)mb) : 0.0;
+  const double sb = block_sum<VNT>(sc, redd);
+  if (t == 0) {
+    VPart* pp = parts + (size_t)row * G + g;
+    st_dev(&pp->amkey, am);
+    st_dev(&pp->mf, mb);
+    st_dev(&pp->se, sb);
+  }
+  VS_TR(A, 2);
+  if (block_arrive(&rowdone[row], &flag) != (uint32_t)(G - 1)) return;
+  VS_TR(A, 3);
+  // last workgroup of this row: merge the G partials in one wave (G <= 64)
+  if (t < WAVE) {
+    u64 k = 0;
+    float mm = -__builtin_inff();
+    double e = 0.0;
+    if (t < G) {
+      const VPart* pp = parts + (size_t)row * G + t;
+      k = ld_dev(&pp->amkey);
+      mm = ld_dev(&pp->mf);
+      e = ld_dev(&pp->se);
+    }
+    const u64 bam = wave_max(k);
+    const float M = wave_max(mm);
+    const double S = wave_sum((e > 0.0 && is_finite(M)) ? e * exp((double)mm - (double)M) : 0.0);
+    const int req = row / A.T;
+    uint32_t last = 0;
+    if (t == 0) {
+      const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
+      st_dev(&A.out_argmax[row], (int32_t)key_index(bam));
+      if (A.out_lp) A.out_lp[row] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
+      st_dev(&rowdone[row], 0u);
+      publish_wait();
+      last = ctr_add(&reqdone[req], 1u) == (uint32_t)(A.T - 1);
+    }
+    // last row of the request: accept prefix (specdec.py:327), 64 positions per ballot
+    if (lane_bcast(last, 0)) {
+      int nacc = 0;
+      for (int base = 0; base < A.T - 1; base += WAVE) {
+        const int i = base + t;
+        bool stop = i >= A.T - 1;
+        if (!stop) stop = A.drafts[(size_t)req * (A.T - 1) + i] != ld_dev(&A.out_argmax[req * A.T + i]);
+        const unsigned long long mb2 = __ballot(stop);
+        if (mb2) {
+          nacc += __ffsll((long long)mb2) - 1;
+          break;
+        }
+        nacc += WAVE;
+      }
+      if (t == 0) {
+        A.out_accept[req] = nacc;
+        st_dev(&reqdone[req], 0u);
+      }
+    }
+  }
+}
+
+}  // namespace vs
+
+using namespace vs;
+
+extern "C" size_t vs_verify_workspace_bytes(int B, int T, int V) {
+  (void)V;
+  size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
+  return 8 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
+}
+
+extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t ld, int vocab_valid,
+                                const int32_t* drafts, int32_t* out_argmax, int32_t* out_accept, float* out_logprob,
+                                void* ws, size_t ws_bytes, vs_stream_t stream) {
+  if (B < 0 || T < 1) return fail(VS_EINVAL, "vs_verify_greedy: B < 0 or T < 1");
+  if (B == 0) return VS_OK;
+  if (V < 1 || vocab_valid < 1 || vocab_valid > V) return fail(VS_EINVAL, "vs_verify_greedy: need 1 <= vocab_valid <= V");
+  if (ld < V) return fail(VS_EINVAL, "vs_verify_greedy: ld < V");
+  if (dtype != VS_F32 && dtype != VS_BF16 && dtype != VS_F16) return fail(VS_EINVAL, "vs_verify_greedy: bad dtype");
+  if (!logits || !out_argmax || !out_accept || !ws || (T > 1 && !drafts))
+    return fail(VS_EINVAL, "vs_verify_greedy: null pointer argument");
+  if ((long long)B * T > VRMAX) return fail(VS_EINVAL, "vs_verify_greedy: B*T above 8192 rows");
+  if (ws_bytes < vs_verify_workspace_bytes(B, T, V)) return fail(VS_EWORKSPACE, "vs_verify_greedy: workspace too small");
+  const DevInfo* dv = dev_info();
+  if (!dv) return fail(VS_EHIP, "vs_verify_greedy: no HIP device");
+  const int VEC = dtype == VS_F32 ? 4 : 8;
+  const int unit = VNT * VEC;
+  const int R = B * T;
+  const int chmax = VNV_MAX * unit;
+  int gmin = (vocab_valid + chmax - 1) / chmax;
+  if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
+  int G = (2 * dv->cus + R - 1) / R;  // aim at >= 2 workgroups per CU in flight
+  if (G > VGMAX) G = VGMAX;
+  if (G < gmin) G = gmin;
+  int CH = (vocab_valid + G - 1) / G;
+  CH = (CH + unit - 1) / unit * unit;
+  G = (vocab_valid + CH - 1) / CH;
+  VerifyArgs a;
+  a.logits = logits;
+  a.ld = ld;
+  a.B = B;
+  a.T = T;
+  a.V = V;
+  a.vv = vocab_valid;
+  a.G = G;
+  a.CH = CH;
+  a.NV = CH / unit;
+  a.vec_ok = ((uintptr_t)logits % 16 == 0) && (ld % VEC == 0);
+  a.drafts = drafts;
+  a.out_argmax = out_argmax;
+  a.out_accept = out_accept;
+  a.out_lp = out_logprob;
+  a.ws = (char*)ws;
+  a.trace = g_trace;
+  const size_t grid = (size_t)R * G;
+  if (grid > 0x7FFFFFFF) return fail(VS_EINVAL, "vs_verify_greedy: grid too large");
+  if (dtype == VS_F32)
+    hipLaunchKernelGGL(vs_verify_kernel<VS_F32>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
+  else if (dtype == VS_BF16)
+    hipLaunchKernelGGL(vs_verify_kernel<VS_BF16>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(vs_verify_kernel<VS_F16>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "vs_verify_greedy: launch");
+  return VS_OK;
+}

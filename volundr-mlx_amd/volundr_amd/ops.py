@@ -1,0 +1,309 @@
+"""Batched device entry points over torch tensors: sample_batch (Sampler.sample for B rows) and verify_greedy.
+
+Torch is the plumbing (device memory, the current stream); the arithmetic is in libvolundr_sampling.so, called
+through its C ABI with raw device pointers. No CPU fallback exists: a missing library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import math
+import threading
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import ROW_DTYPE, VS_BF16, VS_F16, VS_F32, VS_ROW_GREEDY, check
+
+_DTYPES = {torch.float32: VS_F32, torch.bfloat16: VS_BF16, torch.float16: VS_F16}
+_ws_lock = threading.Lock()
+_ws: dict = {}
+
+
+def _stream_handle(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def workspace(dev: torch.device, nbytes: int, kind: str = "sample") -> torch.Tensor:
+    """A zeroed workspace of >= nbytes for (device, current stream, kind); grown and re-zeroed on demand. The
+    sampling and verify kernels keep different layouts, so each has its own."""
+    key = (dev.index, _stream_handle(dev), kind)
+    with _ws_lock:
+        w = _ws.get(key)
+        if w is None or w.numel() < nbytes:
+            w = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            check(_lib.load().vs_workspace_init(w.data_ptr(), w.numel(), key[1]), "vs_workspace_init")
+            _ws[key] = w
+        return w
+
+
+def reset_workspace(dev: torch.device, kind: str = "sample"):
+    """Re-zero a workspace of (device, current stream), e.g. after a row reported VS_OUT_TIMEOUT."""
+    key = (dev.index, _stream_handle(dev), kind)
+    with _ws_lock:
+        w = _ws.get(key)
+        if w is not None:
+            check(_lib.load().vs_workspace_init(w.data_ptr(), w.numel(), key[1]), "vs_workspace_init")
+
+
+def _require_cuda(t: torch.Tensor, name: str):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the token-selection path runs only on the HIP device)")
+
+
+def _wrap_id(t: int, V: int) -> Optional[int]:
+    """NumPy indexing of a [V] row by a single id that passed the reference's `t < V` test (negative ids index from
+    the end; below -V NumPy raises)."""
+    t = int(t)
+    if t >= V:
+        return None
+    if t < 0:
+        if t < -V:
+            raise IndexError(f"index {t} is out of bounds for axis 0 with size {V}")
+        t += V
+    return t
+
+
+@dataclass
+class PackedRows:
+    """Host-packed per-row inputs of vs_sample_batch (numpy), see pack_rows."""
+    params: np.ndarray      # ROW_DTYPE [B]
+    hist: np.ndarray        # int32
+    bias_ids: np.ndarray    # int32
+    bias_vals: np.ndarray   # float32
+    mask_ids: np.ndarray    # int32
+
+    def to(self, dev) -> "DeviceRows":
+        def up(a):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(dev) if a.size else None
+        return DeviceRows(torch.from_numpy(self.params.view(np.uint8).copy()).to(dev), up(self.hist),
+                          up(self.bias_ids), up(self.bias_vals), up(self.mask_ids), len(self.params))
+
+
+@dataclass
+class DeviceRows:
+    params: torch.Tensor
+    hist: Optional[torch.Tensor]
+    bias_ids: Optional[torch.Tensor]
+    bias_vals: Optional[torch.Tensor]
+    mask_ids: Optional[torch.Tensor]
+    B: int
+
+
+def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, extras=None) -> PackedRows:
+    """Pack the per-row parameters the way Sampler.sample reads them (volundr-mlx/sampler.py:100-156).
+
+    samplings : Sampling-like objects (session.Sampling); u : B uniform draws in [0, 1)
+    histories : per-row token histories (iterables of ints: the tokens Sampler.accept recorded) or None
+    produced  : per-row Sampler.produced (the min_new_tokens stop mask, sampler.py:123), default 0
+    extras    : per-row budget biases [(id, bias)] applied before logit_bias (sampler.py:104-106)
+    """
+    B = len(samplings)
+    P = np.zeros(B, dtype=ROW_DTYPE)
+    u = np.asarray(u, dtype=np.float64).reshape(-1)
+    if u.size != B:
+        raise ValueError("one uniform draw per row is required")
+    hist_parts, bias_i, bias_v, mask = [], [], [], []
+    hpos = bpos = mpos = 0
+    for r, sp in enumerate(samplings):
+        p = P[r]
+        p["temperature"] = np.float32(sp.temperature)
+        p["repetition_penalty"] = np.float32(sp.repetition_penalty)
+        p["frequency_penalty"] = np.float32(sp.frequency_penalty)
+        p["presence_penalty"] = np.float32(sp.presence_penalty)
+        k = sp.top_k if sp.top_k else 0          # sampler.py:133: None and 0 mean off
+        if k < 0:
+            k = 1                                # max(min(k, n), 1) == 1 for k < 0 (:134)
+        p["top_k"] = min(int(k), 2**31 - 1)
+        p["flags"] = VS_ROW_GREEDY if sp.greedy else 0
+        p["top_p"] = float(sp.top_p)
+        p["min_p"] = float(sp.min_p)
+        p["u"] = float(u[r])
+        h = np.asarray([] if histories is None or histories[r] is None else histories[r], dtype=np.int64).reshape(-1)
+        if h.size and (h.min() < 0 or h.max() >= 2**31):
+            raise ValueError("token histories must hold ids in [0, 2^31)")
+        p["hist_begin"], p["hist_end"] = hpos, hpos + h.size
+        hist_parts.append(h.astype(np.int32))
+        hpos += h.size
+        # additive biases in application order: budget extra, then logit_bias (sampler.py:104-109)
+        items = []
+        for t, d in list(extras[r] if extras is not None and extras[r] else []) + list(sp.logit_bias):
+            w = _wrap_id(t, V)
+            if w is not None:
+                items.append((w, np.float32(d)))
+        if items:
+            ids = np.asarray([i for i, _ in items], dtype=np.int32)
+            vals = np.asarray([v for _, v in items], dtype=np.float32)
+            o = np.argsort(ids, kind="stable")
+            bias_i.append(ids[o])
+            bias_v.append(vals[o])
+        p["bias_begin"], p["bias_end"] = bpos, bpos + len(items)
+        bpos += len(items)
+        sup = sorted({w for w in (_wrap_id(t, V) for t in sp.suppress_tokens) if w is not None})
+        p["supp_begin"], p["supp_end"] = mpos, mpos + len(sup)
+        mask.append(np.asarray(sup, dtype=np.int32))
+        mpos += len(sup)
+        pr = 0 if produced is None else int(produced[r])
+        st = []
+        if pr < sp.min_new_tokens and sp.stop_token_ids:
+            st = sorted({w for w in (_wrap_id(t, V) for t in sp.stop_token_ids) if w is not None})
+        p["stop_begin"], p["stop_end"] = mpos, mpos + len(st)
+        mask.append(np.asarray(st, dtype=np.int32))
+        mpos += len(st)
+    cat = lambda xs, dt: np.concatenate(xs).astype(dt) if xs else np.zeros(0, dt)  # noqa: E731
+    return PackedRows(P, cat(hist_parts, np.int32), cat(bias_i, np.int32), cat(bias_v, np.float32),
+                      cat(mask, np.int32))
+
+
+@dataclass
+class SampleOut:
+    ids: torch.Tensor       # int32 [B]
+    logprobs: torch.Tensor  # float32 [B]
+    flags: torch.Tensor     # int32 view of the uint32 VS_OUT_* bits [B]
+    keep: torch.Tensor      # int32 [B]
+
+
+def alloc_out(B: int, dev) -> SampleOut:
+    z = lambda dt: torch.empty(B, dtype=dt, device=dev)  # noqa: E731
+    return SampleOut(z(torch.int32), z(torch.float32), z(torch.int32), z(torch.int32))
+
+
+def sample_rows(logits: torch.Tensor, rows: DeviceRows, out: Optional[SampleOut] = None) -> SampleOut:
+    """vs_sample_batch on device-resident inputs (no host work besides the launch)."""
+    _require_cuda(logits, "logits")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit stride along V")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    B, V = logits.shape
+    if B != rows.B:
+        raise ValueError("params and logits disagree on B")
+    dev = logits.device
+    out = out if out is not None else alloc_out(B, dev)
+    L = _lib.load()
+    nbytes = L.vs_sample_workspace_bytes(B, V)
+    ws = workspace(dev, nbytes)
+    ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+    rc = L.vs_sample_batch(logits.data_ptr(), _DTYPES[logits.dtype], B, V, logits.stride(0), rows.params.data_ptr(),
+                           ptr(rows.hist), ptr(rows.bias_ids), ptr(rows.bias_vals), ptr(rows.mask_ids),
+                           out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(), out.keep.data_ptr(),
+                           ws.data_ptr(), ws.numel(), _stream_handle(dev))
+    check(rc, "vs_sample_batch")
+    return out
+
+
+def sample_batch(logits: torch.Tensor, samplings: Sequence, u, histories=None, produced=None,
+                 extras=None) -> SampleOut:
+    """Sampler.sample (sampler.py:100-156) for every row of logits [B, V], with the uniform draws supplied."""
+    _require_cuda(logits, "logits")
+    rows = pack_rows(samplings, u, logits.shape[-1], histories, produced, extras).to(logits.device)
+    return sample_rows(logits, rows)
+
+
+@dataclass
+class VerifyOut:
+    argmax: torch.Tensor   # int32 [B, T]
+    accept: torch.Tensor   # int32 [B]
+    logprobs: torch.Tensor  # float32 [B, T]
+
+
+def verify_greedy(logits: torch.Tensor, drafts: Optional[torch.Tensor], vocab_valid: Optional[int] = None,
+                  out: Optional[VerifyOut] = None) -> VerifyOut:
+    """Greedy verify (spec/specdec.py:326-327, scheduler.py:462-463): logits [B, T, V] (or [T, V]), drafts
+    [B, T-1] int32 = inp[:, 1:] -> first-max argmax over [:vocab_valid], accept length, chosen-token logprob."""
+    _require_cuda(logits, "logits")
+    if logits.dim() == 2:
+        logits = logits.unsqueeze(0)
+    if logits.dim() != 3 or logits.stride(2) != 1 or logits.stride(0) != logits.shape[1] * logits.stride(1):
+        raise ValueError("logits must be [B, T, V] with rows evenly strided")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    B, T, V = logits.shape
+    vv = V if vocab_valid is None else int(vocab_valid)
+    dev = logits.device
+    if T > 1:
+        if drafts is None:
+            raise ValueError("drafts [B, T-1] are required when T > 1")
+        _require_cuda(drafts, "drafts")
+        drafts = drafts.reshape(B, T - 1).to(torch.int32).contiguous()
+    if out is None:
+        out = VerifyOut(torch.empty(B, T, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int32, device=dev),
+                        torch.empty(B, T, dtype=torch.float32, device=dev))
+    L = _lib.load()
+    nbytes = L.vs_verify_workspace_bytes(B, T, V)
+    ws = workspace(dev, nbytes, "verify")
+    rc = L.vs_verify_greedy(logits.data_ptr(), _DTYPES[logits.dtype], B, T, V, logits.stride(1), vv,
+                            drafts.data_ptr() if T > 1 else 0, out.argmax.data_ptr(), out.accept.data_ptr(),
+                            out.logprobs.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(dev))
+    check(rc, "vs_verify_greedy")
+    return out
+
+
+def emitted(drafts_row, argmax_row, nacc: int):
+    """Tokens one verify step emits for a request (specdec.py:335-336): accepted drafts + the bonus token."""
+    return [int(t) for t in drafts_row[:nacc]] + [int(argmax_row[nacc])]
+
+
+def fix_scale(V: int) -> float:
+    """Fixed-point scale of the probability masses used by the cooperative select (mirrors the library)."""
+    return math.ldexp(1.0, 63 - max(0, (V - 1).bit_length()))
+
+
+class PreparedSample:
+    """vs_sample_batch with every argument bound once (device-resident logits slots, params, outputs, workspace),
+    for serving loops that call the same batch shape every step: __call__(i) launches on logits slot i with no
+    host work besides the C call."""
+
+    def __init__(self, logits_slots: Sequence[torch.Tensor], rows: DeviceRows, out: Optional[SampleOut] = None):
+        x0 = logits_slots[0]
+        _require_cuda(x0, "logits")
+        B, V = x0.shape
+        self.dev = x0.device
+        self.out = out if out is not None else alloc_out(B, self.dev)
+        L = _lib.load()
+        self._fn = L.vs_sample_batch
+        ws = workspace(self.dev, L.vs_sample_workspace_bytes(B, V))
+        self._ws = ws
+        ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+        self._slots = [x.data_ptr() for x in logits_slots]
+        self._keep = (list(logits_slots), rows, self.out)
+        self._rest = (_DTYPES[x0.dtype], B, V, x0.stride(0), rows.params.data_ptr(), ptr(rows.hist),
+                      ptr(rows.bias_ids), ptr(rows.bias_vals), ptr(rows.mask_ids), self.out.ids.data_ptr(),
+                      self.out.logprobs.data_ptr(), self.out.flags.data_ptr(), self.out.keep.data_ptr(),
+                      ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
+
+    def __call__(self, slot: int = 0) -> SampleOut:
+        rc = self._fn(self._slots[slot], *self._rest)
+        if rc:
+            check(rc, "vs_sample_batch")
+        return self.out
+
+
+class PreparedVerify:
+    """vs_verify_greedy with every argument bound once (see PreparedSample)."""
+
+    def __init__(self, logits_slots: Sequence[torch.Tensor], drafts: torch.Tensor, vocab_valid: Optional[int] = None):
+        x0 = logits_slots[0]
+        _require_cuda(x0, "logits")
+        B, T, V = x0.shape
+        self.dev = x0.device
+        vv = V if vocab_valid is None else int(vocab_valid)
+        drafts = drafts.reshape(B, T - 1).to(torch.int32).contiguous()
+        self.out = VerifyOut(torch.empty(B, T, dtype=torch.int32, device=self.dev),
+                             torch.empty(B, dtype=torch.int32, device=self.dev),
+                             torch.empty(B, T, dtype=torch.float32, device=self.dev))
+        L = _lib.load()
+        self._fn = L.vs_verify_greedy
+        ws = workspace(self.dev, L.vs_verify_workspace_bytes(B, T, V), "verify")
+        self._slots = [x.data_ptr() for x in logits_slots]
+        self._keep = (list(logits_slots), drafts, ws)
+        self._rest = (_DTYPES[x0.dtype], B, T, V, x0.stride(1), vv, drafts.data_ptr(), self.out.argmax.data_ptr(),
+                      self.out.accept.data_ptr(), self.out.logprobs.data_ptr(), ws.data_ptr(), ws.numel(),
+                      _stream_handle(self.dev))
+
+    def __call__(self, slot: int = 0) -> VerifyOut:
+        rc = self._fn(self._slots[slot], *self._rest)
+        if rc:
+            check(rc, "vs_verify_greedy")
+        return self.out
