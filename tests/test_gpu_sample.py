@@ -66,6 +66,36 @@ def test_coop_path_near_flat(dev):
     assert all(f & OUT_COOP for f in fl)
 
 
+@pytest.mark.parametrize("sigma,top_p", [(2.0, 0.9), (4.0, 1.0), (1.0, 0.5), (6.0, 0.99)])
+def test_binned_path_medium_sets(dev, sigma, top_p):
+    # kept sets of a few hundred to a few thousand tokens: the two-level value-bin path
+    rng = np.random.default_rng(int(sigma * 10) + int(top_p * 100))
+    B, V = 4, 60000
+    x = (rng.standard_normal((B, V)) * sigma).astype(np.float32)
+    ps = [Sampling(top_p=top_p, temperature=float(tt)) for tt in (0.7, 1.0, 1.3, 2.0)]
+    out, refs, _ = run(dev, x, ps, rng.random(B), label=f"binned s{sigma} p{top_p}")
+    assert all(f & OUT_COOP for f in out.flags.cpu().numpy() if not f & OUT_GATHER)
+
+
+def test_binned_path_many_draws(dev):
+    # one row, many draws: exercises the speculative draw-bin ranges across the CDF
+    rng = np.random.default_rng(21)
+    V = 80000
+    x = (rng.standard_normal((1, V)) * 0.3).astype(np.float32)
+    xs = np.repeat(x, 16, axis=0)
+    ps = [Sampling(top_p=0.9)] * 16
+    run(dev, xs, ps, np.linspace(0.0, 0.999999, 16), label="binned draws")
+
+
+def test_ties_fall_back_to_radix(dev):
+    # bf16 near-flat logits: a few hundred distinct values for 100k tokens, so value bins hold long runs of ties
+    rng = np.random.default_rng(22)
+    B, V = 3, 100000
+    x = (rng.standard_normal((B, V)) * 0.05).astype(np.float32)
+    ps = [Sampling(top_p=0.95), Sampling(top_p=1.0), Sampling(top_p=0.3, temperature=0.5)]
+    run(dev, x, ps, rng.random(B), dtype=torch.bfloat16, label="bf16 ties")
+
+
 def test_gather_path(dev):
     rng = np.random.default_rng(12)
     B, V = 3, 20000

@@ -25,12 +25,17 @@ namespace vs {
 
 constexpr int SNT = 512;         // threads per workgroup
 constexpr int SNW = SNT / WAVE;  // waves per workgroup
-constexpr int EPT_MAX = 24;      // logits per lane kept in VGPRs
+constexpr int NRED = 16;         // entries of each LDS reduction/broadcast array (>= SNW and >= 6)
+constexpr int NMISC = 192;       // LDS scalar slots
+constexpr int EPT_MAX = 24;      // logits per lane in flight during the load
 constexpr int NBIN = 256;        // radix digit = 8 bits
-constexpr int MAX_ROUNDS = 24;   // histogram slots per row (8 count rounds + 1 + 7 + 7 mass rounds)
+constexpr int MAX_ROUNDS = 32;   // histogram slots per row (8 count + 1 coarse + 4 fine + 1 + 7 + 7 radix rounds)
 constexpr int GMAX = 64;         // workgroups per row
-constexpr int GCAP = 1024;       // gather capacity of the FULL path
-constexpr int SORT_MAX = 1024;   // largest in-workgroup sort
+constexpr int GCAP = 1024;       // gather area of the FULL path (keys)
+constexpr int GSMALL = 128;      // kept sets up to this size are finished in one workgroup
+constexpr int GCAP2 = 512;       // elements gathered from the located value bins
+constexpr int NSET = 4;          // coarse value bins refined in the second histogram round
+constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 4096;   // LDS key area (32 KB)
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
 constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
@@ -49,7 +54,9 @@ struct RowCtl {
   u64 mfix;         // min-p kept fixed-point mass
   double mf64;      // min-p kept float64 mass
   uint32_t err;     // a workgroup of the row timed out
-  uint32_t pad[3];
+  uint32_t nminkey; // ~ord32 of the smallest finite logit (max-reduced)
+  uint32_t g2count; // second gather reservations
+  uint32_t pad;
 };
 static_assert(sizeof(RowCtl) == 64, "RowCtl layout");
 
@@ -104,14 +111,13 @@ struct SampleArgs {
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
-// LDS layout (dynamic): [R0: max(CH*4 + GCAP*8, KEYS_CAP*8)] [tk: SNT u64] [hist] [scratch]
-// R0 holds, in turn: the penalty counts (cnt, CH u32); then either the TOPK/merge keys (keys, <= KEYS_CAP u64) or,
-// for FULL rows, the processed chunk (xv, CH floats) followed by the gather keys (fkeys, <= GCAP u64).
+// LDS layout (dynamic): [xv: CH floats] [keys: max(KEYS_CAP u64, CH u32), the penalty counts during the edits]
+// [tk: 2*KCAP u64] [hist] [scratch] [fine bins]. Every class reads its chunk from xv; keys holds candidate lists.
 struct Smem {
-  uint32_t* cnt;  // penalty counts
-  float* xv;      // FULL rows: the processed chunk
-  u64* fkeys;     // FULL rows: gathered keys
-  u64* keys;
+  uint32_t* cnt;  // penalty counts (during the edits)
+  float* xv;      // the processed chunk
+  u64* fkeys;     // gathered keys (= keys)
+  u64* keys;      // candidate lists
   u64* tk;
   uint32_t* hc;
   u64* hfix;
@@ -120,23 +126,27 @@ struct Smem {
   u64* red64;
   double* redf;
   int* redi;
-  int* misc;
+  int* misc;     // NMISC ints
+  uint32_t* fc;  // NSET*256 fine-bin counts
+  u64* ffix;     // NSET*256 fine-bin fixed-point masses
+  double* ff64;  // NSET*256 fine-bin float64 masses
 };
 
 __host__ __device__ inline size_t xv_bytes(int CH) { return ((size_t)CH * 4 + 15) & ~(size_t)15; }
-__host__ __device__ inline size_t region0(int CH) {
-  const size_t a = xv_bytes(CH) + (size_t)GCAP * 8, b = (size_t)KEYS_CAP * 8;
+__host__ __device__ inline size_t keys_bytes(int CH) {
+  const size_t a = (size_t)KEYS_CAP * 8, b = xv_bytes(CH);
   return a > b ? a : b;
 }
+__host__ __device__ inline size_t region0(int CH) { return xv_bytes(CH) + keys_bytes(CH); }
 __device__ __forceinline__ Smem carve(char* base, int CH) {
   Smem s;
-  s.cnt = (uint32_t*)base;
   s.xv = (float*)base;
-  s.fkeys = (u64*)(base + xv_bytes(CH));
-  s.keys = (u64*)base;
+  s.keys = (u64*)(base + xv_bytes(CH));
+  s.fkeys = s.keys;
+  s.cnt = (uint32_t*)s.keys;  // the penalty counts use the key area before any class needs it
   char* p = base + region0(CH);
   s.tk = (u64*)p;
-  p += SNT * 8;
+  p += 2 * KCAP * 8;
   s.hfix = (u64*)p;
   p += NBIN * 8;
   s.hf64 = (double*)p;
@@ -146,15 +156,23 @@ __device__ __forceinline__ Smem carve(char* base, int CH) {
   s.hc = (uint32_t*)p;
   p += NBIN * 4;
   s.red64 = (u64*)p;
-  p += SNW * 8;
+  p += NRED * 8;
   s.redf = (double*)p;
-  p += SNW * 8;
+  p += NRED * 8;
   s.redi = (int*)p;
-  p += SNW * 4;
+  p += NRED * 4;
   s.misc = (int*)p;
+  p += NMISC * 4;
+  s.ffix = (u64*)p;
+  p += NSET * NBIN * 8;
+  s.ff64 = (double*)p;
+  p += NSET * NBIN * 8;
+  s.fc = (uint32_t*)p;
   return s;
 }
-static size_t smem_bytes(int CH) { return region0(CH) + SNT * 8 + NBIN * (8 + 8 + 8 + 4) + SNW * (8 + 8 + 4) + 64 * 4; }
+static size_t smem_bytes(int CH) {
+  return region0(CH) + 2 * KCAP * 8 + NBIN * (8 + 8 + 8 + 4) + NRED * (8 + 8 + 4) + NMISC * 4 + NSET * NBIN * (8 + 8 + 4);
+}
 
 // ---------------------------------------------------------------------------------------------------------------
 // Histogram scan. One wave walks the 256 bins: lane L owns digits 255-4L .. 252-4L (descending key order), so the
@@ -172,7 +190,8 @@ struct ScanOut {
   u64 mk;
 };
 
-__device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, double target) {
+__device__ __forceinline__ ScanOut scan256(const Smem& s, const uint32_t* hc, const u64* hfix, const double* hf64,
+                                           const u64* hmk, bool count_mode, double target) {
   if (threadIdx.x < WAVE) {
     const int L = threadIdx.x;
     u64 c[4], w[4];
@@ -182,9 +201,9 @@ __device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, dou
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d = NBIN - 1 - (4 * L + i);
-      c[i] = s.hc[d];
-      w[i] = count_mode ? c[i] : s.hfix[d];
-      f[i] = s.hf64[d];
+      c[i] = hc[d];
+      w[i] = count_mode ? c[i] : hfix[d];
+      f[i] = hf64[d];
       lc += c[i];
       lw += w[i];
       lf += f[i];
@@ -239,10 +258,10 @@ __device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, dou
       s.red64[0] = hc2;
       s.red64[1] = hw;
       s.redf[0] = hf;
-      s.red64[2] = s.hc[d];
-      s.red64[3] = s.hfix[d];
-      s.redf[1] = s.hf64[d];
-      s.red64[4] = s.hmk[d];
+      s.red64[2] = hc[d];
+      s.red64[3] = hfix[d];
+      s.redf[1] = hf64[d];
+      s.red64[4] = hmk ? hmk[d] : 0;
     }
   }
   __syncthreads();
@@ -257,6 +276,10 @@ __device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, dou
   o.mk = s.red64[4];
   __syncthreads();
   return o;
+}
+
+__device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, double target) {
+  return scan256(s, s.hc, s.hfix, s.hf64, s.hmk, count_mode, target);
 }
 
 __device__ __forceinline__ void hist_clear(const Smem& s) {
@@ -305,58 +328,6 @@ __device__ __forceinline__ u64 block_kth(const Smem& s, const u64* keys, int n, 
   }
 }
 
-// Bitonic compare-exchange of the element at position i with its partner i^j in stage (k, j), descending overall.
-__device__ __forceinline__ u64 bitonic_keep(u64 mine, u64 other, int i, int j, int k) {
-  const bool desc = (i & k) == 0;
-  const bool lower = (i & j) == 0;
-  const u64 mx = mine > other ? mine : other, mn = mine > other ? other : mine;
-  return (desc == lower) ? mx : mn;
-}
-
-// Sort a[0..n) descending (n <= SORT_MAX) in place, zero-padded to a power of two >= 64. Thread t holds positions t
-// and t+512 in registers; partners within a wave are exchanged with cross-lane moves, partners in other waves
-// through LDS, so most of the network needs no barrier. `a` must have room for the padded length (and >= SNT).
-__device__ __forceinline__ void block_sort_desc(u64* a, int n) {
-  int P = 64;
-  while (P < n) P <<= 1;
-  const int t = threadIdx.x;
-  __syncthreads();
-  u64 e0 = t < n ? a[t] : 0;
-  u64 e1 = (P > SNT && t + SNT < n) ? a[t + SNT] : 0;
-  for (int k = 2; k <= P; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j >= SNT) {
-        const bool desc = (t & k) == 0;
-        const u64 mx = e0 > e1 ? e0 : e1, mn = e0 > e1 ? e1 : e0;
-        e0 = desc ? mx : mn;
-        e1 = desc ? mn : mx;
-      } else if (j >= WAVE) {
-        __syncthreads();
-        a[t] = e0;
-        if (P > SNT) a[t + SNT] = e1;
-        __syncthreads();
-        const u64 p0 = a[t ^ j];
-        e0 = bitonic_keep(e0, p0, t, j, k);
-        if (P > SNT) {
-          const u64 p1 = a[(t + SNT) ^ j];
-          e1 = bitonic_keep(e1, p1, t + SNT, j, k);
-        }
-      } else {
-        const u64 p0 = lane_xor_rt(e0, j);
-        e0 = bitonic_keep(e0, p0, t, j, k);
-        if (P > SNT) {
-          const u64 p1 = lane_xor_rt(e1, j);
-          e1 = bitonic_keep(e1, p1, t + SNT, j, k);
-        }
-      }
-    }
-  }
-  __syncthreads();
-  if (t < P) a[t] = e0;
-  if (P > SNT && t + SNT < P) a[t + SNT] = e1;
-  __syncthreads();
-}
-
 struct Final {
   int32_t token;
   float lp;
@@ -364,11 +335,11 @@ struct Final {
   int32_t keep;
 };
 
-// sampler.py:141-156 on n <= SORT_MAX keys sorted descending in LDS (a[0] is the row maximum), in one wave: lane L
+// sampler.py:141-156 on n <= 256 keys sorted descending in LDS (a[0] is the row maximum), in one wave: lane L
 // owns positions [L*E, L*E+E), so every sum and prefix is a lane-sequential loop plus one wave scan. The result is
 // broadcast to the whole workgroup.
 __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n, const vs_row_params& P) {
-  constexpr int EM = SORT_MAX / WAVE;
+  constexpr int EM = 4;  // n <= 256
   if (threadIdx.x < WAVE) {
     const int L = threadIdx.x;
     const int E = (n + WAVE - 1) / WAVE;
@@ -488,6 +459,51 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
   f.lp = (float)s.redf[0];
   __syncthreads();
   return f;
+}
+
+// Rank by counting (unique keys): out[r] = the key of rank r (0 = largest) for r < kout. O(n) per element; used
+// only for small n, where it is cheaper on one CU than a sorting network. `in` and `out` must not overlap.
+__device__ __forceinline__ void block_rank_sort(const u64* in, int n, u64* out, int kout) {
+  for (int i = threadIdx.x; i < n; i += SNT) {
+    const u64 ki = in[i];
+    int r = 0, j = 0;
+    for (; j + 4 <= n; j += 4) r += (in[j] > ki) + (in[j + 1] > ki) + (in[j + 2] > ki) + (in[j + 3] > ki);
+    for (; j < n; ++j) r += in[j] > ki;
+    if (r < kout) out[r] = ki;
+  }
+  __syncthreads();
+}
+
+// Lower bound L for the k-th largest key of the workgroup, from the lane maxima: each wave extracts its q = ceil(k/8)
+// largest lane maxima (q wave-wide max reductions); every extracted key is >= the smallest wave's q-th value, and
+// there are >= k of them when the waves together extracted k. Returns 1 (no bound) otherwise.
+__device__ __forceinline__ u64 lane_max_bound(u64 tmax, int k, const Smem& s) {
+  const int q = (k + SNW - 1) / SNW;
+  u64 cur = tmax, wb = 0;
+  int got = 0;
+  for (int i = 0; i < q; ++i) {
+    const u64 m = wave_max(cur);
+    if (m == 0) break;
+    wb = m;
+    ++got;
+    if (cur == m) cur = 0;
+  }
+  const int w = threadIdx.x / WAVE;
+  __syncthreads();
+  if (lane_id() == 0) {
+    s.red64[w] = wb;
+    s.redi[w] = got;
+  }
+  __syncthreads();
+  u64 L = ~0ull;
+  int tot = 0;
+#pragma unroll
+  for (int i = 0; i < SNW; ++i) {
+    tot += s.redi[i];
+    if (s.redi[i] > 0) L = s.red64[i] < L ? s.red64[i] : L;
+  }
+  __syncthreads();
+  return tot >= k ? L : 1;
 }
 
 __device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Final& f) {
@@ -633,49 +649,62 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   }
   VS_TR(A, 1);
 
-  // ---- logit edits and penalties (sampler.py:104-126), float32 throughout ----
-  const bool has_bias = P.bias_end > P.bias_begin;
-  const bool has_supp = P.supp_end > P.supp_begin;
-  const bool has_stop = P.stop_end > P.stop_begin;
+  // ---- the chunk moves to LDS (xv): the edits and every class read it from there with compact loops, which keeps
+  // the code small enough for the instruction cache and frees the chunk's VGPRs ----
+  FOR_ELEMS({ s.xv[e - lo] = x; })
+  __syncthreads();
+
+  // ---- logit edits and penalties (sampler.py:104-126), float32 throughout, applied sparsely ----
   const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
   const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
-  if (has_pen) {
+  if (P.bias_end > P.bias_begin) {  // :104-109; ids sorted, equal ids in application order: one lane per run
+    for (int p = P.bias_begin + t; p < P.bias_end; p += SNT) {
+      const int id = A.bias_ids[p];
+      if (id >= lo && id < hi && (p == P.bias_begin || A.bias_ids[p - 1] != id)) {
+        float y = s.xv[id - lo];
+        for (int q = p; q < P.bias_end && A.bias_ids[q] == id; ++q) y = y + A.bias_vals[q];
+        s.xv[id - lo] = y;
+      }
+    }
+    __syncthreads();
+  }
+  if (P.supp_end > P.supp_begin) {  // :110-112
+    for (int p = P.supp_begin + t; p < P.supp_end; p += SNT) {
+      const int id = A.mask_ids[p];
+      if (id >= lo && id < hi) s.xv[id - lo] = -__builtin_inff();
+    }
+    __syncthreads();
+  }
+  if (has_pen) {  // :113-122 over the multiset of generated tokens
     for (int i = t; i < A.CH; i += SNT) s.cnt[i] = 0;
     __syncthreads();
     count_history(A.hist, P.hist_begin, P.hist_end, lo, hi, s.cnt);
     __syncthreads();
+    for (int i = t; i < hi - lo; i += SNT) {
+      const uint32_t c = s.cnt[i];
+      if (c) {
+        float y = s.xv[i];
+        if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
+        const float cf = (float)c;
+        const float fc = fpen * cf;
+        const float sub = fc + ppen;
+        s.xv[i] = y - sub;
+      }
+    }
+    __syncthreads();
   }
-  if (has_bias || has_supp || has_pen || has_stop) {
-    FOR_ELEMS({
-      if (has_bias) {  // sampler.py:104-109, equal ids applied in list order
-        int p = lower_bound_ids(A.bias_ids, P.bias_begin, P.bias_end, e);
-        while (p < P.bias_end && A.bias_ids[p] == e) {
-          x = x + A.bias_vals[p];
-          ++p;
-        }
-      }
-      if (has_supp) {  // :110-112
-        const int p = lower_bound_ids(A.mask_ids, P.supp_begin, P.supp_end, e);
-        if (p < P.supp_end && A.mask_ids[p] == e) x = -__builtin_inff();
-      }
-      if (has_pen) {  // :113-122
-        const uint32_t c = s.cnt[e - lo];
-        if (c) {
-          float y = x;
-          if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
-          const float cf = (float)c;
-          const float fc = fpen * cf;
-          const float sub = fc + ppen;
-          y = y - sub;
-          x = y;
-        }
-      }
-      if (has_stop) {  // :123-126
-        const int p = lower_bound_ids(A.mask_ids, P.stop_begin, P.stop_end, e);
-        if (p < P.stop_end && A.mask_ids[p] == e) x = -__builtin_inff();
-      }
-    })
-    __syncthreads();  // the count area is reused below
+  if (P.stop_end > P.stop_begin) {  // :123-126
+    for (int p = P.stop_begin + t; p < P.stop_end; p += SNT) {
+      const int id = A.mask_ids[p];
+      if (id >= lo && id < hi) s.xv[id - lo] = -__builtin_inff();
+    }
+    __syncthreads();
+  }
+#define FOR_XV(BODY)                          \
+  for (int i_ = t; i_ < hi - lo; i_ += SNT) { \
+    const int e = lo + i_;                    \
+    const float x = s.xv[i_];                 \
+    BODY                                      \
   }
   VS_TR(A, 2);
 
@@ -714,7 +743,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     // ---- sampler.py:127-128: np.argmax(x), first maximum; logprob = log-softmax of the processed row ----
     u64 am = 0;
     float mf = -__builtin_inff();
-    FOR_ELEMS({
+    FOR_XV({
       const u64 k = amkey64(x, (uint32_t)e);
       am = k > am ? k : am;
       if (is_finite(x)) mf = x > mf ? x : mf;
@@ -723,7 +752,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     mf = block_max<SNT>(mf, (float*)s.redf);
     double se = 0.0;
     if (is_finite(mf)) {
-      FOR_ELEMS({
+      FOR_XV({
         if (is_finite(x)) se += exp((double)x - (double)mf);
       })
     }
@@ -764,7 +793,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     const int k = top_k;
     u64 tmax = 0, am = 0;
     int nf = 0;
-    FOR_ELEMS({
+    FOR_XV({
       const u64 ka = amkey64(x, (uint32_t)e);
       am = ka > am ? ka : am;
       if (is_finite(x)) {
@@ -774,24 +803,16 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
     })
     const int nb_fin = block_sum<SNT>(nf, s.redi);
-    const int nz = block_sum<SNT>(tmax != 0 ? 1 : 0, s.redi);
     am = block_max<SNT>(am, s.red64);
     VS_TR(A, 10);
     int kc = 0;
     if (nb_fin > 0) {
-      // Lower bound L for the k-th largest key: the k-th largest lane maximum (the k lanes above it each hold a
-      // distinct key >= it). Only keys >= L can be in the local top-k.
-      u64 L = 1;
-      if (nb_fin > k && nz > k) {
-        s.tk[t] = tmax;
-        block_sort_desc(s.tk, SNT);
-        L = s.tk[k - 1];
-        __syncthreads();
-      }
+      // Only keys >= L can be in the local top-k; typically a small multiple of k survive.
+      const u64 L = nb_fin > k ? lane_max_bound(tmax, k, s) : (u64)1;
       VS_TR(A, 11);
       if (t == 0) s.misc[4] = 0;
       __syncthreads();
-      FOR_ELEMS({
+      FOR_XV({
         if (is_finite(x)) {
           const u64 kk = key64(x, (uint32_t)e);
           if (kk >= L) {
@@ -807,58 +828,65 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #ifdef VS_TRACE
       if (t == 0 && A.trace) A.trace[(size_t)blockIdx.x * 32 + 19] = C;
 #endif
-      if (C <= SORT_MAX) {
-        block_sort_desc(s.keys, C);
-        VS_TR(A, 13);
-        kc = C < k ? C : k;
-        if (t < kc) st_dev(&cand[g * A.kcap + t], s.keys[t]);
+      kc = C < k ? C : k;
+      if (C <= RANK_MAX) {
+        block_rank_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
       } else {
-        // Many keys above the bound (few lanes hold finite values): radix select over the VGPR-resident chunk.
-        u64 prefix = 0;
-        int shift = 56, krem = k;
-        u64 T = 0;
-        for (;;) {
-          hist_clear(s);
-          FOR_ELEMS({
-            if (is_finite(x)) {
-              const u64 kk = key64(x, (uint32_t)e);
-              if (prefix_match(kk, shift, prefix)) atomicAdd(&s.hc[(kk >> shift) & 0xFF], 1u);
+        // Many keys above the bound (few lanes hold finite values): radix select, then rank the k survivors.
+        u64 T;
+        if (C <= KEYS_CAP) {
+          T = block_kth(s, s.keys, C, k);
+        } else {
+          u64 prefix = 0;
+          int shift = 56, krem = k;
+          for (;;) {
+            hist_clear(s);
+            FOR_XV({
+              if (is_finite(x)) {
+                const u64 kk = key64(x, (uint32_t)e);
+                if (prefix_match(kk, shift, prefix)) atomicAdd(&s.hc[(kk >> shift) & 0xFF], 1u);
+              }
+            })
+            __syncthreads();
+            const ScanOut o = hist_scan(s, true, (double)krem);
+            const int need = krem - (int)o.cnt_before;
+            const u64 np = (prefix << 8) | (u64)o.digit;
+            if ((int)o.cnt == need || shift == 0) {
+              T = np << shift;
+              break;
             }
-          })
-          __syncthreads();
-          const ScanOut o = hist_scan(s, true, (double)krem);
-          const int need = krem - (int)o.cnt_before;
-          const u64 np = (prefix << 8) | (u64)o.digit;
-          if ((int)o.cnt == need || shift == 0) {
-            T = np << shift;
-            break;
+            krem = need;
+            prefix = np;
+            shift -= 8;
           }
-          krem = need;
-          prefix = np;
-          shift -= 8;
         }
         if (t == 0) s.misc[5] = 0;
         __syncthreads();
-        FOR_ELEMS({
+        u64* sel = s.tk + KCAP;  // k <= KCAP survivors
+        FOR_XV({
           if (is_finite(x)) {
             const u64 kk = key64(x, (uint32_t)e);
             if (kk >= T) {
               const int p = atomicAdd(&s.misc[5], 1);
-              if (p < A.kcap) st_dev(&cand[g * A.kcap + p], kk);
+              if (p < KCAP) sel[p] = kk;
             }
           }
         })
         __syncthreads();
-        kc = min(s.misc[5], A.kcap);
+        block_rank_sort(sel, kc, s.tk, kc);
       }
+      for (int i = t; i < kc; i += SNT) st_dev(&cand[g * A.kcap + i], s.tk[i]);
+      VS_TR(A, 13);
     }
     put_part(am, (uint32_t)nb_fin, (uint32_t)kc, 0.0f, 0.0);
     VS_TR(A, 3);
     VS_TRC(A, 31);
     if (arrive_done()) {
       VS_TR(A, 4);
-      // ---- merge: the last workgroup of the row (partials read by one wave, G <= 64) ----
-      int* offs = (int*)s.tk;  // [2*G]: candidate offset and count per workgroup (tk is free until the sort)
+      // ---- merge (last workgroup of the row). Each workgroup's list is its sorted local top-min(k, n_g). Any keff
+      // entries taken from the list heads bound the global keff-th key from below, so with r = ceil(keff / lists)
+      // heads per list, M = keff-th largest of those heads leaves only about keff survivors. ----
+      int* kcs = s.misc + 32;  // [G] list lengths (G <= 64)
       if (t < WAVE) {
         int c = 0, nf2 = 0;
         u64 k2 = 0;
@@ -866,25 +894,24 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           c = (int)ld_dev(&parts[t].kc);
           nf2 = (int)ld_dev(&parts[t].nfin);
           k2 = ld_dev(&parts[t].amkey);
+          kcs[t] = c;
         }
-        const int incl = wave_scan(c);
-        const int tot = wave_sum(c);
         const int nn = wave_sum(nf2);
         const u64 bam2 = wave_max(k2);
-        if (t < G) {
-          offs[2 * t] = incl - c;
-          offs[2 * t + 1] = c;
-        }
+        const int nl = wave_sum(c > 0 ? 1 : 0);
         if (t == 0) {
-          s.misc[6] = tot;
           s.misc[7] = nn;
+          s.misc[8] = nl;
           s.red64[0] = bam2;
+          s.misc[9] = 0;
         }
       }
       __syncthreads();
-      const int C = s.misc[6];
       const int n = s.misc[7];
+      const int nl = s.misc[8];
       const u64 bam = s.red64[0];
+      int keff = k < n ? k : n;  // sampler.py:133-134
+      if (keff < 1) keff = 1;
       __syncthreads();
       if (n == 0) {  // sampler.py:131-132
         Final f;
@@ -894,35 +921,71 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         f.keep = 0;
         write_out(A, row, f);
       } else {
-        for (int idx = t; idx < G * A.kcap; idx += SNT) {
+        const int tot = G * A.kcap;
+        for (int idx = t; idx < tot; idx += SNT) {  // all lists into LDS (one round trip), unused slots zero
           const int i = idx / A.kcap, q = idx - i * A.kcap;
-          if (q < offs[2 * i + 1]) s.keys[offs[2 * i] + q] = ld_dev(&cand[idx]);
+          s.keys[idx] = q < kcs[i] ? ld_dev(&cand[idx]) : (u64)0;
         }
         __syncthreads();
-        int keff = k < n ? k : n;  // sampler.py:133-134
-        if (keff < 1) keff = 1;
-        VS_TR(A, 5);
-        const u64* sorted;
-        if (C <= SORT_MAX) {
-          block_sort_desc(s.keys, C);  // sampler.py:140 on the candidates; the first keff are the top-k
-          sorted = s.keys;
-        } else {
-          const u64 T = block_kth(s, s.keys, C, keff);
-          if (t == 0) s.misc[9] = 0;
+        const int r = (keff + nl - 1) / nl;
+        // the first r entries of every list, packed into c0 (<= keff + 63 keys; tk is free until the survivors)
+        u64* c0 = s.tk;
+        int* offs = s.misc + 96;  // [G]
+        if (t < WAVE) {
+          const int lim = t < G ? (kcs[t] < r ? kcs[t] : r) : 0;
+          const int incl = wave_scan(lim);
+          if (t < G) offs[t] = incl - lim;
+          if (t == WAVE - 1) s.misc[10] = incl;
+        }
+        __syncthreads();
+        for (int idx = t; idx < G * r; idx += SNT) {
+          const int i = idx / r, q = idx - i * r;
+          if (q < kcs[i]) c0[offs[i] + q] = s.keys[i * A.kcap + q];
+        }
+        __syncthreads();
+        const int n0 = s.misc[10];
+        u64 M = 0;
+        if (n0 >= keff) {  // M = the keff-th largest of c0
+          for (int i = t; i < n0; i += SNT) {
+            const u64 ki = c0[i];
+            int rank = 0;
+            for (int j = 0; j < n0; ++j) rank += c0[j] > ki;
+            if (rank == keff - 1) s.red64[1] = ki;
+          }
           __syncthreads();
-          for (int i = t; i < C; i += SNT) {
+          M = s.red64[1];
+        }
+        __syncthreads();
+        u64* sel = s.tk + KCAP;
+        for (int idx = t; idx < tot; idx += SNT) {
+          const u64 kk = s.keys[idx];
+          if (kk != 0 && kk >= M) {
+            const int p = atomicAdd(&s.misc[9], 1);
+            if (p < KCAP) sel[p] = kk;
+          }
+        }
+        __syncthreads();
+        const int Cm = s.misc[9];
+        __syncthreads();
+        VS_TR(A, 5);
+        if (Cm <= KCAP) {
+          block_rank_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
+        } else {
+          const u64 T = block_kth(s, s.keys, tot, keff);
+          if (t == 0) s.misc[10] = 0;
+          __syncthreads();
+          for (int i = t; i < tot; i += SNT) {
             const u64 kk = s.keys[i];
             if (kk >= T) {
-              const int p = atomicAdd(&s.misc[9], 1);
-              if (p < SNT) s.tk[p] = kk;
+              const int p = atomicAdd(&s.misc[10], 1);
+              if (p < KCAP) sel[p] = kk;
             }
           }
           __syncthreads();
-          block_sort_desc(s.tk, keff);
-          sorted = s.tk;
+          block_rank_sort(sel, keff, s.tk, keff);
         }
         VS_TR(A, 6);
-        const Final f = wave_sample(s, sorted, keff, P);
+        const Final f = wave_sample(s, s.tk, keff, P);
         VS_TR(A, 7);
         write_out(A, row, f);
       }
@@ -932,20 +995,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   }
 
   // =================================== FULL class ===================================
-  // The chunk moves to LDS (xv): every later pass of this class reads it from there, so the 24 VGPRs of the
-  // chunk are free for the selection state.
-  FOR_ELEMS({ s.xv[e - lo] = x; })
-  __syncthreads();
-#define FOR_XV(BODY)                              \
-  for (int i_ = t; i_ < hi - lo; i_ += SNT) {     \
-    const int e = lo + i_;                        \
-    const float x = s.xv[i_];                     \
-    BODY                                          \
-  }
-  // ---- row statistics: finite count, largest finite logit, np.argmax key ----
+  // ---- row statistics: finite count, largest and smallest finite logit, np.argmax key ----
   {
     int nf = 0;
-    uint32_t mk = 0;
+    uint32_t mk = 0, nmk = 0;
     u64 am = 0;
     FOR_XV({
       const u64 ka = amkey64(x, (uint32_t)e);
@@ -954,14 +1007,19 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         ++nf;
         const uint32_t o = ord32(x);
         mk = o > mk ? o : mk;
+        nmk = ~o > nmk ? ~o : nmk;
       }
     })
     nf = block_sum<SNT>(nf, s.redi);
     mk = block_max<SNT>(mk, (uint32_t*)s.redi);
+    nmk = block_max<SNT>(nmk, (uint32_t*)s.redi);
     am = block_max<SNT>(am, s.red64);
     if (t == 0) {
-      if (nf) atomicAdd(&ctl->nfin, (uint32_t)nf);
-      if (mk) atomicMax(&ctl->mkey, mk);
+      if (nf) {
+        atomicAdd(&ctl->nfin, (uint32_t)nf);
+        atomicMax(&ctl->mkey, mk);
+        atomicMax(&ctl->nminkey, nmk);
+      }
       atomicMax(&ctl->amkey, am);
     }
   }
@@ -973,9 +1031,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   fin.lp = 0.0f;
   fin.flags = VS_OUT_TIMEOUT;
   fin.keep = 0;
+  bool g0_writes = true;  // false when the last workgroup of the row writes the result itself
   if (ok) {
     const int n = (int)ld_relaxed(&ctl->nfin);
     const uint32_t mkey = ld_relaxed(&ctl->mkey);
+    const uint32_t minkey = ~ld_relaxed(&ctl->nminkey);
     const u64 amk = ld_relaxed64(&ctl->amkey);
     if (n == 0) {  // sampler.py:131-132
       fin.token = (int32_t)key_index(amk);
@@ -984,11 +1044,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       int k = top_k > 0 ? (top_k < n ? top_k : n) : n;  // sampler.py:133-134
       if (k < 1) k = 1;
       const float tt = P.temperature;
-      const float xmax = inv_ord32(mkey);
-      const float xs0 = xmax / tt;  // xs[0]: the maximum always survives
-      int mode = 0;                 // 0 all finite, 1 key >= Tk, 2 exp(-40) filter
+      const float xs0 = inv_ord32(mkey) / tt;  // xs[0]: the maximum always survives
+      int mode = 0;                            // 0 all finite, 1 key >= Tk, 2 exp(-40) filter
       u64 Tk = 0;
       float thr = 0.0f;
+      float xs_lo = inv_ord32(minkey) / tt;  // smallest x/t of the kept set (a lower bound for mode 1)
       if (k < n) {
         // top-k with k beyond the TOPK class: cooperative count-weighted radix select (sampler.py:135-136)
         mode = 1;
@@ -1028,24 +1088,46 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           prefix = np;
           shift -= 8;
         }
+        xs_lo = key_value(Tk) / tt;
       } else if (n > 4096) {
         mode = 2;  // sampler.py:137-139: keep x/t >= m/t - 40 (float32)
         thr = xs0 - 40.0f;
+        xs_lo = xs_lo > thr ? xs_lo : thr;
       }
       if (ok) {
 #define IS_CAND(x, kk) (is_finite(x) && (mode == 0 || (mode == 1 ? (kk) >= Tk : ((x) / tt) >= thr)))
         const double scale = A.fix_scale;
+        // Value bins: u = xs0 - x/t >= 0 is monotone in the logit, so the fine index f = u * 65536 / span splits
+        // the kept set, in sampler.py:140 order, into contiguous ranges. Bins are stored by digit 255 - c (coarse
+        // c = f >> 8) and 255 - (f & 255) (fine), so that the 256-bin scan walks them in descending-logit order.
+        const float span = xs0 - xs_lo;
+        const float fscale = span > 0.0f ? 65536.0f / span : 0.0f;
+        auto fine_of = [&](float x) -> int {
+          const float u = xs0 - x / tt;
+          int f = (int)(u * fscale);
+          f = f < 0 ? 0 : (f > 65535 ? 65535 : f);
+          return 65535 - f;  // (coarse digit << 8) | fine digit
+        };
+        auto mass = [&](float x, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
+          const float d = x / tt - xs0;
+          const double pr = (double)expf(d);
+          *fx = (u64)(pr * scale + 0.5);
+          return pr;
+        };
         VS_TR(A, 4);
-        // ---- mass histogram of the kept set (top digit) + bounded gather ----
+        // ---- round 1: coarse mass histogram of the kept set + its size + a bounded gather ----
         hist_clear(s);
         int cb = 0;
         FOR_XV({
           const u64 kk = key64(x, (uint32_t)e);
           if (IS_CAND(x, kk)) {
             ++cb;
-            const float d = x / tt - xs0;
-            const double pr = exp((double)d);
-            hist_add(s, kk, 56, (u64)(pr * scale + 0.5), pr);
+            u64 fx;
+            const double pr = mass(x, &fx);
+            const int c = fine_of(x) >> 8;
+            atomicAdd(&s.hc[c], 1u);
+            atomicAdd(&s.hfix[c], fx);
+            unsafeAtomicAdd(&s.hf64[c], pr);
           }
         })
         cb = block_sum<SNT>(cb, s.redi);
@@ -1055,176 +1137,428 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         }
         __syncthreads();
         const int gbase = s.misc[9];
-        if (gbase + cb <= GCAP) {
+        if (gbase + cb <= GSMALL) {
           FOR_XV({
             const u64 kk = key64(x, (uint32_t)e);
             if (IS_CAND(x, kk)) st_dev(&gather[gbase + atomicAdd(&s.misc[10], 1)], kk);
           })
         }
-        const int s1 = slot++;
-        {
-          HistSlot* hs = hslots + s1;
-          if (t < NBIN && s.hc[t]) {
-            atomicAdd(&hs->cnt[t], s.hc[t]);
-            atomicAdd(&hs->fix[t], s.hfix[t]);
-            unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
-            atomicMax(&hs->mk[t], s.hmk[t]);
-          }
+        HistSlot* h1 = hslots + slot++;
+        if (t < NBIN && s.hc[t]) {
+          atomicAdd(&h1->cnt[t], s.hc[t]);
+          atomicAdd(&h1->fix[t], s.hfix[t]);
+          unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
         }
         ++nbar;
         ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
         if (ok) {
           const int total = (int)ld_relaxed(&ctl->gcount);
           VS_TR(A, 5);
-          if (total <= GCAP) {
-            // ---- small kept set: one workgroup finishes exactly as for TOPK ----
+          bool radix = false;
+          if (total <= GSMALL) {
+            // ---- small kept set: one workgroup ranks it and finishes as for TOPK ----
             if (g == 0) {
-              for (int i = t; i < total; i += SNT) s.fkeys[i] = ld_dev(&gather[i]);
+              for (int i = t; i < total; i += SNT) s.keys[i] = ld_dev(&gather[i]);
               __syncthreads();
-              block_sort_desc(s.fkeys, total);
-              fin = wave_sample(s, s.fkeys, total, P);
+              block_rank_sort(s.keys, total, s.tk, total);
+              fin = wave_sample(s, s.tk, total, P);
               fin.flags |= VS_OUT_GATHER;
             }
+          } else if (P.min_p > 0.0) {
+            radix = true;  // min-p on a large kept set: the radix path below handles it
           } else {
-            // ---- large kept set: cooperative mass-weighted radix select ----
-            HistSlot* h1 = hslots + s1;
-            auto load_slot = [&](HistSlot* hs) {
-              if (t < NBIN) {
-                s.hc[t] = ld_relaxed(&hs->cnt[t]);
-                s.hfix[t] = ld_relaxed64(&hs->fix[t]);
-                s.hf64[t] = ld_relaxed_f64(&hs->f64[t]);
-                s.hmk[t] = ld_relaxed64(&hs->mk[t]);
-              }
-              __syncthreads();
-            };
-            load_slot(h1);
+            // ---- large kept set: locate the top-p and draw positions by value bins ----
+            if (t < NBIN) {
+              s.hc[t] = ld_relaxed(&h1->cnt[t]);
+              s.hfix[t] = ld_relaxed64(&h1->fix[t]);
+              s.hf64[t] = ld_relaxed_f64(&h1->f64[t]);
+            }
+            __syncthreads();
             const u64 Sfix = block_sum<SNT>(t < NBIN ? s.hfix[t] : (u64)0, s.red64);
             const double Sf = block_sum<SNT>(t < NBIN ? s.hf64[t] : 0.0, s.redf);
-            // select: the first key (descending) whose inclusive cumulative mass reaches target
-            struct Sel {
-              u64 key, cnt_before, fix_before, fix;
-              double f64_before, f64;
-            };
-            auto select = [&](double target) -> Sel {
-              Sel r;
-              r.key = 0;
-              r.cnt_before = r.fix_before = r.fix = 0;
-              r.f64_before = r.f64 = 0.0;
-              load_slot(h1);
-              u64 prefix = 0;
-              int shift = 56;
-              for (;;) {
-                const ScanOut o = hist_scan(s, false, target - (double)r.fix_before);
-                r.cnt_before += o.cnt_before;
-                r.fix_before += o.fix_before;
-                r.f64_before += o.f64_before;
-                if (o.cnt <= 1 || shift == 0) {
-                  r.key = o.mk;
-                  r.fix = o.fix;
-                  r.f64 = o.f64;
-                  return r;
-                }
-                prefix = (prefix << 8) | (u64)o.digit;
-                shift -= 8;
-                // next digit: histogram of the candidates under this prefix
-                hist_clear(s);
-                FOR_XV({
-                  const u64 kk = key64(x, (uint32_t)e);
-                  if (IS_CAND(x, kk) && (kk >> (shift + 8)) == prefix) {
-                    const float d = x / tt - xs0;
-                    const double pr = exp((double)d);
-                    hist_add(s, kk, shift, (u64)(pr * scale + 0.5), pr);
-                  }
-                })
-                __syncthreads();
-                HistSlot* hs = hslots + slot;
-                ++slot;
-                if (t < NBIN && s.hc[t]) {
-                  atomicAdd(&hs->cnt[t], s.hc[t]);
-                  atomicAdd(&hs->fix[t], s.hfix[t]);
-                  unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
-                  atomicMax(&hs->mk[t], s.hmk[t]);
-                }
-                ++nbar;
-                ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
-                if (!ok) return r;
-                load_slot(hs);
-              }
-            };
-            int keep = total;
-            u64 zfix = Sfix;
-            double zf = Sf;
-            uint32_t flags = VS_OUT_COOP;
-            if (P.top_p < 1.0) {  // sampler.py:145-148
-              const double tgt = P.top_p * (double)Sfix;
-              const Sel a = select(tgt);
-              if (ok) {
-                keep = (int)a.cnt_before + 1;
-                zfix = a.fix_before + a.fix;
-                zf = a.f64_before + a.f64;
-                const double tol = 1e-6 * (double)Sfix;
-                if (fabs((double)a.fix_before - tgt) < tol || fabs((double)zfix - tgt) < tol)
-                  flags |= VS_OUT_TOPP_BOUNDARY;
-              }
+            const bool has_tp = P.top_p < 1.0;
+            const double tgt_p = P.top_p * (double)Sfix;
+            ScanOut cpo;
+            cpo.digit = -1;
+            u64 zlo = Sfix, zhi = Sfix;
+            if (has_tp) {
+              cpo = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, tgt_p);
+              zlo = cpo.fix_before;
+              zhi = cpo.fix_before + cpo.fix;
             }
-            VS_TR(A, 6);
-            if (ok && P.min_p > 0.0) {  // sampler.py:149-152
-              const double pthr = (1.0 / Sf) * P.min_p;
-              int mc = 0;
-              u64 mfx = 0;
-              double mff = 0.0;
+            const int dlo = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, P.u * (double)zlo).digit;
+            const int dhi = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, P.u * (double)zhi).digit;
+            // coarse digits to refine: the top-p bin and the draw's range dlo >= d >= dhi
+            int set[NSET];
+            int ns = 0;
+            if (has_tp) set[ns++] = cpo.digit;
+            for (int d = dlo; d >= dhi; --d) {
+              if (has_tp && d == cpo.digit) continue;
+              if (ns < NSET) set[ns] = d;
+              ++ns;
+            }
+            if (ns > NSET) {
+              radix = true;
+            } else {
+              // ---- round 2: fine histograms of the selected coarse bins ----
+              for (int i = t; i < NSET * NBIN; i += SNT) {
+                s.fc[i] = 0;
+                s.ffix[i] = 0;
+                s.ff64[i] = 0.0;
+              }
+              __syncthreads();
               FOR_XV({
                 const u64 kk = key64(x, (uint32_t)e);
                 if (IS_CAND(x, kk)) {
-                  const float d = x / tt - xs0;
-                  const double pr = exp((double)d);
-                  if (!(pr / Sf < pthr)) {
-                    ++mc;
-                    mfx += (u64)(pr * scale + 0.5);
-                    mff += pr;
+                  const int id = fine_of(x);
+                  const int c = id >> 8;
+                  int j = -1;
+                  for (int q = 0; q < NSET; ++q)
+                    if (q < ns && set[q] == c) j = q;
+                  if (j >= 0) {
+                    u64 fx;
+                    const double pr = mass(x, &fx);
+                    const int b2 = j * NBIN + (id & 0xFF);
+                    atomicAdd(&s.fc[b2], 1u);
+                    atomicAdd(&s.ffix[b2], fx);
+                    unsafeAtomicAdd(&s.ff64[b2], pr);
                   }
                 }
               })
-              mc = block_sum<SNT>(mc, s.redi);
-              mfx = block_sum<SNT>(mfx, s.red64);
-              mff = block_sum<SNT>(mff, s.redf);
-              if (t == 0) {
-                atomicAdd(&ctl->mcnt, (uint32_t)mc);
-                atomicAdd(&ctl->mfix, mfx);
-                unsafeAtomicAdd(&ctl->mf64, mff);
+              __syncthreads();
+              HistSlot* h2 = hslots + slot;
+              slot += ns;
+              for (int i = t; i < ns * NBIN; i += SNT) {
+                if (s.fc[i]) {
+                  HistSlot* hs = h2 + i / NBIN;
+                  const int b2 = i % NBIN;
+                  atomicAdd(&hs->cnt[b2], s.fc[i]);
+                  atomicAdd(&hs->fix[b2], s.ffix[i]);
+                  unsafeAtomicAdd(&hs->f64[b2], s.ff64[i]);
+                }
               }
               ++nbar;
               ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
               if (ok) {
-                const int cm = (int)ld_relaxed(&ctl->mcnt);
-                const int km = cm > 1 ? cm : 1;
-                if (km < keep) {
-                  keep = km;
-                  if (cm >= 1) {
-                    zfix = ld_relaxed64(&ctl->mfix);
-                    zf = ld_relaxed_f64(&ctl->mf64);
-                  } else {
-                    zfix = (u64)(scale + 0.5);
-                    zf = 1.0;
+                for (int i = t; i < ns * NBIN; i += SNT) {
+                  const HistSlot* hs = h2 + i / NBIN;
+                  const int b2 = i % NBIN;
+                  s.fc[i] = ld_relaxed(&hs->cnt[b2]);
+                  s.ffix[i] = ld_relaxed64(&hs->fix[b2]);
+                  s.ff64[i] = ld_relaxed_f64(&hs->f64[b2]);
+                }
+                __syncthreads();
+                // Locate a target in the two-level histogram: the fine bin id and the sums before it.
+                struct Loc {
+                  int id, set_j;
+                  u64 cnt_before, fix_before;
+                  double f64_before;
+                };
+                auto locate = [&](double target) -> Loc {
+                  Loc r;
+                  const ScanOut co = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, target);
+                  int j = -1;
+#pragma unroll
+                  for (int q = 0; q < NSET; ++q)
+                    if (q < ns && set[q] == co.digit) j = q;
+                  r.set_j = j;
+                  r.cnt_before = co.cnt_before;
+                  r.fix_before = co.fix_before;
+                  r.f64_before = co.f64_before;
+                  r.id = co.digit << 8;
+                  if (j >= 0) {
+                    const ScanOut fo = scan256(s, s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN, nullptr,
+                                               false, target - (double)co.fix_before);
+                    r.id |= fo.digit;
+                    r.cnt_before += fo.cnt_before;
+                    r.fix_before += fo.fix_before;
+                    r.f64_before += fo.f64_before;
                   }
+                  return r;
+                };
+                Loc lp_ = {-1, -1, 0, 0, 0.0};
+                u64 z2lo = Sfix, z2hi = Sfix;
+                if (has_tp) {
+                  lp_ = locate(tgt_p);
+                  z2lo = lp_.fix_before;
+                  z2hi = lp_.fix_before + (lp_.set_j >= 0 ? (u64)s.ffix[lp_.set_j * NBIN + (lp_.id & 0xFF)] : (u64)0);
+                }
+                const Loc la = locate(P.u * (double)z2lo), lb = locate(P.u * (double)z2hi);
+                // gather: the top-p fine bin and the fine bins la.id >= id >= lb.id
+                int gcount = 0;
+                bool located = la.set_j >= 0 && lb.set_j >= 0 && (!has_tp || lp_.set_j >= 0);
+                if (located) {
+                  for (int i = t; i < ns * NBIN; i += SNT) {
+                    const int id = (set[i / NBIN] << 8) | (i % NBIN);
+                    if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id)) gcount += (int)s.fc[i];
+                  }
+                  gcount = block_sum<SNT>(gcount, s.redi);
+                }
+                if (!located || gcount > GCAP2) {
+                  radix = true;
+                } else {
+                  FOR_XV({
+                    const u64 kk = key64(x, (uint32_t)e);
+                    if (IS_CAND(x, kk)) {
+                      const int id = fine_of(x);
+                      if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id))
+                        st_dev(&gather[atomicAdd(&ctl->g2count, 1u)], kk);
+                    }
+                  })
+                  g0_writes = false;
+                  VS_TR(A, 6);
+                  if (!arrive_done()) return;  // the last workgroup of the row resolves the exact positions
+                  VS_TR(A, 7);
+                  // ---- final: exact key order inside the located fine bins ----
+                  const int m = (int)ld_relaxed(&ctl->g2count);
+                  u64* fk = s.keys;
+                  int* fi = (int*)(s.keys + GCAP2);
+                  u64* fxs = s.keys + GCAP2 + GCAP2 / 2;
+                  double* fds = (double*)(s.keys + 2 * GCAP2 + GCAP2 / 2);
+                  u64* xch = (u64*)(s.misc + 160);  // two 8-byte exchange slots
+                  for (int i = t; i < m; i += SNT) {
+                    const u64 kk = ld_dev(&gather[i]);
+                    const float x = key_value(kk);
+                    fk[i] = kk;
+                    fi[i] = fine_of(x);
+                    fds[i] = mass(x, &fxs[i]);
+                  }
+                  __syncthreads();
+                  // First element (descending key) of fine bin `id` whose cumulative mass inside the bin reaches
+                  // `tgt` (the last element of the bin if none does, which only rounding can cause).
+                  struct Pick {
+                    u64 key, cnt_in, fix_in, fix;
+                    double f64_in, f64;
+                  };
+                  auto pick = [&](int id, double tgt) -> Pick {
+                    u64 best = 0, low = ~0ull;
+                    for (int i = t; i < m; i += SNT) {
+                      if (fi[i] != id) continue;
+                      const u64 ki = fk[i];
+                      u64 cum = 0;
+                      for (int j = 0; j < m; ++j)
+                        if (fi[j] == id && fk[j] > ki) cum += fxs[j];
+                      if ((double)(cum + fxs[i]) >= tgt) best = ki > best ? ki : best;
+                      low = ki < low ? ki : low;
+                    }
+                    best = block_max<SNT>(best, s.red64);
+                    low = block_min<SNT>(low, s.red64);
+                    const u64 win = best ? best : low;
+                    Pick pk;
+                    pk.key = win;
+                    u64 cnt = 0, fx = 0;
+                    double fd = 0.0;
+                    for (int i = t; i < m; i += SNT) {
+                      if (fi[i] == id && fk[i] > win) {
+                        ++cnt;
+                        fx += fxs[i];
+                        fd += fds[i];
+                      }
+                      if (fk[i] == win) {
+                        xch[0] = fxs[i];
+                        ((double*)xch)[1] = fds[i];
+                      }
+                    }
+                    __syncthreads();
+                    const u64 wfix = xch[0];
+                    const double wf = ((double*)xch)[1];
+                    pk.cnt_in = block_sum<SNT>(cnt, s.red64);
+                    pk.fix_in = block_sum<SNT>(fx, s.red64);
+                    pk.f64_in = block_sum<SNT>(fd, s.redf);
+                    pk.fix = wfix;
+                    pk.f64 = wf;
+                    return pk;
+                  };
+                  uint32_t flags = VS_OUT_COOP;
+                  int keep = total;
+                  u64 zfix = Sfix;
+                  double zf = Sf;
+                  if (has_tp) {  // sampler.py:145-148
+                    const Pick pp = pick(lp_.id, tgt_p - (double)lp_.fix_before);
+                    keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
+                    zfix = lp_.fix_before + pp.fix_in + pp.fix;
+                    zf = lp_.f64_before + pp.f64_in + pp.f64;
+                    const double tol = 1e-6 * (double)Sfix;
+                    if (fabs((double)(zfix - pp.fix) - tgt_p) < tol || fabs((double)zfix - tgt_p) < tol)
+                      flags |= VS_OUT_TOPP_BOUNDARY;
+                  }
+                  // sampler.py:153-156
+                  const double tgt_d = P.u * (double)zfix;
+                  const Loc ld = locate(tgt_d);
+                  const Pick pd = pick(ld.id, tgt_d - (double)ld.fix_before);
+                  const float d = key_value(pd.key) / tt - xs0;
+                  const double before = (double)(ld.fix_before + pd.fix_in);
+                  const double tol = 1e-6 * (double)zfix;
+                  if (fabs(before - tgt_d) < tol || fabs(before + (double)pd.fix - tgt_d) < tol)
+                    flags |= VS_OUT_DRAW_BOUNDARY;
+                  fin.token = (int32_t)key_index(pd.key);
+                  fin.lp = (float)((double)d - log(zf));
+                  fin.keep = keep;
+                  fin.flags = flags;
+                  VS_TR(A, 8);
+                  write_out(A, row, fin);
+                  cleanup(slot);
+                  return;
                 }
               }
             }
-            VS_TR(A, 7);
-            if (ok) {  // sampler.py:153-156
-              const double tgt = P.u * (double)zfix;
-              const Sel bsel = select(tgt);
-              if (ok) {
-                const float xb = key_value(bsel.key);
-                const float d = xb / tt - xs0;
-                fin.token = (int32_t)key_index(bsel.key);
-                fin.lp = (float)((double)d - log(zf));
-                fin.keep = keep;
-                const double tol = 1e-6 * (double)zfix;
-                if (fabs((double)bsel.fix_before - tgt) < tol ||
-                    fabs((double)(bsel.fix_before + bsel.fix) - tgt) < tol)
-                  flags |= VS_OUT_DRAW_BOUNDARY;
-                fin.flags = flags;
+          }
+          if (ok && radix) {
+            // ---- radix fallback: cooperative mass-weighted radix select on the 64-bit keys ----
+            hist_clear(s);
+            FOR_XV({
+              const u64 kk = key64(x, (uint32_t)e);
+              if (IS_CAND(x, kk)) {
+                u64 fx;
+                const double pr = mass(x, &fx);
+                hist_add(s, kk, 56, fx, pr);
+              }
+            })
+            __syncthreads();
+            HistSlot* hr = hslots + slot++;
+            if (t < NBIN && s.hc[t]) {
+              atomicAdd(&hr->cnt[t], s.hc[t]);
+              atomicAdd(&hr->fix[t], s.hfix[t]);
+              unsafeAtomicAdd(&hr->f64[t], s.hf64[t]);
+              atomicMax(&hr->mk[t], s.hmk[t]);
+            }
+            ++nbar;
+            ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+            if (ok) {
+              auto load_slot = [&](HistSlot* hs) {
+                if (t < NBIN) {
+                  s.hc[t] = ld_relaxed(&hs->cnt[t]);
+                  s.hfix[t] = ld_relaxed64(&hs->fix[t]);
+                  s.hf64[t] = ld_relaxed_f64(&hs->f64[t]);
+                  s.hmk[t] = ld_relaxed64(&hs->mk[t]);
+                }
+                __syncthreads();
+              };
+              load_slot(hr);
+              const u64 Sfix = block_sum<SNT>(t < NBIN ? s.hfix[t] : (u64)0, s.red64);
+              const double Sf = block_sum<SNT>(t < NBIN ? s.hf64[t] : 0.0, s.redf);
+              // the first key (descending) whose inclusive cumulative mass reaches target
+              struct Sel {
+                u64 key, cnt_before, fix_before, fix;
+                double f64_before, f64;
+              };
+              auto select = [&](double target) -> Sel {
+                Sel r;
+                r.key = 0;
+                r.cnt_before = r.fix_before = r.fix = 0;
+                r.f64_before = r.f64 = 0.0;
+                load_slot(hr);
+                u64 prefix = 0;
+                int shift = 56;
+                for (;;) {
+                  const ScanOut o = hist_scan(s, false, target - (double)r.fix_before);
+                  r.cnt_before += o.cnt_before;
+                  r.fix_before += o.fix_before;
+                  r.f64_before += o.f64_before;
+                  if (o.cnt <= 1 || shift == 0) {
+                    r.key = o.mk;
+                    r.fix = o.fix;
+                    r.f64 = o.f64;
+                    return r;
+                  }
+                  prefix = (prefix << 8) | (u64)o.digit;
+                  shift -= 8;
+                  hist_clear(s);
+                  FOR_XV({
+                    const u64 kk = key64(x, (uint32_t)e);
+                    if (IS_CAND(x, kk) && (kk >> (shift + 8)) == prefix) {
+                      u64 fx;
+                      const double pr = mass(x, &fx);
+                      hist_add(s, kk, shift, fx, pr);
+                    }
+                  })
+                  __syncthreads();
+                  HistSlot* hs = hslots + slot;
+                  ++slot;
+                  if (t < NBIN && s.hc[t]) {
+                    atomicAdd(&hs->cnt[t], s.hc[t]);
+                    atomicAdd(&hs->fix[t], s.hfix[t]);
+                    unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
+                    atomicMax(&hs->mk[t], s.hmk[t]);
+                  }
+                  ++nbar;
+                  ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+                  if (!ok) return r;
+                  load_slot(hs);
+                }
+              };
+              int keep = total;
+              u64 zfix = Sfix;
+              double zf = Sf;
+              uint32_t flags = VS_OUT_COOP;
+              if (P.top_p < 1.0) {  // sampler.py:145-148
+                const double tgt = P.top_p * (double)Sfix;
+                const Sel a = select(tgt);
+                if (ok) {
+                  keep = (int)a.cnt_before + 1;
+                  zfix = a.fix_before + a.fix;
+                  zf = a.f64_before + a.f64;
+                  const double tol = 1e-6 * (double)Sfix;
+                  if (fabs((double)a.fix_before - tgt) < tol || fabs((double)zfix - tgt) < tol)
+                    flags |= VS_OUT_TOPP_BOUNDARY;
+                }
+              }
+              if (ok && P.min_p > 0.0) {  // sampler.py:149-152
+                const double pthr = (1.0 / Sf) * P.min_p;
+                int mc = 0;
+                u64 mfx = 0;
+                double mff = 0.0;
+                FOR_XV({
+                  const u64 kk = key64(x, (uint32_t)e);
+                  if (IS_CAND(x, kk)) {
+                    u64 fx;
+                    const double pr = mass(x, &fx);
+                    if (!(pr / Sf < pthr)) {
+                      ++mc;
+                      mfx += fx;
+                      mff += pr;
+                    }
+                  }
+                })
+                mc = block_sum<SNT>(mc, s.redi);
+                mfx = block_sum<SNT>(mfx, s.red64);
+                mff = block_sum<SNT>(mff, s.redf);
+                if (t == 0) {
+                  atomicAdd(&ctl->mcnt, (uint32_t)mc);
+                  atomicAdd(&ctl->mfix, mfx);
+                  unsafeAtomicAdd(&ctl->mf64, mff);
+                }
+                ++nbar;
+                ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+                if (ok) {
+                  const int cm = (int)ld_relaxed(&ctl->mcnt);
+                  const int km = cm > 1 ? cm : 1;
+                  if (km < keep) {
+                    keep = km;
+                    if (cm >= 1) {
+                      zfix = ld_relaxed64(&ctl->mfix);
+                      zf = ld_relaxed_f64(&ctl->mf64);
+                    } else {
+                      zfix = (u64)(scale + 0.5);
+                      zf = 1.0;
+                    }
+                  }
+                }
+              }
+              if (ok) {  // sampler.py:153-156
+                const double tgt = P.u * (double)zfix;
+                const Sel bsel = select(tgt);
+                if (ok) {
+                  const float d = key_value(bsel.key) / tt - xs0;
+                  fin.token = (int32_t)key_index(bsel.key);
+                  fin.lp = (float)((double)d - log(zf));
+                  fin.keep = keep;
+                  const double tol = 1e-6 * (double)zfix;
+                  if (fabs((double)bsel.fix_before - tgt) < tol ||
+                      fabs((double)(bsel.fix_before + bsel.fix) - tgt) < tol)
+                    flags |= VS_OUT_DRAW_BOUNDARY;
+                  fin.flags = flags;
+                }
               }
             }
           }
@@ -1235,8 +1569,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   }
 #undef FOR_XV
   VS_TR(A, 9);
-  // In the gather case only workgroup 0 computed `fin`; in every other case all workgroups agree.
-  if (g == 0) write_out(A, row, fin);
+  // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree.
+  if (g == 0 && g0_writes) write_out(A, row, fin);
   if (!ok && t == 0) atomicOr(&ctl->err, 1u);  // a timed-out row clears every histogram slot
   if (arrive_done()) {
     const bool err = ld_relaxed(&ctl->err) != 0;
@@ -1252,6 +1586,14 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 // Host entry points
 // =================================================================================================================
 using namespace vs;
+
+static bool use_cooperative() {
+  static const bool coop = [] {
+    const char* v = getenv("VS_COOPERATIVE");
+    return v && v[0] == '1';
+  }();
+  return coop;
+}
 
 extern "C" size_t vs_sample_workspace_bytes(int B, int V) {
   (void)V;
@@ -1333,8 +1675,15 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
     a.row0 = r0;
     a.B = (B - r0) < RB ? (B - r0) : RB;
     void* kargs[] = {&a};
-    e = hipLaunchCooperativeKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: cooperative launch");
+    // The grid never exceeds what the device holds at once (RB above), so on an otherwise idle device every
+    // workgroup of a row is resident and the row barriers complete; a plain launch is ~18 us cheaper than a
+    // cooperative one on MI355X. VS_COOPERATIVE=1 requests the residency guarantee of a cooperative launch; without
+    // it, a barrier that cannot complete ends with VS_OUT_TIMEOUT on that row instead of hanging.
+    if (use_cooperative())
+      e = hipLaunchCooperativeKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);
+    else
+      e = hipLaunchKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: launch");
   }
   return VS_OK;
 }

@@ -93,14 +93,19 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   u64 am = 0;
   float m = -__builtin_inff();
   double se = 0.0;
-  for (int j0 = 0; j0 < A.NV; j0 += U) {
-    uint4 raw[U];
+  auto load = [&](uint4* r, int j0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int base = lo + ((j0 + u) * VNT + t) * VEC;
-      raw[u] = make_uint4(0, 0, 0, 0);
-      if (j0 + u < A.NV && A.vec_ok && base + VEC <= hi) raw[u] = *(const uint4*)(rowp + (int64_t)base * (DT == VS_F32 ? 4 : 2));
+      r[u] = make_uint4(0, 0, 0, 0);
+      if (j0 + u < A.NV && A.vec_ok && base + VEC <= hi)
+        r[u] = *(const uint4*)(rowp + (int64_t)base * (DT == VS_F32 ? 4 : 2));
     }
+  };
+  uint4 cur[U], nxt[U];
+  load(cur, 0);
+  for (int j0 = 0; j0 < A.NV; j0 += U) {
+    if (j0 + U < A.NV) load(nxt, j0 + U);  // the next batch is in flight while this one is reduced
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (j0 + u >= A.NV) continue;
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       float xs[VEC];
 #pragma unroll
       for (int q = 0; q < VEC; ++q)
-        xs[q] = full ? TR::get(raw[u], q) : (base + q < hi ? TR::one(rowp, base + q) : -__builtin_inff());
+        xs[q] = full ? TR::get(cur[u], q) : (base + q < hi ? TR::one(rowp, base + q) : -__builtin_inff());
       float vm = -__builtin_inff();
 #pragma unroll
       for (int q = 0; q < VEC; ++q) {
@@ -131,6 +136,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
         se += (double)acc;
       }
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) cur[u] = nxt[u];
   }
   VS_TR(A, 1);
   // workgroup merge of (m, se) pairs and the key
@@ -224,6 +231,8 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   int gmin = (vocab_valid + chmax - 1) / chmax;
   if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
   int G = (2 * dv->cus + R - 1) / R;  // aim at >= 2 workgroups per CU in flight
+  const int g4 = (vocab_valid + 4 * unit - 1) / (4 * unit);  // and at most 4 loads per lane
+  if (G < g4) G = g4;
   if (G > VGMAX) G = VGMAX;
   if (G < gmin) G = gmin;
   int CH = (vocab_valid + G - 1) / G;
