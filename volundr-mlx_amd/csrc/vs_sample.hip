@@ -56,7 +56,7 @@ struct RowCtl {
   uint32_t err;     // a workgroup of the row timed out
   uint32_t nminkey; // ~ord32 of the smallest finite logit (max-reduced)
   uint32_t g2count; // second gather reservations
-  uint32_t pad;
+  uint32_t gmax;    // largest per-workgroup kept count
 };
 static_assert(sizeof(RowCtl) == 64, "RowCtl layout");
 
@@ -474,36 +474,74 @@ __device__ __forceinline__ void block_rank_sort(const u64* in, int n, u64* out, 
   __syncthreads();
 }
 
-// Lower bound L for the k-th largest key of the workgroup, from the lane maxima: each wave extracts its q = ceil(k/8)
-// largest lane maxima (q wave-wide max reductions); every extracted key is >= the smallest wave's q-th value, and
-// there are >= k of them when the waves together extracted k. Returns 1 (no bound) otherwise.
-__device__ __forceinline__ u64 lane_max_bound(u64 tmax, int k, const Smem& s) {
+// Lower bound for the k-th largest logit of the workgroup, from the lane maxima (ord32 values): each wave extracts
+// its q = ceil(k/8) largest lane maxima; all extracted lanes hold a value >= the smallest wave's q-th value, and they
+// are >= k lanes when the waves together extracted k. Returns 0 (no bound) otherwise. Ties between lanes only make
+// the bound looser (a lane is extracted once per round).
+__device__ __forceinline__ uint32_t lane_max_bound(uint32_t tmax, int k, const Smem& s) {
   const int q = (k + SNW - 1) / SNW;
-  u64 cur = tmax, wb = 0;
+  uint32_t cur = tmax, wb = 0;
   int got = 0;
   for (int i = 0; i < q; ++i) {
-    const u64 m = wave_max(cur);
+    const uint32_t m = wave_max(cur);
     if (m == 0) break;
     wb = m;
+    // retire exactly one lane holding m (the lowest such lane)
+    const unsigned long long hb = __ballot(cur == m);
+    if (lane_id() == __ffsll((long long)hb) - 1) cur = 0;
     ++got;
-    if (cur == m) cur = 0;
   }
   const int w = threadIdx.x / WAVE;
+  uint32_t* wbs = (uint32_t*)(s.misc + 180);
   __syncthreads();
   if (lane_id() == 0) {
-    s.red64[w] = wb;
+    wbs[w] = wb;
     s.redi[w] = got;
   }
   __syncthreads();
-  u64 L = ~0ull;
+  uint32_t L = ~0u;
   int tot = 0;
 #pragma unroll
   for (int i = 0; i < SNW; ++i) {
     tot += s.redi[i];
-    if (s.redi[i] > 0) L = s.red64[i] < L ? s.red64[i] : L;
+    if (s.redi[i] > 0) L = wbs[i] < L ? wbs[i] : L;
   }
   __syncthreads();
-  return tot >= k ? L : 1;
+  return tot >= k ? L : 0u;
+}
+
+// One LDS exchange for the per-workgroup statistics: a sum, two 32-bit maxima and a 64-bit maximum.
+struct Stats {
+  int n;
+  uint32_t mx1, mx2;
+  u64 am;
+};
+__device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, u64 am, const Smem& s) {
+  n = wave_sum(n);
+  mx1 = wave_max(mx1);
+  mx2 = wave_max(mx2);
+  am = wave_max(am);
+  const int w = threadIdx.x / WAVE;
+  uint32_t* m1 = (uint32_t*)(s.misc + 164);
+  uint32_t* m2 = (uint32_t*)(s.misc + 172);
+  __syncthreads();
+  if (lane_id() == 0) {
+    s.redi[w] = n;
+    m1[w] = mx1;
+    m2[w] = mx2;
+    s.red64[w] = am;
+  }
+  __syncthreads();
+  Stats r = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < SNW; ++i) {
+    r.n += s.redi[i];
+    r.mx1 = m1[i] > r.mx1 ? m1[i] : r.mx1;
+    r.mx2 = m2[i] > r.mx2 ? m2[i] : r.mx2;
+    r.am = s.red64[i] > r.am ? s.red64[i] : r.am;
+  }
+  __syncthreads();
+  return r;
 }
 
 __device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Final& f) {
@@ -700,12 +738,21 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     }
     __syncthreads();
   }
-#define FOR_XV(BODY)                          \
-  for (int i_ = t; i_ < hi - lo; i_ += SNT) { \
-    const int e = lo + i_;                    \
-    const float x = s.xv[i_];                 \
-    BODY                                      \
+#define FOR_XV(BODY)                                              \
+  _Pragma("unroll 4") for (int i_ = t; i_ < hi - lo; i_ += SNT) { \
+    const int e = lo + i_;                                        \
+    const float x = s.xv[i_];                                     \
+    BODY                                                          \
   }
+  // np.argmax key of the chunk; only needed when a whole row has no finite logit (sampler.py:131-132)
+  auto chunk_amkey = [&]() -> u64 {
+    u64 am = 0;
+    FOR_XV({
+      const u64 ka = amkey64(x, (uint32_t)e);
+      am = ka > am ? ka : am;
+    })
+    return block_max<SNT>(am, s.red64);
+  };
   VS_TR(A, 2);
 
   const int top_k = P.top_k;
@@ -791,33 +838,31 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   if (cls == CLS_TOPK) {
     // ---- local top-k by key among finite logits (sampler.py:133-136, ties toward the lower index) ----
     const int k = top_k;
-    u64 tmax = 0, am = 0;
+    uint32_t tmax = 0;
     int nf = 0;
     FOR_XV({
-      const u64 ka = amkey64(x, (uint32_t)e);
-      am = ka > am ? ka : am;
       if (is_finite(x)) {
         ++nf;
-        const u64 kk = key64(x, (uint32_t)e);
-        tmax = kk > tmax ? kk : tmax;
+        const uint32_t o = ord32(x);
+        tmax = o > tmax ? o : tmax;
       }
     })
     const int nb_fin = block_sum<SNT>(nf, s.redi);
-    am = block_max<SNT>(am, s.red64);
+    const u64 am = nb_fin ? (u64)0 : chunk_amkey();
     VS_TR(A, 10);
     int kc = 0;
     if (nb_fin > 0) {
-      // Only keys >= L can be in the local top-k; typically a small multiple of k survive.
-      const u64 L = nb_fin > k ? lane_max_bound(tmax, k, s) : (u64)1;
+      // Only logits >= L can be in the local top-k; typically a small multiple of k survive.
+      const uint32_t L = nb_fin > k ? lane_max_bound(tmax, k, s) : 0u;
       VS_TR(A, 11);
       if (t == 0) s.misc[4] = 0;
       __syncthreads();
       FOR_XV({
         if (is_finite(x)) {
-          const u64 kk = key64(x, (uint32_t)e);
-          if (kk >= L) {
+          const uint32_t o = ord32(x);
+          if (o >= L) {
             const int p = atomicAdd(&s.misc[4], 1);
-            if (p < KEYS_CAP) s.keys[p] = kk;
+            if (p < KEYS_CAP) s.keys[p] = ((u64)o << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
           }
         }
       })
@@ -907,6 +952,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         }
       }
       __syncthreads();
+      VS_TR(A, 14);
       const int n = s.misc[7];
       const int nl = s.misc[8];
       const u64 bam = s.red64[0];
@@ -922,11 +968,20 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         write_out(A, row, f);
       } else {
         const int tot = G * A.kcap;
-        for (int idx = t; idx < tot; idx += SNT) {  // all lists into LDS (one round trip), unused slots zero
-          const int i = idx / A.kcap, q = idx - i * A.kcap;
-          s.keys[idx] = q < kcs[i] ? ld_dev(&cand[idx]) : (u64)0;
+        {  // all lists into LDS, unused slots zero: KEYS_CAP / SNT independent loads per lane, one round trip
+          const int sh = __builtin_ctz(A.kcap);  // kcap is a power of two
+          u64 r[KEYS_CAP / SNT];
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+            const int idx = t + u * SNT;
+            r[u] = (idx < tot && (idx & (A.kcap - 1)) < kcs[idx >> sh]) ? ld_dev(&cand[idx]) : (u64)0;
+          }
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u)
+            if (t + u * SNT < tot) s.keys[t + u * SNT] = r[u];
         }
         __syncthreads();
+        VS_TR(A, 15);
         const int r = (keff + nl - 1) / nl;
         // the first r entries of every list, packed into c0 (<= keff + 63 keys; tk is free until the survivors)
         u64* c0 = s.tk;
@@ -938,12 +993,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (t == WAVE - 1) s.misc[10] = incl;
         }
         __syncthreads();
-        for (int idx = t; idx < G * r; idx += SNT) {
+        for (int idx = t; idx < G * r; idx += SNT) {  // one (list, position) per lane
           const int i = idx / r, q = idx - i * r;
           if (q < kcs[i]) c0[offs[i] + q] = s.keys[i * A.kcap + q];
         }
         __syncthreads();
         const int n0 = s.misc[10];
+        VS_TR(A, 16);
         u64 M = 0;
         if (n0 >= keff) {  // M = the keff-th largest of c0
           for (int i = t; i < n0; i += SNT) {
@@ -956,6 +1012,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           M = s.red64[1];
         }
         __syncthreads();
+        VS_TR(A, 17);
         u64* sel = s.tk + KCAP;
         for (int idx = t; idx < tot; idx += SNT) {
           const u64 kk = s.keys[idx];
@@ -999,10 +1056,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   {
     int nf = 0;
     uint32_t mk = 0, nmk = 0;
-    u64 am = 0;
     FOR_XV({
-      const u64 ka = amkey64(x, (uint32_t)e);
-      am = ka > am ? ka : am;
       if (is_finite(x)) {
         ++nf;
         const uint32_t o = ord32(x);
@@ -1010,17 +1064,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         nmk = ~o > nmk ? ~o : nmk;
       }
     })
-    nf = block_sum<SNT>(nf, s.redi);
-    mk = block_max<SNT>(mk, (uint32_t*)s.redi);
-    nmk = block_max<SNT>(nmk, (uint32_t*)s.redi);
-    am = block_max<SNT>(am, s.red64);
+    Stats st = block_stats(nf, mk, nmk, 0, s);
+    if (st.n == 0) st.am = chunk_amkey();
     if (t == 0) {
-      if (nf) {
-        atomicAdd(&ctl->nfin, (uint32_t)nf);
-        atomicMax(&ctl->mkey, mk);
-        atomicMax(&ctl->nminkey, nmk);
+      if (st.n) {
+        atomicAdd(&ctl->nfin, (uint32_t)st.n);
+        atomicMax(&ctl->mkey, st.mx1);
+        atomicMax(&ctl->nminkey, st.mx2);
       }
-      atomicMax(&ctl->amkey, am);
+      atomicMax(&ctl->amkey, st.am);
     }
   }
   ++nbar;
@@ -1131,16 +1183,19 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           }
         })
         cb = block_sum<SNT>(cb, s.redi);
+        // each workgroup gathers into its own region of GB keys when its kept count fits
+        const int GB = 1 << (31 - __builtin_clz(GCAP / G));  // power of two <= GCAP / G
         if (t == 0) {
-          s.misc[9] = (int)atomicAdd(&ctl->gcount, (uint32_t)cb);
+          atomicAdd(&ctl->gcount, (uint32_t)cb);
+          atomicMax(&ctl->gmax, (uint32_t)cb);
+          st_dev(&parts[g].kc, (uint32_t)cb);
           s.misc[10] = 0;
         }
         __syncthreads();
-        const int gbase = s.misc[9];
-        if (gbase + cb <= GSMALL) {
+        if (cb <= GB && cb <= GSMALL) {
           FOR_XV({
             const u64 kk = key64(x, (uint32_t)e);
-            if (IS_CAND(x, kk)) st_dev(&gather[gbase + atomicAdd(&s.misc[10], 1)], kk);
+            if (IS_CAND(x, kk)) st_dev(&gather[g * GB + atomicAdd(&s.misc[10], 1)], kk);
           })
         }
         HistSlot* h1 = hslots + slot++;
@@ -1153,12 +1208,37 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
         if (ok) {
           const int total = (int)ld_relaxed(&ctl->gcount);
+          const int gmax = (int)ld_relaxed(&ctl->gmax);
           VS_TR(A, 5);
           bool radix = false;
-          if (total <= GSMALL) {
+          if (total <= GSMALL && gmax <= GB) {
             // ---- small kept set: one workgroup ranks it and finishes as for TOPK ----
             if (g == 0) {
-              for (int i = t; i < total; i += SNT) s.keys[i] = ld_dev(&gather[i]);
+              int* offs = s.misc + 96;  // [G]
+              int* cnts = s.misc + 32;  // [G]
+              if (t < WAVE) {
+                const int c = t < G ? (int)ld_dev(&parts[t].kc) : 0;
+                const int incl = wave_scan(c);
+                if (t < G) {
+                  offs[t] = incl - c;
+                  cnts[t] = c;
+                }
+              }
+              __syncthreads();
+              {  // GCAP / SNT independent loads per lane, one round trip
+                const int sh = __builtin_ctz(GB);  // GB is a power of two
+                u64 r[GCAP / SNT];
+#pragma unroll
+                for (int u = 0; u < GCAP / SNT; ++u) {
+                  const int idx = t + u * SNT;
+                  r[u] = (idx < G * GB && (idx & (GB - 1)) < cnts[idx >> sh]) ? ld_dev(&gather[idx]) : (u64)0;
+                }
+#pragma unroll
+                for (int u = 0; u < GCAP / SNT; ++u) {
+                  const int idx = t + u * SNT;
+                  if (idx < G * GB && (idx & (GB - 1)) < cnts[idx >> sh]) s.keys[offs[idx >> sh] + (idx & (GB - 1))] = r[u];
+                }
+              }
               __syncthreads();
               block_rank_sort(s.keys, total, s.tk, total);
               fin = wave_sample(s, s.tk, total, P);
@@ -1643,8 +1723,8 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
   if (RB > rows_target) RB = rows_target;
   if (RB < 1) return fail(VS_EINVAL, "vs_sample_batch: a row does not fit on the device at once");
   if (ws_bytes < (size_t)RB * ROW_WS) return fail(VS_EWORKSPACE, "vs_sample_batch: workspace too small");
-  int kcap = KEYS_CAP / G;
-  if (kcap > KCAP) kcap = KCAP;
+  int kcap = 1;  // list capacity per workgroup: a power of two <= KEYS_CAP / G
+  while (kcap * 2 <= KEYS_CAP / G && kcap * 2 <= KCAP) kcap *= 2;
   int bits = 0;
   while ((1ll << bits) < (long long)V) ++bits;
   SampleArgs a;
