@@ -24,6 +24,13 @@ for p in (ROOT, ROOT / "volundr-mlx_amd"):
         sys.path.insert(0, str(p))
 
 METRIC = "sampling step latency µs + HBM GB/s at B=16, V=163840 on 1 MI355X"
+WORKLOADS = {
+    "c1": "C1: B=1 V=163840 fp32, top-k 20 (BASELINE configs[0])",
+    "c2": "C2: greedy verify [1,17,163840] bf16 + drafts [1,16] (BASELINE configs[1])",
+    "c3": "C3: B=16 V=163840 fp32 mixed-parameter sampling, histories 16x4096 (BASELINE configs[2])",
+    "c4": "C4: greedy verify [4,17,163840] bf16 + drafts [4,16] (BASELINE configs[3])",
+    "c5": "C5: B=16 V=163840 fp32 near-flat, top-p 0.95, histories 16x32768 (BASELINE configs[4])",
+}
 PEAK_GBPS = 8000.0
 V = 163840
 
@@ -132,6 +139,8 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB --steps times (rocprof counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the token-selection path is per-row and needs no collectives; "
@@ -142,39 +151,60 @@ def main():
     from volundr_amd import synth
 
     dev = torch.device("cuda:0")
+    if a.copy_calibration:
+        n = a.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(a.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "steps": a.steps}))
+        return
     d = synth.CONFIGS[a.config](seed=0)
-    B = d["logits"].shape[0]
-    (e2e, kern), (e2e_w, kern_w), algo = bench_sample(torch, dev, d, a.steps, a.warmup, a.slots)
+    verify = "logits_bf16" in d
+    if verify:
+        (e2e, kern), (e2e_w, kern_w), algo, ntok = bench_verify(torch, dev, d, a.steps, a.warmup, a.slots)
+        B = d["logits_bf16"].shape[0]
+    else:
+        (e2e, kern), (e2e_w, kern_w), algo = bench_sample(torch, dev, d, a.steps, a.warmup, a.slots)
+        B = d["logits"].shape[0]
+        ntok = B
     others = {}
+
+    def entry(e2e_, ev_, e2e_w_, ab_, ntok_):
+        return {"us_per_step": round(e2e_, 2), "warm_us_per_step": round(e2e_w_, 2),
+                "kernel_us_event_pairs": round(ev_, 2), "algo_bytes": ab_,
+                "hbm_gbps": round(ab_ / (e2e_ * 1e-6) / 1e9, 1), "tokens_per_s": round(ntok_ / (e2e_ * 1e-6), 1)}
+
     if not a.no_others:
-        for name in ("c1", "c5"):
+        for name in ("c1", "c3", "c5"):
             if name == a.config:
                 continue
             dd = synth.CONFIGS[name](seed=0)
             (oe, ok), (we, wk), ab = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
-            others[name] = {"us_per_step": round(oe, 2), "kernel_us": round(ok, 2), "warm_us_per_step": round(we, 2),
-                            "warm_kernel_us": round(wk, 2), "algo_bytes": ab,
-                            "hbm_gbps": round(ab / (ok * 1e-6) / 1e9, 1),
-                            "tokens_per_s": round(dd["logits"].shape[0] / (oe * 1e-6), 1)}
+            others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         for name in ("c2", "c4"):
+            if name == a.config:
+                continue
             dd = synth.CONFIGS[name](seed=0)
-            (oe, ok), (we, wk), ab, ntok = bench_verify(torch, dev, dd, a.steps, a.warmup, a.slots)
-            others[name] = {"us_per_step": round(oe, 2), "kernel_us": round(ok, 2), "warm_us_per_step": round(we, 2),
-                            "warm_kernel_us": round(wk, 2), "algo_bytes": ab,
-                            "hbm_gbps": round(ab / (ok * 1e-6) / 1e9, 1),
-                            "tokens_per_s": round(ntok / (oe * 1e-6), 1)}
-    cpu = None if a.no_cpu else cpu_baseline(d)
-    ach = algo / (kern * 1e-6) / 1e9
+            (oe, ok), (we, wk), ab, nt = bench_verify(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others[name] = entry(oe, ok, we, ab, nt)
+    cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
+    # One kernel per step, launched back to back: the per-step time is the kernel's average launch duration plus
+    # the inter-dispatch gap (rocprofv3 --kernel-trace agrees within a few percent); per-launch event pairs add
+    # their own overhead and are reported separately.
+    ach = algo / (e2e * 1e-6) / 1e9
     line = {
         "metric": METRIC, "value": round(e2e, 2), "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(e2e / 1000.0, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"{a.config.upper()}: B={B} V={V} fp32 mixed-parameter sampling (BASELINE configs[2])",
-                   "B": B, "V": V, "history_len": None if d["hists"] is None else int(d["hists"].shape[1]),
+        "dtype": "bf16" if verify else "f32", "data": "synthetic",
+        "config": {"workload": WORKLOADS[a.config], "B": B, "V": V,
+                   "history_len": None if verify or d["hists"] is None else int(d["hists"].shape[1]),
                    "logit_slots": a.slots},
-        "tokens_per_s": round(B / (e2e * 1e-6), 1),
+        "tokens_per_s": round(ntok / (e2e * 1e-6), 1),
         "hbm_gbps": round(algo / (e2e * 1e-6) / 1e9, 1),
-        "kernel_us": round(kern, 2), "warm_us_per_step": round(e2e_w, 2), "warm_kernel_us": round(kern_w, 2),
+        "kernel_us_event_pairs": round(kern, 2), "warm_us_per_step": round(e2e_w, 2),
+        "warm_kernel_us_event_pairs": round(kern_w, 2),
         "kernels_per_step": 1,
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(ach / PEAK_GBPS, 4), "traffic": load_traffic(a.config),

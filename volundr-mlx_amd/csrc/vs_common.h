@@ -180,6 +180,21 @@ __device__ __forceinline__ T wave_scan(T v) {
   return v;
 }
 
+// Wave-aggregated append: lanes with `pred` get consecutive slots of *counter (an LDS counter), with one atomic per
+// wave instead of one per lane (same-address atomics serialise). Works on LDS or device counters. Returns the
+// slot, or -1.
+template <typename C>
+__device__ __forceinline__ int wave_append(bool pred, C* counter) {
+  const unsigned long long m = __ballot(pred);
+  if (!m) return -1;
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  const int leader = __ffsll((long long)m) - 1;
+  int base = 0;
+  if (lane_id() == leader) base = (int)atomicAdd(counter, (C)__popcll(m));
+  base = __builtin_amdgcn_readlane(base, leader);
+  return pred ? base + below : -1;
+}
+
 // Block-wide reductions for a block of NT threads; `red` is LDS scratch of >= NT/64 elements of T.
 // Every thread receives the result.
 template <int NT, typename T>

@@ -858,13 +858,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       if (t == 0) s.misc[4] = 0;
       __syncthreads();
       FOR_XV({
-        if (is_finite(x)) {
-          const uint32_t o = ord32(x);
-          if (o >= L) {
-            const int p = atomicAdd(&s.misc[4], 1);
-            if (p < KEYS_CAP) s.keys[p] = ((u64)o << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
-          }
-        }
+        const uint32_t o = ord32(x);
+        const bool c = is_finite(x) && o >= L;
+        const int p = wave_append(c, &s.misc[4]);
+        if (c && p < KEYS_CAP) s.keys[p] = ((u64)o << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
       })
       __syncthreads();
       const int C = s.misc[4];
@@ -1016,10 +1013,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         u64* sel = s.tk + KCAP;
         for (int idx = t; idx < tot; idx += SNT) {
           const u64 kk = s.keys[idx];
-          if (kk != 0 && kk >= M) {
-            const int p = atomicAdd(&s.misc[9], 1);
-            if (p < KCAP) sel[p] = kk;
-          }
+          const bool c = kk != 0 && kk >= M;
+          const int p = wave_append(c, &s.misc[9]);
+          if (c && p < KCAP) sel[p] = kk;
         }
         __syncthreads();
         const int Cm = s.misc[9];
@@ -1064,8 +1060,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         nmk = ~o > nmk ? ~o : nmk;
       }
     })
+    VS_TR(A, 20);
     Stats st = block_stats(nf, mk, nmk, 0, s);
     if (st.n == 0) st.am = chunk_amkey();
+    VS_TR(A, 21);
     if (t == 0) {
       if (st.n) {
         atomicAdd(&ctl->nfin, (uint32_t)st.n);
@@ -1075,6 +1073,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       atomicMax(&ctl->amkey, st.am);
     }
   }
+#ifdef VS_TRACE
+  publish_wait();
+  __syncthreads();
+  VS_TR(A, 22);
+#endif
   ++nbar;
   ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
   VS_TR(A, 3);
@@ -1195,7 +1198,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (cb <= GB && cb <= GSMALL) {
           FOR_XV({
             const u64 kk = key64(x, (uint32_t)e);
-            if (IS_CAND(x, kk)) st_dev(&gather[g * GB + atomicAdd(&s.misc[10], 1)], kk);
+            const bool c = IS_CAND(x, kk);
+            const int p = wave_append(c, &s.misc[10]);
+            if (c) st_dev(&gather[g * GB + p], kk);
           })
         }
         HistSlot* h1 = hslots + slot++;
@@ -1379,11 +1384,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 } else {
                   FOR_XV({
                     const u64 kk = key64(x, (uint32_t)e);
+                    bool c = false;
                     if (IS_CAND(x, kk)) {
                       const int id = fine_of(x);
-                      if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id))
-                        st_dev(&gather[atomicAdd(&ctl->g2count, 1u)], kk);
+                      c = (has_tp && id == lp_.id) || (id <= la.id && id >= lb.id);
                     }
+                    const int p = wave_append(c, &ctl->g2count);
+                    if (c) st_dev(&gather[p], kk);
                   })
                   g0_writes = false;
                   VS_TR(A, 6);
