@@ -128,6 +128,16 @@ def test_edits(dev):
     assert out.ids[0].item() == 5 and out.ids[3].item() == V - 1
 
 
+def test_long_and_unaligned_histories(dev):
+    # histories beyond the in-register prefetch (32768 tokens) and rows whose history starts unaligned
+    rng = np.random.default_rng(23)
+    B, V = 3, 20000
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    ps = [Sampling(top_k=30, repetition_penalty=1.3, frequency_penalty=0.05, presence_penalty=0.2)] * B
+    hists = [rng.integers(0, V, size=40001), rng.integers(0, 300, size=7), rng.integers(0, V, size=32771)]
+    run(dev, x, ps, rng.random(B), hists, label="long histories")
+
+
 def test_nonfinite_rows(dev):
     V = 3000
     x = np.zeros((5, V), np.float32)

@@ -474,6 +474,76 @@ __device__ __forceinline__ void block_rank_sort(const u64* in, int n, u64* out, 
   __syncthreads();
 }
 
+// Sort 64*E keys held by one wave descending (lane L holds positions L + 64*i in e[i]); the bitonic network is
+// fully unrolled: partners at distance < 64 are exchanged across lanes (DPP / permlane), the others in-lane.
+template <int E>
+__device__ __forceinline__ void wave_sort_desc(u64 (&e)[E]) {
+  const int L = lane_id();
+#pragma unroll
+  for (int k = 2; k <= 64 * E; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+        const int d = j / 64;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          if ((i & d) == 0) {
+            const int pos = L + 64 * i;
+            const bool desc = (pos & k) == 0;
+            const u64 a = e[i], b = e[i + d];
+            const u64 mx = a > b ? a : b, mn = a > b ? b : a;
+            e[i] = desc ? mx : mn;
+            e[i + d] = desc ? mn : mx;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const u64 o = lane_xor_rt(e[i], j);
+          const int pos = L + 64 * i;
+          const bool desc = (pos & k) == 0, lower = (pos & j) == 0;
+          const u64 mx = e[i] > o ? e[i] : o, mn = e[i] > o ? o : e[i];
+          e[i] = (desc == lower) ? mx : mn;
+        }
+      }
+    }
+  }
+}
+
+// Sorted copy of n <= 256 keys: out[r] = key of rank r for r < kout. One wave sorts (the others wait at the final
+// barrier); larger n falls back to rank counting over the whole workgroup.
+__device__ __forceinline__ void small_sort(const u64* in, int n, u64* out, int kout) {
+  if (n > 256) {
+    block_rank_sort(in, n, out, kout);
+    return;
+  }
+  if (threadIdx.x < WAVE) {
+    const int L = threadIdx.x;
+    if (n <= 64) {
+      u64 e[1] = {L < n ? in[L] : (u64)0};
+      wave_sort_desc<1>(e);
+      if (L < kout) out[L] = e[0];
+    } else if (n <= 128) {
+      u64 e[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) e[i] = L + 64 * i < n ? in[L + 64 * i] : (u64)0;
+      wave_sort_desc<2>(e);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (L + 64 * i < kout) out[L + 64 * i] = e[i];
+    } else {
+      u64 e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = L + 64 * i < n ? in[L + 64 * i] : (u64)0;
+      wave_sort_desc<4>(e);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (L + 64 * i < kout) out[L + 64 * i] = e[i];
+    }
+  }
+  __syncthreads();
+}
+
 // Lower bound for the k-th largest logit of the workgroup, from the lane maxima (ord32 values): each wave extracts
 // its q = ceil(k/8) largest lane maxima; all extracted lanes hold a value >= the smallest wave's q-th value, and they
 // are >= k lanes when the waves together extracted k. Returns 0 (no bound) otherwise. Ties between lanes only make
@@ -838,15 +908,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   if (cls == CLS_TOPK) {
     // ---- local top-k by key among finite logits (sampler.py:133-136, ties toward the lower index) ----
     const int k = top_k;
-    uint32_t tmax = 0;
+    float fmx = -__builtin_inff();
     int nf = 0;
     FOR_XV({
       if (is_finite(x)) {
         ++nf;
-        const uint32_t o = ord32(x);
-        tmax = o > tmax ? o : tmax;
+        fmx = fmaxf(fmx, x);
       }
     })
+    const uint32_t tmax = nf ? ord32(fmx) : 0u;
     const int nb_fin = block_sum<SNT>(nf, s.redi);
     const u64 am = nb_fin ? (u64)0 : chunk_amkey();
     VS_TR(A, 10);
@@ -857,11 +927,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       VS_TR(A, 11);
       if (t == 0) s.misc[4] = 0;
       __syncthreads();
+      const float Lf = L ? inv_ord32(L) : -__builtin_inff();  // x >= Lf  <=>  ord32(x) >= L for finite x
       FOR_XV({
-        const uint32_t o = ord32(x);
-        const bool c = is_finite(x) && o >= L;
+        const bool c = x >= Lf && is_finite(x);
         const int p = wave_append(c, &s.misc[4]);
-        if (c && p < KEYS_CAP) s.keys[p] = ((u64)o << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+        if (c && p < KEYS_CAP) s.keys[p] = key64(x, (uint32_t)e);
       })
       __syncthreads();
       const int C = s.misc[4];
@@ -872,7 +942,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #endif
       kc = C < k ? C : k;
       if (C <= RANK_MAX) {
-        block_rank_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
+        small_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
       } else {
         // Many keys above the bound (few lanes hold finite values): radix select, then rank the k survivors.
         u64 T;
@@ -915,47 +985,54 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           }
         })
         __syncthreads();
-        block_rank_sort(sel, kc, s.tk, kc);
+        small_sort(sel, kc, s.tk, kc);
       }
-      for (int i = t; i < kc; i += SNT) st_dev(&cand[g * A.kcap + i], s.tk[i]);
+      for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
       VS_TR(A, 13);
     }
+    if (nb_fin == 0)  // an empty list is all zeros too
+      for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], (u64)0);
     put_part(am, (uint32_t)nb_fin, (uint32_t)kc, 0.0f, 0.0);
     VS_TR(A, 3);
     VS_TRC(A, 31);
     if (arrive_done()) {
       VS_TR(A, 4);
-      // ---- merge (last workgroup of the row). Each workgroup's list is its sorted local top-min(k, n_g). Any keff
-      // entries taken from the list heads bound the global keff-th key from below, so with r = ceil(keff / lists)
-      // heads per list, M = keff-th largest of those heads leaves only about keff survivors. ----
-      int* kcs = s.misc + 32;  // [G] list lengths (G <= 64)
-      if (t < WAVE) {
-        int c = 0, nf2 = 0;
+      // ---- merge (last workgroup of the row). Each workgroup's list is its sorted local top-min(k, n_g), zero
+      // padded. Any keff list entries bound the global keff-th key from below, so with r = ceil(keff / lists) heads
+      // per list, M = the keff-th largest of those heads leaves about keff survivors. ----
+      const int tot = G * A.kcap;
+      {  // partials and all lists in one round trip
+        u64 r8[KEYS_CAP / SNT];
+#pragma unroll
+        for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+          const int idx = t + u * SNT;
+          r8[u] = idx < tot ? ld_dev(&cand[idx]) : (u64)0;
+        }
+        int nf2 = 0;
         u64 k2 = 0;
         if (t < G) {
-          c = (int)ld_dev(&parts[t].kc);
           nf2 = (int)ld_dev(&parts[t].nfin);
           k2 = ld_dev(&parts[t].amkey);
-          kcs[t] = c;
         }
-        const int nn = wave_sum(nf2);
-        const u64 bam2 = wave_max(k2);
-        const int nl = wave_sum(c > 0 ? 1 : 0);
-        if (t == 0) {
-          s.misc[7] = nn;
-          s.misc[8] = nl;
-          s.red64[0] = bam2;
-          s.misc[9] = 0;
+#pragma unroll
+        for (int u = 0; u < KEYS_CAP / SNT; ++u)
+          if (t + u * SNT < tot) s.keys[t + u * SNT] = r8[u];
+        if (t < WAVE) {
+          const int nn = wave_sum(nf2);
+          const u64 bam2 = wave_max(k2);
+          if (t == 0) {
+            s.misc[7] = nn;
+            s.red64[0] = bam2;
+            s.misc[9] = 0;
+          }
         }
       }
       __syncthreads();
       VS_TR(A, 14);
       const int n = s.misc[7];
-      const int nl = s.misc[8];
       const u64 bam = s.red64[0];
       int keff = k < n ? k : n;  // sampler.py:133-134
       if (keff < 1) keff = 1;
-      __syncthreads();
       if (n == 0) {  // sampler.py:131-132
         Final f;
         f.token = (int32_t)key_index(bam);
@@ -964,49 +1041,31 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         f.keep = 0;
         write_out(A, row, f);
       } else {
-        const int tot = G * A.kcap;
-        {  // all lists into LDS, unused slots zero: KEYS_CAP / SNT independent loads per lane, one round trip
-          const int sh = __builtin_ctz(A.kcap);  // kcap is a power of two
-          u64 r[KEYS_CAP / SNT];
-#pragma unroll
-          for (int u = 0; u < KEYS_CAP / SNT; ++u) {
-            const int idx = t + u * SNT;
-            r[u] = (idx < tot && (idx & (A.kcap - 1)) < kcs[idx >> sh]) ? ld_dev(&cand[idx]) : (u64)0;
-          }
-#pragma unroll
-          for (int u = 0; u < KEYS_CAP / SNT; ++u)
-            if (t + u * SNT < tot) s.keys[t + u * SNT] = r[u];
-        }
-        __syncthreads();
-        VS_TR(A, 15);
-        const int r = (keff + nl - 1) / nl;
-        // the first r entries of every list, packed into c0 (<= keff + 63 keys; tk is free until the survivors)
-        u64* c0 = s.tk;
-        int* offs = s.misc + 96;  // [G]
+        // lists with at least one entry (one wave)
         if (t < WAVE) {
-          const int lim = t < G ? (kcs[t] < r ? kcs[t] : r) : 0;
-          const int incl = wave_scan(lim);
-          if (t < G) offs[t] = incl - lim;
-          if (t == WAVE - 1) s.misc[10] = incl;
+          const int nl_ = wave_sum((t < G && s.keys[t * A.kcap] != 0) ? 1 : 0);
+          if (t == 0) s.misc[8] = nl_;
         }
         __syncthreads();
-        for (int idx = t; idx < G * r; idx += SNT) {  // one (list, position) per lane
-          const int i = idx / r, q = idx - i * r;
-          if (q < kcs[i]) c0[offs[i] + q] = s.keys[i * A.kcap + q];
-        }
-        __syncthreads();
-        const int n0 = s.misc[10];
-        VS_TR(A, 16);
+        const int nl = s.misc[8];
+        const int r = (keff + nl - 1) / nl;
+        VS_TR(A, 15);
+        // M = the keff-th largest of the first r entries of every list (0 when they are fewer than keff)
+        const int nh = G * r;
         u64 M = 0;
-        if (n0 >= keff) {  // M = the keff-th largest of c0
-          for (int i = t; i < n0; i += SNT) {
-            const u64 ki = c0[i];
-            int rank = 0;
-            for (int j = 0; j < n0; ++j) rank += c0[j] > ki;
-            if (rank == keff - 1) s.red64[1] = ki;
-          }
-          __syncthreads();
-          M = s.red64[1];
+        u64* heads = s.tk;  // tk is free until the survivors are sorted
+        for (int idx = t; idx < nh; idx += SNT) heads[idx] = s.keys[(idx / r) * A.kcap + idx % r];
+        __syncthreads();
+        VS_TR(A, 16);
+        if (nh <= 256) {
+          u64* hs = s.tk + KCAP;
+          small_sort(heads, nh, hs, nh < KCAP ? nh : KCAP);
+          M = keff - 1 < nh ? hs[keff - 1] : (u64)0;  // a zero here means fewer than keff heads: no bound
+        } else {
+          int avail = 0;
+          for (int idx = t; idx < nh; idx += SNT) avail += heads[idx] != 0;
+          avail = block_sum<SNT>(avail, s.redi);
+          if (avail >= keff) M = block_kth(s, heads, nh, keff);
         }
         __syncthreads();
         VS_TR(A, 17);
@@ -1022,7 +1081,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         __syncthreads();
         VS_TR(A, 5);
         if (Cm <= KCAP) {
-          block_rank_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
+          small_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
         } else {
           const u64 T = block_kth(s, s.keys, tot, keff);
           if (t == 0) s.misc[10] = 0;
@@ -1035,7 +1094,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             }
           }
           __syncthreads();
-          block_rank_sort(sel, keff, s.tk, keff);
+          small_sort(sel, keff, s.tk, keff);
         }
         VS_TR(A, 6);
         const Final f = wave_sample(s, s.tk, keff, P);
@@ -1245,7 +1304,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 }
               }
               __syncthreads();
-              block_rank_sort(s.keys, total, s.tk, total);
+              small_sort(s.keys, total, s.tk, total);
               fin = wave_sample(s, s.tk, total, P);
               fin.flags |= VS_OUT_GATHER;
             }
