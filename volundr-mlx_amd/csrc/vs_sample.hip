@@ -36,7 +36,7 @@ constexpr int GSMALL = 128;      // kept sets up to this size are finished in on
 constexpr int GCAP2 = 512;       // elements gathered from the located value bins
 constexpr int NSET = 4;          // coarse value bins refined in the second histogram round
 constexpr int RANK_MAX = 512;    // largest set ranked by counting
-constexpr int KEYS_CAP = 4096;   // LDS key area (32 KB)
+constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
 constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
 
@@ -95,7 +95,8 @@ struct SampleArgs {
   int vec_ok;  // 16-byte loads allowed
   int has_hist;
   int lds_ch;  // chunk length the LDS areas are sized for
-  int kcap;    // TOPK class bound for this launch
+  int kcap;    // candidate-list capacity per workgroup (a power of two)
+  int kmax;    // largest top_k of the TOPK class for this launch
   uint32_t spin_limit;
   double fix_scale;  // probability -> fixed point
   const vs_row_params* params;
@@ -501,9 +502,8 @@ __device__ __forceinline__ void wave_sort_desc(u64 (&e)[E]) {
         for (int i = 0; i < E; ++i) {
           const u64 o = lane_xor_rt(e[i], j);
           const int pos = L + 64 * i;
-          const bool desc = (pos & k) == 0, lower = (pos & j) == 0;
-          const u64 mx = e[i] > o ? e[i] : o, mn = e[i] > o ? o : e[i];
-          e[i] = (desc == lower) ? mx : mn;
+          const bool take_max = ((pos & k) == 0) == ((pos & j) == 0);
+          e[i] = ((e[i] > o) == take_max) ? e[i] : o;
         }
       }
     }
@@ -826,7 +826,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   VS_TR(A, 2);
 
   const int top_k = P.top_k;
-  const int cls = (P.flags & VS_ROW_GREEDY) ? CLS_GREEDY : ((top_k >= 1 && top_k <= A.kcap) ? CLS_TOPK : CLS_FULL);
+  const int cls = (P.flags & VS_ROW_GREEDY) ? CLS_GREEDY : ((top_k >= 1 && top_k <= A.kmax) ? CLS_TOPK : CLS_FULL);
   int slot = 0;  // histogram slots used by this row (identical in all its workgroups)
   uint32_t nbar = 0;
   bool ok = true;
@@ -940,10 +940,46 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #ifdef VS_TRACE
       if (t == 0 && A.trace) A.trace[(size_t)blockIdx.x * 32 + 19] = C;
 #endif
-      kc = C < k ? C : k;
-      if (C <= RANK_MAX) {
+      // The list this workgroup publishes: its rloc = ceil(k / G) largest keys first (the heads, descending), then
+      // the other candidates in any order, zero padded to kcap. The merge bounds the global keff-th key with the
+      // heads and only sorts the survivors.
+      const int rloc = (k + G - 1) / G;
+      if (C <= 256 && C <= A.kcap && rloc <= 8) {
+        kc = C;
+        u64* hl = s.tk;         // heads
+        u64* rest = s.tk + 16;  // the other candidates (<= 256)
+        if (t < WAVE) {
+          u64 ev[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ev[i] = t + 64 * i < C ? s.keys[t + 64 * i] : (u64)0;
+          for (int h = 0; h < rloc; ++h) {
+            u64 lm = ev[0];
+#pragma unroll
+            for (int i = 1; i < 4; ++i) lm = ev[i] > lm ? ev[i] : lm;
+            const u64 m = wave_max(lm);
+            if (t == 0) hl[h] = m;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (ev[i] == m) ev[i] = 0;  // keys are unique: one slot retires (none when m == 0)
+          }
+          if (t == 0) s.misc[5] = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int p = wave_append(ev[i] != 0, &s.misc[5]);
+            if (ev[i] != 0) rest[p] = ev[i];
+          }
+        }
+        __syncthreads();
+        const int R = s.misc[5];
+        for (int i = t; i < A.kcap; i += SNT) {
+          const u64 v = i < rloc ? hl[i] : (i - rloc < R ? rest[i - rloc] : (u64)0);
+          st_dev(&cand[g * A.kcap + i], v);
+        }
+      } else if (C <= RANK_MAX) {
+        kc = C < k ? C : k;
         small_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
       } else {
+        kc = C < k ? C : k;
         // Many keys above the bound (few lanes hold finite values): radix select, then rank the k survivors.
         u64 T;
         if (C <= KEYS_CAP) {
@@ -987,7 +1023,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         __syncthreads();
         small_sort(sel, kc, s.tk, kc);
       }
-      for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
+      if (!(C <= 256 && C <= A.kcap && rloc <= 8))  // the sorted local top-k serves as the list
+        for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
       VS_TR(A, 13);
     }
     if (nb_fin == 0)  // an empty list is all zeros too
@@ -1041,16 +1078,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         f.keep = 0;
         write_out(A, row, f);
       } else {
-        // lists with at least one entry (one wave)
-        if (t < WAVE) {
-          const int nl_ = wave_sum((t < G && s.keys[t * A.kcap] != 0) ? 1 : 0);
-          if (t == 0) s.misc[8] = nl_;
-        }
-        __syncthreads();
-        const int nl = s.misc[8];
-        const int r = (keff + nl - 1) / nl;
+        // every list starts with its r largest keys in descending order
+        const int r = (k + G - 1) / G;
         VS_TR(A, 15);
-        // M = the keff-th largest of the first r entries of every list (0 when they are fewer than keff)
+        // M = the keff-th largest list head (0 when there are fewer than keff heads)
         const int nh = G * r;
         u64 M = 0;
         u64* heads = s.tk;  // tk is free until the survivors are sorted
@@ -1790,7 +1821,8 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
   if (RB < 1) return fail(VS_EINVAL, "vs_sample_batch: a row does not fit on the device at once");
   if (ws_bytes < (size_t)RB * ROW_WS) return fail(VS_EWORKSPACE, "vs_sample_batch: workspace too small");
   int kcap = 1;  // list capacity per workgroup: a power of two <= KEYS_CAP / G
-  while (kcap * 2 <= KEYS_CAP / G && kcap * 2 <= KCAP) kcap *= 2;
+  while (kcap * 2 <= KEYS_CAP / G && kcap * 2 <= 1024) kcap *= 2;
+  const int kmax = kcap < KCAP ? kcap : KCAP;
   int bits = 0;
   while ((1ll << bits) < (long long)V) ++bits;
   SampleArgs a;
@@ -1804,6 +1836,7 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
   a.has_hist = has_hist;
   a.lds_ch = lds_ch;
   a.kcap = kcap;
+  a.kmax = kmax;
   a.spin_limit = 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.params = params;
