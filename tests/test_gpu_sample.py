@@ -48,6 +48,63 @@ def test_random_mix(dev, V, seed):
     run(dev, x, ps, rng.random(B), hists, label=f"mix V{V} s{seed}")
 
 
+@pytest.mark.parametrize("k", [50, 256])
+def test_topk_concentrated_lists(dev, k):
+    """The row's largest logits all sit in one workgroup's chunk: that list alone holds the top k, so the merge keeps
+    many survivors (and for k=256 takes its radix-select path)."""
+    rng = np.random.default_rng(41 + k)
+    B, V = 16, 163840
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    x[:, :600] += 20.0 + rng.random((B, 600)).astype(np.float32)
+    x[1::2, V - 700:] += 19.0  # odd rows: a second dense block at the far end
+    ps = [Sampling(temperature=1.0, top_k=k, top_p=float(rng.choice([1.0, 0.9]))) for _ in range(B)]
+    run(dev, x, ps, rng.random(B), label=f"concentrated k{k}")
+
+
+@pytest.mark.parametrize("nb,rest", [(60, -100.0), (1500, -100.0), (600, 0.0)])
+@pytest.mark.parametrize("t", [0.7, 1.3, 0.31])
+def test_exp40_filter_boundary(dev, nb, rest, t):
+    """Whole-vocabulary rows (V > 4096, no top-k): many logits sit within a few ulps of the cut
+    x / t >= max / t - 40 (sampler.py:137-139), so the kept set must be decided exactly as float32 division does."""
+    V = 20000
+    B = 4
+    x = np.full((B, V), rest, np.float32)
+    rng = np.random.default_rng(int(nb + 10 * t))
+    if rest == 0.0:
+        x += rng.standard_normal((B, V)).astype(np.float32)
+    m = np.float32(10.0)
+    cut = np.float32(m / np.float32(t) - np.float32(40.0)) * np.float32(t)
+    for b in range(B):
+        x[b, 7 + b] = m
+        pos = rng.choice(np.arange(20, V), size=nb, replace=False)
+        steps = np.arange(nb) - nb // 2
+        x[b, pos] = (cut.view(np.int32) + np.sign(cut) * steps).astype(np.int32).view(np.float32)
+    ps = [Sampling(temperature=t, top_k=0, top_p=1.0) for _ in range(B)]
+    out, refs, _ = run(dev, x, ps, rng.random(B), label=f"exp40 nb{nb} t{t}")
+    for r in refs:
+        assert r.keep > 1
+
+
+def test_exp40_near_misses_in_many_lanes(dev):
+    """Hundreds of logits a few ulps below the exp(-40) cut in one chunk (many lanes pass the coarse lane bound)
+    while only a few logits are kept: the small kept-set path must still gather every kept logit."""
+    V, B, t = 20000, 4, 0.7
+    x = np.full((B, V), -100.0, np.float32)
+    m = np.float32(10.0)
+    cut = np.float32(m / np.float32(t) - np.float32(40.0)) * np.float32(t)
+    ci = cut.view(np.int32)
+    rng = np.random.default_rng(5)
+    for b in range(B):
+        x[b, 3] = m
+        below = (ci + np.sign(cut) * -rng.integers(1, 6, size=400)).astype(np.int32).view(np.float32)
+        x[b, 20:420] = below
+        x[b, 500 + 37 * np.arange(30)] = (ci + np.sign(cut) * rng.integers(0, 5, size=30)).astype(np.int32).view(np.float32)
+    ps = [Sampling(temperature=t, top_k=0, top_p=float(p)) for p in (1.0, 0.9, 1.0, 0.5)]
+    out, refs, _ = run(dev, x, ps, rng.random(B), label="exp40 near misses")
+    assert refs[0].keep == 31 and refs[2].keep == 31
+    assert all(int(f) & OUT_GATHER for f in out.flags.cpu().numpy())  # the small kept-set path
+
+
 def test_bf16_rows(dev):
     rng = np.random.default_rng(7)
     B, V = 6, 30000

@@ -12,15 +12,39 @@
 // Phase timestamps for development builds (-DVS_TRACE): workgroup 0-thread writes the 100 MHz wall clock into
 // trace[blockIdx.x * 32 + id]. Compiled out of the shipped library.
 #ifdef VS_TRACE
-#define VS_TR(A, id)                                                                           \
-  do {                                                                                         \
-    if ((A).trace && threadIdx.x == 0) (A).trace[(size_t)blockIdx.x * 32 + (id)] = wall_clock64(); \
+// Phase stamps go to LDS (a global store per stamp would make the stamping wave wait on store completion at
+// every vmcnt wait) and are written out once at the end of the workgroup.
+#define VS_TR_DECL(A)                                   \
+  __shared__ unsigned long long vs_tr_lds[32];          \
+  if (threadIdx.x < 32) vs_tr_lds[threadIdx.x] = 0;     \
+  __syncthreads()
+#define VS_TR(A, id)                                                 \
+  do {                                                               \
+    if ((A).trace && threadIdx.x == 0) vs_tr_lds[id] = wall_clock64(); \
   } while (0)
-#define VS_TRC(A, id)                                                                          \
-  do {                                                                                         \
-    if ((A).trace && threadIdx.x == 0) (A).trace[(size_t)blockIdx.x * 32 + (id)] = clock64();   \
+#define VS_TRV(A, id, val)                                  \
+  do {                                                      \
+    if ((A).trace && threadIdx.x == 0) vs_tr_lds[id] = (val); \
+  } while (0)
+#define VS_TRC(A, id)                                           \
+  do {                                                          \
+    if ((A).trace && threadIdx.x == 0) vs_tr_lds[id] = clock64(); \
+  } while (0)
+#define VS_TR_FLUSH(A)                                                                             \
+  do {                                                                                             \
+    if ((A).trace && threadIdx.x == 0)                                                             \
+      for (int i_ = 0; i_ < 32; ++i_) (A).trace[(size_t)blockIdx.x * 32 + i_] = vs_tr_lds[i_];     \
   } while (0)
 #else
+#define VS_TR_DECL(A) \
+  do {                \
+  } while (0)
+#define VS_TRV(A, id, val) \
+  do {                     \
+  } while (0)
+#define VS_TR_FLUSH(A) \
+  do {                 \
+  } while (0)
 #define VS_TRC(A, id) \
   do {                \
   } while (0)
@@ -193,6 +217,17 @@ __device__ __forceinline__ int wave_append(bool pred, C* counter) {
   if (lane_id() == leader) base = (int)atomicAdd(counter, (C)__popcll(m));
   base = __builtin_amdgcn_readlane(base, leader);
   return pred ? base + below : -1;
+}
+
+// Reserve n consecutive slots of *counter for this lane (one atomic per wave): returns the lane's first slot.
+template <typename C>
+__device__ __forceinline__ int wave_alloc(int n, C* counter) {
+  const int incl = wave_scan(n);
+  const int total = __builtin_amdgcn_readlane(incl, WAVE - 1);
+  int base = 0;
+  if (lane_id() == 0 && total) base = (int)atomicAdd(counter, (C)total);
+  base = __builtin_amdgcn_readlane(base, 0);
+  return base + incl - n;
 }
 
 // Block-wide reductions for a block of NT threads; `red` is LDS scratch of >= NT/64 elements of T.

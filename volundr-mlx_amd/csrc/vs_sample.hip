@@ -475,6 +475,40 @@ __device__ __forceinline__ void block_rank_sort(const u64* in, int n, u64* out, 
   __syncthreads();
 }
 
+__device__ __forceinline__ int pow2_ceil(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// Descending order by rank: out[#{j : in[j] > in[i]}] = in[i] for ranks below kout (distinct keys get distinct
+// ranks). T lanes of one wave share each key's comparisons, T = the largest power of two <= 64 with T * n <= SNT.
+// The caller has synchronised after writing `in`; ends with a barrier.
+__device__ __forceinline__ void rank_sort(const u64* in, int n, u64* out, int kout) {
+  if (n > SNT / 2) {
+    block_rank_sort(in, n, out, kout);
+    return;
+  }
+  int T = 64;
+  while (T > 2 && T * n > SNT) T >>= 1;
+  const int t = threadIdx.x;
+  const int i = t / T, sub = t & (T - 1);
+  u64 ki = 0;
+  int r = 0;
+  if (i < n) {
+    ki = in[i];
+    for (int j = sub; j < n; j += T) r += in[j] > ki ? 1 : 0;
+  }
+  r += lane_xor<1>(r);
+  if (T > 2) r += lane_xor<2>(r);
+  if (T > 4) r += lane_xor<4>(r);
+  if (T > 8) r += lane_xor<8>(r);
+  if (T > 16) r += lane_xor<16>(r);
+  if (T > 32) r += lane_xor<32>(r);
+  if (sub == 0 && i < n && r < kout) out[r] = ki;
+  __syncthreads();
+}
+
 // Sort 64*E keys held by one wave descending (lane L holds positions L + 64*i in e[i]); the bitonic network is
 // fully unrolled: partners at distance < 64 are exchanged across lanes (DPP / permlane), the others in-lane.
 template <int E>
@@ -544,40 +578,47 @@ __device__ __forceinline__ void small_sort(const u64* in, int n, u64* out, int k
   __syncthreads();
 }
 
-// Lower bound for the k-th largest logit of the workgroup, from the lane maxima (ord32 values): each wave extracts
-// its q = ceil(k/8) largest lane maxima; all extracted lanes hold a value >= the smallest wave's q-th value, and they
-// are >= k lanes when the waves together extracted k. Returns 0 (no bound) otherwise. Ties between lanes only make
-// the bound looser (a lane is extracted once per round).
-__device__ __forceinline__ uint32_t lane_max_bound(uint32_t tmax, int k, const Smem& s) {
+// Lower bound for the k-th largest logit of the workgroup, from the lane maxima (ord32 values, 0 for a lane with no
+// finite logit): each wave finds its q-th largest lane maximum, q = min(ceil(k/8), its non-zero lanes), by a
+// most-significant-bit-first radix select on ballots. Those q lanes of every wave hold values >= the smallest wave's
+// result, so when the waves' q add up to >= k the workgroup has >= k logits >= L. L = 0 otherwise (no bound).
+// nlanes = lanes holding a finite logit.
+struct LaneBound {
+  uint32_t L;
+  int nlanes;
+};
+__device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const Smem& s) {
   const int q = (k + SNW - 1) / SNW;
-  uint32_t cur = tmax, wb = 0;
-  int got = 0;
-  for (int i = 0; i < q; ++i) {
-    const uint32_t m = wave_max(cur);
-    if (m == 0) break;
-    wb = m;
-    // retire exactly one lane holding m (the lowest such lane)
-    const unsigned long long hb = __ballot(cur == m);
-    if (lane_id() == __ffsll((long long)hb) - 1) cur = 0;
-    ++got;
+  const int nz = __popcll(__ballot(tmax != 0));
+  const int got = nz < q ? nz : q;
+  uint32_t wb = 0;
+  if (got > 0) {
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = wb | (1u << b);
+      if (__popcll(__ballot(tmax >= c)) >= got) wb = c;
+    }
   }
   const int w = threadIdx.x / WAVE;
   uint32_t* wbs = (uint32_t*)(s.misc + 180);
-  __syncthreads();
   if (lane_id() == 0) {
     wbs[w] = wb;
     s.redi[w] = got;
+    s.redi[SNW + w] = nz;
   }
   __syncthreads();
+  LaneBound r;
   uint32_t L = ~0u;
-  int tot = 0;
+  int tot = 0, nl = 0;
 #pragma unroll
   for (int i = 0; i < SNW; ++i) {
     tot += s.redi[i];
+    nl += s.redi[SNW + i];
     if (s.redi[i] > 0) L = wbs[i] < L ? wbs[i] : L;
   }
   __syncthreads();
-  return tot >= k ? L : 0u;
+  r.L = tot >= k ? L : 0u;
+  r.nlanes = nl;
+  return r;
 }
 
 // One LDS exchange for the per-workgroup statistics: a sum, two 32-bit maxima and a 64-bit maximum.
@@ -657,37 +698,77 @@ struct DTraits<VS_F16> {
   __device__ static float cv(LT v) { return f16_to_f32(v); }
 };
 
-// Count the history tokens that fall in [lo, hi) into cnt[tok - lo] (the counts Sampler.accept keeps,
-// sampler.py:77-78). Four 16-byte loads per lane are in flight per iteration.
-__device__ __forceinline__ void count_history(const int32_t* h, int64_t b, int64_t e, int lo, int hi, uint32_t* cnt) {
+// ---------------------------------------------------------------------------------------------------------------
+// History counts (the counts Sampler.accept keeps, sampler.py:77-78) for the tokens in [lo, hi): cnt[tok - lo] += 1
+// for every occurrence, and the in-range positions are recorded in `list` (up to lcap of them; *nlist counts all)
+// so the penalties can visit only those. The history is read as 16-byte vectors, HB per lane per batch; the first
+// batch is loaded by hist_prefetch before the logits arrive.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int HB = 2;
+struct HistWin {
+  int64_t b, e, a, nv;  // [b, e): the ids; a: first 16-byte aligned position; nv: whole vectors from a
+};
+__device__ __forceinline__ HistWin hist_window(int64_t b, int64_t e) {
+  HistWin w;
+  w.b = b;
+  w.e = e;
+  w.a = (b + 3) & ~(int64_t)3;
+  if (w.a > e) w.a = e;
+  w.nv = (e - w.a) >> 2;
+  return w;
+}
+__device__ __forceinline__ void hist_load(const int32_t* h, const HistWin& w, int64_t v0, int4 (&r)[HB]) {
+  const int4* hv = (const int4*)(h + w.a);
+#pragma unroll
+  for (int u = 0; u < HB; ++u) {
+    const int64_t vi = v0 + (int64_t)u * SNT;
+    r[u] = vi < w.nv ? hv[vi] : make_int4(-1, -1, -1, -1);
+  }
+}
+// Count n ids per lane (all lanes of the block call this together).
+template <int N>
+__device__ __forceinline__ void hist_take(const int32_t (&tk)[N], int lo, int hi, uint32_t* cnt, uint32_t* list,
+                                          int lcap, int* nlist) {
+  int c = 0;
+#pragma unroll
+  for (int q = 0; q < N; ++q) c += (tk[q] >= lo && tk[q] < hi) ? 1 : 0;
+  int p = wave_alloc(c, nlist);
+  if (c) {
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+      if (tk[q] >= lo && tk[q] < hi) {
+        atomicAdd(&cnt[tk[q] - lo], 1u);
+        if (p < lcap) list[p] = (uint32_t)(tk[q] - lo);
+        ++p;
+      }
+  }
+}
+__device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, const int4 (&pre)[HB], int lo, int hi,
+                                           uint32_t* cnt, uint32_t* list, int lcap, int* nlist) {
   const int t = threadIdx.x;
-  int64_t a = (b + 3) & ~(int64_t)3;  // first 16-byte aligned position
-  if (a > e) a = e;
-  for (int64_t i = b + t; i < a; i += SNT) {
-    const int32_t tok = h[i];
-    if (tok >= lo && tok < hi) atomicAdd(&cnt[tok - lo], 1u);
+  {  // the unaligned head (< 4 ids) and tail (< 4 ids), one id per lane
+    const int nh = (int)(w.a - w.b);
+    const int64_t tb = w.a + w.nv * 4;
+    const int nt = (int)(w.e - tb);
+    int32_t one[1] = {-1};
+    if (t < nh) one[0] = h[w.b + t];
+    else if (t - nh < nt) one[0] = h[tb + (t - nh)];
+    hist_take(one, lo, hi, cnt, list, lcap, nlist);
   }
-  const int64_t nv = (e - a) >> 2;  // whole int4 vectors
-  const int4* hv = (const int4*)(h + a);
-  constexpr int U = 4;
-  for (int64_t v0 = t; v0 < nv; v0 += (int64_t)SNT * U) {
-    int4 r[U];
+  int4 r[HB];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t vi = v0 + (int64_t)u * SNT;
-      r[u] = vi < nv ? hv[vi] : make_int4(-1, -1, -1, -1);
+  for (int u = 0; u < HB; ++u) r[u] = pre[u];
+  for (int64_t v0 = 0; v0 < w.nv; v0 += (int64_t)SNT * HB) {
+    int32_t tk[4 * HB];
+#pragma unroll
+    for (int u = 0; u < HB; ++u) {
+      tk[4 * u] = r[u].x;
+      tk[4 * u + 1] = r[u].y;
+      tk[4 * u + 2] = r[u].z;
+      tk[4 * u + 3] = r[u].w;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int32_t tk[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (tk[q] >= lo && tk[q] < hi) atomicAdd(&cnt[tk[q] - lo], 1u);
-    }
-  }
-  for (int64_t i = a + nv * 4 + t; i < e; i += SNT) {
-    const int32_t tok = h[i];
-    if (tok >= lo && tok < hi) atomicAdd(&cnt[tok - lo], 1u);
+    if (v0 + (int64_t)SNT * HB < w.nv) hist_load(h, w, v0 + (int64_t)SNT * HB + t, r);  // next batch in flight
+    hist_take(tk, lo, hi, cnt, list, lcap, nlist);
   }
 }
 
@@ -720,6 +801,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int lo = g * A.CH;
   const int hi = min(V, lo + A.CH);
   const int NV = A.NV;
+  VS_TR_DECL(A);
   VS_TR(A, 0);
   VS_TRC(A, 30);
 
@@ -741,6 +823,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
     }
   }
+  // ---- while the logits are in flight: the first batch of the history ids, and the count array cleared ----
+  const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
+  const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
+  HistWin hw;
+  int4 hpre[HB];
+  if (has_pen) {
+    hw = hist_window(P.hist_begin, P.hist_end);
+    hist_load(A.hist, hw, t, hpre);
+    for (int i = t; i < A.CH / 4; i += SNT) ((uint4*)s.cnt)[i] = make_uint4(0, 0, 0, 0);
+    if (t == 0) s.misc[13] = 0;
+  }
 #define ELEM(j, q) (lo + ((j) * SNT + t) * VEC + (q))
 #define FOR_ELEMS(BODY)                                 \
   _Pragma("unroll") for (int j = 0; j < NVMAX; ++j) {   \
@@ -761,10 +854,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   // the code small enough for the instruction cache and frees the chunk's VGPRs ----
   FOR_ELEMS({ s.xv[e - lo] = x; })
   __syncthreads();
+  VS_TR(A, 23);
 
   // ---- logit edits and penalties (sampler.py:104-126), float32 throughout, applied sparsely ----
-  const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
-  const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
   if (P.bias_end > P.bias_begin) {  // :104-109; ids sorted, equal ids in application order: one lane per run
     for (int p = P.bias_begin + t; p < P.bias_end; p += SNT) {
       const int id = A.bias_ids[p];
@@ -784,19 +876,31 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     __syncthreads();
   }
   if (has_pen) {  // :113-122 over the multiset of generated tokens
-    for (int i = t; i < A.CH; i += SNT) s.cnt[i] = 0;
+    uint32_t* list = s.cnt + A.CH;  // in-range history positions, after the counts in the key area
+    const int lcap = (int)(keys_bytes(A.lds_ch) / 4) - A.CH;
+    hist_count(A.hist, hw, hpre, lo, hi, s.cnt, list, lcap, &s.misc[13]);
     __syncthreads();
-    count_history(A.hist, P.hist_begin, P.hist_end, lo, hi, s.cnt);
-    __syncthreads();
-    for (int i = t; i < hi - lo; i += SNT) {
-      const uint32_t c = s.cnt[i];
-      if (c) {
-        float y = s.xv[i];
-        if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
-        const float cf = (float)c;
-        const float fc = fpen * cf;
-        const float sub = fc + ppen;
-        s.xv[i] = y - sub;
+    VS_TR(A, 24);
+    auto penalise = [&](int i, uint32_t c) {
+      float y = s.xv[i];
+      if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
+      const float cf = (float)c;
+      const float fc = fpen * cf;
+      const float sub = fc + ppen;
+      s.xv[i] = y - sub;
+    };
+    const int nl = s.misc[13];
+    if (nl <= lcap) {
+      // each distinct token once: the first lane to swap its count out applies the penalty
+      for (int j = t; j < nl; j += SNT) {
+        const int i = (int)list[j];
+        const uint32_t c = atomicExch(&s.cnt[i], 0u);
+        if (c) penalise(i, c);
+      }
+    } else {
+      for (int i = t; i < hi - lo; i += SNT) {
+        const uint32_t c = s.cnt[i];
+        if (c) penalise(i, c);
       }
     }
     __syncthreads();
@@ -902,84 +1006,71 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
       cleanup(0);
     }
+    VS_TR_FLUSH(A);
     return;
   }
 
   if (cls == CLS_TOPK) {
     // ---- local top-k by key among finite logits (sampler.py:133-136, ties toward the lower index) ----
     const int k = top_k;
+    if (t == 0) {
+      s.misc[4] = 0;
+      s.misc[14] = 0;
+    }
     float fmx = -__builtin_inff();
-    int nf = 0;
+    bool hasf = false;
     FOR_XV({
       if (is_finite(x)) {
-        ++nf;
+        hasf = true;
         fmx = fmaxf(fmx, x);
       }
     })
-    const uint32_t tmax = nf ? ord32(fmx) : 0u;
-    const int nb_fin = block_sum<SNT>(nf, s.redi);
-    const u64 am = nb_fin ? (u64)0 : chunk_amkey();
+    const uint32_t tmax = hasf ? ord32(fmx) : 0u;  // ord32 of a finite value is never 0
     VS_TR(A, 10);
-    int kc = 0;
-    if (nb_fin > 0) {
-      // Only logits >= L can be in the local top-k; typically a small multiple of k survive.
-      const uint32_t L = nb_fin > k ? lane_max_bound(tmax, k, s) : 0u;
-      VS_TR(A, 11);
-      if (t == 0) s.misc[4] = 0;
-      __syncthreads();
+    // Only logits >= L can be in the local top-k (L = 0: no bound, every finite logit is a candidate).
+    const LaneBound lb = lane_max_bound(tmax, k, s);
+    VS_TR(A, 11);
+    const u64 am = lb.nlanes ? (u64)0 : chunk_amkey();
+    int kc = 0, C = 0;
+    const int kr = pow2_ceil(k);  // list length read by the merge (<= kcap)
+    if (lb.nlanes > 0) {
+      const uint32_t L = lb.L;
       const float Lf = L ? inv_ord32(L) : -__builtin_inff();  // x >= Lf  <=>  ord32(x) >= L for finite x
-      FOR_XV({
-        const bool c = x >= Lf && is_finite(x);
+      // Every candidate sits in a lane whose maximum reaches the bound (about k lanes): the block scans those
+      // lanes' elements together instead of every lane scanning its own.
+      int* ql = (int*)(s.tk + KCAP);  // <= SNT lane ids
+      const bool qual = tmax != 0 && tmax >= L;
+      const int pq = wave_append(qual, &s.misc[14]);
+      if (qual) ql[pq] = t;
+      __syncthreads();
+      const int nq = s.misc[14];
+      const int nel = hi - lo;
+      const int M = (nel + SNT - 1) / SNT;  // elements per lane
+      const int total = nq * M;
+      for (int base = 0; base < total; base += SNT) {
+        const int w = base + t;
+        bool c = false;
+        float x = 0.0f;
+        int i = 0;
+        if (w < total) {
+          const int q = w / M, m = w - q * M;
+          i = ql[q] + SNT * m;
+          if (i < nel) {
+            x = s.xv[i];
+            c = x >= Lf && is_finite(x);
+          }
+        }
         const int p = wave_append(c, &s.misc[4]);
-        if (c && p < KEYS_CAP) s.keys[p] = key64(x, (uint32_t)e);
-      })
+        if (c && p < KEYS_CAP) s.keys[p] = key64(x, (uint32_t)(lo + i));
+      }
       __syncthreads();
-      const int C = s.misc[4];
-      __syncthreads();
+      C = s.misc[4];
       VS_TR(A, 12);
-#ifdef VS_TRACE
-      if (t == 0 && A.trace) A.trace[(size_t)blockIdx.x * 32 + 19] = C;
-#endif
-      // The list this workgroup publishes: its rloc = ceil(k / G) largest keys first (the heads, descending), then
-      // the other candidates in any order, zero padded to kcap. The merge bounds the global keff-th key with the
-      // heads and only sorts the survivors.
-      const int rloc = (k + G - 1) / G;
-      if (C <= 256 && C <= A.kcap && rloc <= 8) {
-        kc = C;
-        u64* hl = s.tk;         // heads
-        u64* rest = s.tk + 16;  // the other candidates (<= 256)
-        if (t < WAVE) {
-          u64 ev[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ev[i] = t + 64 * i < C ? s.keys[t + 64 * i] : (u64)0;
-          for (int h = 0; h < rloc; ++h) {
-            u64 lm = ev[0];
-#pragma unroll
-            for (int i = 1; i < 4; ++i) lm = ev[i] > lm ? ev[i] : lm;
-            const u64 m = wave_max(lm);
-            if (t == 0) hl[h] = m;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (ev[i] == m) ev[i] = 0;  // keys are unique: one slot retires (none when m == 0)
-          }
-          if (t == 0) s.misc[5] = 0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int p = wave_append(ev[i] != 0, &s.misc[5]);
-            if (ev[i] != 0) rest[p] = ev[i];
-          }
-        }
-        __syncthreads();
-        const int R = s.misc[5];
-        for (int i = t; i < A.kcap; i += SNT) {
-          const u64 v = i < rloc ? hl[i] : (i - rloc < R ? rest[i - rloc] : (u64)0);
-          st_dev(&cand[g * A.kcap + i], v);
-        }
-      } else if (C <= RANK_MAX) {
-        kc = C < k ? C : k;
-        small_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
+      VS_TRV(A, 19, C);
+      kc = C < k ? C : k;
+      if (C <= RANK_MAX) {
+        rank_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
       } else {
-        kc = C < k ? C : k;
         // Many keys above the bound (few lanes hold finite values): radix select, then rank the k survivors.
         u64 T;
         if (C <= KEYS_CAP) {
@@ -1021,52 +1112,64 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           }
         })
         __syncthreads();
-        small_sort(sel, kc, s.tk, kc);
+        rank_sort(sel, kc, s.tk, kc);
       }
-      if (!(C <= 256 && C <= A.kcap && rloc <= 8))  // the sorted local top-k serves as the list
-        for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
       VS_TR(A, 13);
     }
-    if (nb_fin == 0)  // an empty list is all zeros too
-      for (int i = t; i < A.kcap; i += SNT) st_dev(&cand[g * A.kcap + i], (u64)0);
-    put_part(am, (uint32_t)nb_fin, (uint32_t)kc, 0.0f, 0.0);
+    // the published list: the sorted local top-kc, zero padded to kr
+    for (int i = t; i < kr; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
+    // C counts every finite logit when there is no bound, and is >= k otherwise: the row's sum decides
+    // min(k, finite count) exactly.
+    put_part(am, (uint32_t)C, (uint32_t)kc, 0.0f, 0.0);
     VS_TR(A, 3);
     VS_TRC(A, 31);
     if (arrive_done()) {
       VS_TR(A, 4);
-      // ---- merge (last workgroup of the row). Each workgroup's list is its sorted local top-min(k, n_g), zero
-      // padded. Any keff list entries bound the global keff-th key from below, so with r = ceil(keff / lists) heads
-      // per list, M = the keff-th largest of those heads leaves about keff survivors. ----
-      const int tot = G * A.kcap;
-      {  // partials and all lists in one round trip
-        u64 r8[KEYS_CAP / SNT];
+      // ---- merge (last workgroup of the row). Each list holds its workgroup's sorted local top-kc. With r =
+      // ceil(k / G) heads per list, M = the keff-th largest head bounds the global keff-th key from below; the
+      // survivors >= M (at most keff + G * r) contain the global top-keff. ----
+      const int lkr = __builtin_ctz((unsigned)kr);
+      const int tot = G * kr;  // <= G * kcap <= KEYS_CAP
+      const int r = (k + G - 1) / G;
+      const int nh = G * r;
+      u64* heads = s.keys;           // nh <= k + G <= 320
+      u64* hs = s.keys + 512;        // keff largest heads
+      u64* sel = (u64*)s.xv;         // survivors (the chunk is no longer needed)
+      u64 r8[KEYS_CAP / SNT];        // all lists, loaded in one round trip
 #pragma unroll
-        for (int u = 0; u < KEYS_CAP / SNT; ++u) {
-          const int idx = t + u * SNT;
-          r8[u] = idx < tot ? ld_dev(&cand[idx]) : (u64)0;
-        }
-        int nf2 = 0;
-        u64 k2 = 0;
-        if (t < G) {
-          nf2 = (int)ld_dev(&parts[t].nfin);
-          k2 = ld_dev(&parts[t].amkey);
-        }
+      for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+        const int idx = t + u * SNT;
+        r8[u] = idx < tot ? ld_dev(&cand[(idx >> lkr) * A.kcap + (idx & (kr - 1))]) : (u64)0;
+      }
+      int nf2 = 0, nz2 = 0;
+      u64 k2 = 0;
+      if (t < G) {
+        nf2 = (int)ld_dev(&parts[t].nfin);
+        k2 = ld_dev(&parts[t].amkey);
+        const int kcg = (int)ld_dev(&parts[t].kc);
+        nz2 = kcg < r ? kcg : r;
+      }
 #pragma unroll
-        for (int u = 0; u < KEYS_CAP / SNT; ++u)
-          if (t + u * SNT < tot) s.keys[t + u * SNT] = r8[u];
-        if (t < WAVE) {
-          const int nn = wave_sum(nf2);
-          const u64 bam2 = wave_max(k2);
-          if (t == 0) {
-            s.misc[7] = nn;
-            s.red64[0] = bam2;
-            s.misc[9] = 0;
-          }
+      for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+        const int idx = t + u * SNT;
+        const int j = idx & (kr - 1);
+        if (idx < tot && j < r) heads[(idx >> lkr) * r + j] = r8[u];
+      }
+      if (t < WAVE) {
+        const int nn = wave_sum(nf2);
+        const int nz = wave_sum(nz2);
+        const u64 bam2 = wave_max(k2);
+        if (t == 0) {
+          s.misc[7] = nn;
+          s.misc[12] = nz;
+          s.red64[0] = bam2;
+          s.misc[9] = 0;
         }
       }
       __syncthreads();
       VS_TR(A, 14);
       const int n = s.misc[7];
+      const int nzh = s.misc[12];  // non-zero heads
       const u64 bam = s.red64[0];
       int keff = k < n ? k : n;  // sampler.py:133-134
       if (keff < 1) keff = 1;
@@ -1078,54 +1181,47 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         f.keep = 0;
         write_out(A, row, f);
       } else {
-        // every list starts with its r largest keys in descending order
-        const int r = (k + G - 1) / G;
-        VS_TR(A, 15);
-        // M = the keff-th largest list head (0 when there are fewer than keff heads)
-        const int nh = G * r;
-        u64 M = 0;
-        u64* heads = s.tk;  // tk is free until the survivors are sorted
-        for (int idx = t; idx < nh; idx += SNT) heads[idx] = s.keys[(idx / r) * A.kcap + idx % r];
-        __syncthreads();
-        VS_TR(A, 16);
-        if (nh <= 256) {
-          u64* hs = s.tk + KCAP;
-          small_sort(heads, nh, hs, nh < KCAP ? nh : KCAP);
-          M = keff - 1 < nh ? hs[keff - 1] : (u64)0;  // a zero here means fewer than keff heads: no bound
-        } else {
-          int avail = 0;
-          for (int idx = t; idx < nh; idx += SNT) avail += heads[idx] != 0;
-          avail = block_sum<SNT>(avail, s.redi);
-          if (avail >= keff) M = block_kth(s, heads, nh, keff);
+        u64 M = 0;  // 0: fewer than keff heads, no bound
+        if (nzh >= keff) {
+          rank_sort(heads, nh, hs, keff);
+          M = hs[keff - 1];
         }
-        __syncthreads();
         VS_TR(A, 17);
-        u64* sel = s.tk + KCAP;
-        for (int idx = t; idx < tot; idx += SNT) {
-          const u64 kk = s.keys[idx];
-          const bool c = kk != 0 && kk >= M;
-          const int p = wave_append(c, &s.misc[9]);
-          if (c && p < KCAP) sel[p] = kk;
+        {  // survivors, straight from the registers
+          int cnt = 0;
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u) cnt += (r8[u] != 0 && r8[u] >= M) ? 1 : 0;
+          int p = wave_alloc(cnt, &s.misc[9]);
+          if (cnt) {
+#pragma unroll
+            for (int u = 0; u < KEYS_CAP / SNT; ++u)
+              if (r8[u] != 0 && r8[u] >= M) {
+                if (p < RANK_MAX) sel[p] = r8[u];
+                ++p;
+              }
+          }
         }
         __syncthreads();
         const int Cm = s.misc[9];
-        __syncthreads();
         VS_TR(A, 5);
-        if (Cm <= KCAP) {
-          small_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
+        if (Cm <= RANK_MAX) {
+          rank_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
         } else {
-          const u64 T = block_kth(s, s.keys, tot, keff);
+          // many survivors (a few lists hold most of the top keys): radix-select the keff-th key of all lists
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u)
+            if (t + u * SNT < tot) s.keys[t + u * SNT] = r8[u];
           if (t == 0) s.misc[10] = 0;
           __syncthreads();
-          for (int i = t; i < tot; i += SNT) {
-            const u64 kk = s.keys[i];
-            if (kk >= T) {
+          const u64 T = block_kth(s, s.keys, tot, keff);
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u)
+            if (r8[u] != 0 && r8[u] >= T) {
               const int p = atomicAdd(&s.misc[10], 1);
-              if (p < KCAP) sel[p] = kk;
+              if (p < RANK_MAX) sel[p] = r8[u];
             }
-          }
           __syncthreads();
-          small_sort(sel, keff, s.tk, keff);
+          rank_sort(sel, keff, s.tk, keff);
         }
         VS_TR(A, 6);
         const Final f = wave_sample(s, s.tk, keff, P);
@@ -1134,22 +1230,25 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
       cleanup(0);
     }
+    VS_TR_FLUSH(A);
     return;
   }
 
   // =================================== FULL class ===================================
   // ---- row statistics: finite count, largest and smallest finite logit, np.argmax key ----
+  uint32_t lane_mk = 0;  // ord32 of this lane's largest finite logit, 0 when it has none
   {
     int nf = 0;
-    uint32_t mk = 0, nmk = 0;
+    float fmx = -__builtin_inff(), fmn = __builtin_inff();
     FOR_XV({
       if (is_finite(x)) {
         ++nf;
-        const uint32_t o = ord32(x);
-        mk = o > mk ? o : mk;
-        nmk = ~o > nmk ? ~o : nmk;
+        fmx = x > fmx ? x : fmx;
+        fmn = x < fmn ? x : fmn;
       }
     })
+    const uint32_t mk = nf ? ord32(fmx) : 0u, nmk = nf ? ~ord32(fmn) : 0u;
+    lane_mk = mk;
     VS_TR(A, 20);
     Stats st = block_stats(nf, mk, nmk, 0, s);
     if (st.n == 0) st.am = chunk_amkey();
@@ -1239,8 +1338,56 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         thr = xs0 - 40.0f;
         xs_lo = xs_lo > thr ? xs_lo : thr;
       }
+      // Every kept logit is >= xlb (mode 1: its key's value part; mode 2: a bound on x with fl(x/t) >= thr, from a
+      // float64 product with a relative slack far above the rounding of the division). Lanes whose maximum is below
+      // xlb hold no kept logit; when few lanes qualify, the passes below visit only their elements.
+      // In mode 2 every x >= xhi passes as well, so the division only decides the few logits in [xlb, xhi).
+      float xlb = -__builtin_inff(), xhi = __builtin_inff();
+      if (mode == 1) {
+        xlb = inv_ord32((uint32_t)(Tk >> 32));
+      } else if (mode == 2 && tt > 0.0f) {
+        const double d = (double)thr * (double)tt;  // exact: a product of two floats
+        const double slack = fabs(d) * 0x1p-20 + (double)tt * 1e-44 + 1e-38;
+        const float f = (float)(d - slack), f2 = (float)(d + slack);
+        if (is_finite(f)) xlb = inv_ord32(ord32(f) - 1u);  // one more step covers the conversion's rounding
+        if (is_finite(f2)) xhi = inv_ord32(ord32(f2) + 1u);
+      }
+      int* ql = (int*)(s.tk + KCAP);  // qualifying lanes (<= SNT)
+      int nq = 0;
       if (ok) {
-#define IS_CAND(x, kk) (is_finite(x) && (mode == 0 || (mode == 1 ? (kk) >= Tk : ((x) / tt) >= thr)))
+        if (t == 0) s.misc[14] = 0;
+        __syncthreads();
+        const bool qual = lane_mk != 0 && lane_mk >= ord32(xlb);
+        const int pq = wave_append(qual, &s.misc[14]);
+        if (qual) ql[pq] = t;
+        __syncthreads();
+        nq = s.misc[14];
+      }
+      // BODY runs for the chunk's logits x >= xlb (e = vocabulary index); it must not use wave-wide operations.
+#define FOR_KEPT(BODY)                                                        \
+  if (nq * 4 <= SNT) {                                                        \
+    const int nel_ = hi - lo, M_ = (nel_ + SNT - 1) / SNT, tot_ = nq * M_;    \
+    for (int w_ = t; w_ < tot_; w_ += SNT) {                                  \
+      const int q_ = w_ / M_, m_ = w_ - q_ * M_;                              \
+      const int i_ = ql[q_] + SNT * m_;                                       \
+      if (i_ < nel_) {                                                        \
+        const int e = lo + i_;                                                \
+        const float x = s.xv[i_];                                             \
+        if (x >= xlb) {                                                       \
+          BODY                                                                \
+        }                                                                     \
+      }                                                                       \
+    }                                                                         \
+  } else {                                                                    \
+    FOR_XV({                                                                  \
+      if (x >= xlb) {                                                         \
+        BODY                                                                  \
+      }                                                                       \
+    })                                                                        \
+  }
+      if (ok) {
+#define IS_CAND(x, kk) \
+  (is_finite(x) && (mode == 0 || (mode == 1 ? (kk) >= Tk : ((x) >= xhi || ((x) / tt) >= thr))))
         const double scale = A.fix_scale;
         // Value bins: u = xs0 - x/t >= 0 is monotone in the logit, so the fine index f = u * 65536 / span splits
         // the kept set, in sampler.py:140 order, into contiguous ranges. Bins are stored by digit 255 - c (coarse
@@ -1261,38 +1408,56 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         };
         VS_TR(A, 4);
         // ---- round 1: coarse mass histogram of the kept set + its size + a bounded gather ----
+        if (t == 0) s.misc[15] = 0;
         hist_clear(s);
-        int cb = 0;
-        FOR_XV({
+        // With few qualifying lanes the kept logits are also listed in LDS for the gather below; otherwise the
+        // kept count exceeds GSMALL and no gather happens.
+        const bool few = nq * 4 <= SNT;
+        int cbr = 0;
+        FOR_KEPT({
           const u64 kk = key64(x, (uint32_t)e);
           if (IS_CAND(x, kk)) {
-            ++cb;
+            ++cbr;
             u64 fx;
             const double pr = mass(x, &fx);
             const int c = fine_of(x) >> 8;
             atomicAdd(&s.hc[c], 1u);
             atomicAdd(&s.hfix[c], fx);
             unsafeAtomicAdd(&s.hf64[c], pr);
+            if (few) {
+              const int p = atomicAdd(&s.misc[15], 1);
+              if (p < KEYS_CAP) s.keys[p] = kk;
+            }
           }
         })
-        cb = block_sum<SNT>(cb, s.redi);
+        int cb;
+        if (few) {
+          __syncthreads();
+          cb = s.misc[15];
+        } else {
+          cb = block_sum<SNT>(cbr, s.redi);
+        }
+        VS_TR(A, 25);
         // each workgroup gathers into its own region of GB keys when its kept count fits
         const int GB = 1 << (31 - __builtin_clz(GCAP / G));  // power of two <= GCAP / G
         if (t == 0) {
           atomicAdd(&ctl->gcount, (uint32_t)cb);
           atomicMax(&ctl->gmax, (uint32_t)cb);
           st_dev(&parts[g].kc, (uint32_t)cb);
-          s.misc[10] = 0;
         }
-        __syncthreads();
         if (cb <= GB && cb <= GSMALL) {
-          FOR_XV({
-            const u64 kk = key64(x, (uint32_t)e);
-            const bool c = IS_CAND(x, kk);
-            const int p = wave_append(c, &s.misc[10]);
-            if (c) st_dev(&gather[g * GB + p], kk);
-          })
+          if (!few) {  // rare: many lane maxima near the bound but few kept logits
+            if (t == 0) s.misc[15] = 0;
+            __syncthreads();
+            FOR_KEPT({
+              const u64 kk = key64(x, (uint32_t)e);
+              if (IS_CAND(x, kk)) s.keys[atomicAdd(&s.misc[15], 1)] = kk;
+            })
+            __syncthreads();
+          }
+          for (int i = t; i < cb; i += SNT) st_dev(&gather[g * GB + i], s.keys[i]);
         }
+        VS_TR(A, 26);
         HistSlot* h1 = hslots + slot++;
         if (t < NBIN && s.hc[t]) {
           atomicAdd(&h1->cnt[t], s.hc[t]);
@@ -1335,7 +1500,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 }
               }
               __syncthreads();
+              VS_TR(A, 27);
               small_sort(s.keys, total, s.tk, total);
+              VS_TR(A, 28);
               fin = wave_sample(s, s.tk, total, P);
               fin.flags |= VS_OUT_GATHER;
             }
@@ -1382,7 +1549,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 s.ff64[i] = 0.0;
               }
               __syncthreads();
-              FOR_XV({
+              FOR_KEPT({
                 const u64 kk = key64(x, (uint32_t)e);
                 if (IS_CAND(x, kk)) {
                   const int id = fine_of(x);
@@ -1472,19 +1639,29 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 if (!located || gcount > GCAP2) {
                   radix = true;
                 } else {
-                  FOR_XV({
+                  if (t == 0) s.misc[16] = 0;
+                  __syncthreads();
+                  FOR_KEPT({
                     const u64 kk = key64(x, (uint32_t)e);
-                    bool c = false;
                     if (IS_CAND(x, kk)) {
                       const int id = fine_of(x);
-                      c = (has_tp && id == lp_.id) || (id <= la.id && id >= lb.id);
+                      if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id)) {
+                        const int p = atomicAdd(&s.misc[16], 1);
+                        if (p < KEYS_CAP) s.keys[p] = kk;
+                      }
                     }
-                    const int p = wave_append(c, &ctl->g2count);
-                    if (c) st_dev(&gather[p], kk);
                   })
+                  __syncthreads();
+                  const int nloc = s.misc[16];  // <= gcount <= GCAP2
+                  if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
+                  __syncthreads();
+                  for (int i = t; i < nloc; i += SNT) st_dev(&gather[s.misc[17] + i], s.keys[i]);
                   g0_writes = false;
                   VS_TR(A, 6);
-                  if (!arrive_done()) return;  // the last workgroup of the row resolves the exact positions
+                  if (!arrive_done()) {
+                    VS_TR_FLUSH(A);
+                    return;
+                  }  // the last workgroup of the row resolves the exact positions
                   VS_TR(A, 7);
                   // ---- final: exact key order inside the located fine bins ----
                   const int m = (int)ld_relaxed(&ctl->g2count);
@@ -1575,6 +1752,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   VS_TR(A, 8);
                   write_out(A, row, fin);
                   cleanup(slot);
+                  VS_TR_FLUSH(A);
                   return;
                 }
               }
@@ -1583,7 +1761,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (ok && radix) {
             // ---- radix fallback: cooperative mass-weighted radix select on the 64-bit keys ----
             hist_clear(s);
-            FOR_XV({
+            FOR_KEPT({
               const u64 kk = key64(x, (uint32_t)e);
               if (IS_CAND(x, kk)) {
                 u64 fx;
@@ -1641,7 +1819,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   prefix = (prefix << 8) | (u64)o.digit;
                   shift -= 8;
                   hist_clear(s);
-                  FOR_XV({
+                  FOR_KEPT({
                     const u64 kk = key64(x, (uint32_t)e);
                     if (IS_CAND(x, kk) && (kk >> (shift + 8)) == prefix) {
                       u64 fx;
@@ -1685,7 +1863,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 int mc = 0;
                 u64 mfx = 0;
                 double mff = 0.0;
-                FOR_XV({
+                FOR_KEPT({
                   const u64 kk = key64(x, (uint32_t)e);
                   if (IS_CAND(x, kk)) {
                     u64 fx;
@@ -1741,6 +1919,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           }
         }
 #undef IS_CAND
+#undef FOR_KEPT
       }
     }
   }
@@ -1753,6 +1932,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     const bool err = ld_relaxed(&ctl->err) != 0;
     cleanup(err ? MAX_ROUNDS : slot);
   }
+  VS_TR_FLUSH(A);
 #undef FOR_ELEMS
 #undef ELEM
 }

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   const int lo = g * A.CH;
   const int hi = min(A.vv, lo + A.CH);
   const char* rowp = (const char*)A.logits + (int64_t)row * A.ld * (DT == VS_F32 ? 4 : 2);
+  VS_TR_DECL(A);
   VS_TR(A, 0);
 
   // One streaming pass: first-max key (np.argmax order, NaN first), running finite maximum m and
@@ -152,7 +153,10 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     st_dev(&pp->se, sb);
   }
   VS_TR(A, 2);
-  if (block_arrive(&rowdone[row], &flag) != (uint32_t)(G - 1)) return;
+  if (block_arrive(&rowdone[row], &flag) != (uint32_t)(G - 1)) {
+    VS_TR_FLUSH(A);
+    return;
+  }
   VS_TR(A, 3);
   // last workgroup of this row: merge the G partials in one wave (G <= 64)
   if (t < WAVE) {
@@ -198,6 +202,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       }
     }
   }
+  VS_TR_FLUSH(A);
 }
 
 }  // namespace vs
