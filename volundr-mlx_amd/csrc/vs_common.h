@@ -14,10 +14,14 @@
 #ifdef VS_TRACE
 // Phase stamps go to LDS (a global store per stamp would make the stamping wave wait on store completion at
 // every vmcnt wait) and are written out once at the end of the workgroup.
-#define VS_TR_DECL(A)                                   \
-  __shared__ unsigned long long vs_tr_lds[32];          \
-  if (threadIdx.x < 32) vs_tr_lds[threadIdx.x] = 0;     \
+__shared__ unsigned long long vs_tr_lds[64];
+#define VS_TR_DECL(A)                               \
+  if (threadIdx.x < 64) vs_tr_lds[threadIdx.x] = 0; \
   __syncthreads()
+#define VS_TRX(id)                                            \
+  do {                                                        \
+    if (threadIdx.x == 0) vs_tr_lds[id] = wall_clock64();     \
+  } while (0)
 #define VS_TR(A, id)                                                 \
   do {                                                               \
     if ((A).trace && threadIdx.x == 0) vs_tr_lds[id] = wall_clock64(); \
@@ -33,9 +37,12 @@
 #define VS_TR_FLUSH(A)                                                                             \
   do {                                                                                             \
     if ((A).trace && threadIdx.x == 0)                                                             \
-      for (int i_ = 0; i_ < 32; ++i_) (A).trace[(size_t)blockIdx.x * 32 + i_] = vs_tr_lds[i_];     \
+      for (int i_ = 0; i_ < 64; ++i_) (A).trace[(size_t)blockIdx.x * 64 + i_] = vs_tr_lds[i_];     \
   } while (0)
 #else
+#define VS_TRX(id) \
+  do {             \
+  } while (0)
 #define VS_TR_DECL(A) \
   do {                \
   } while (0)

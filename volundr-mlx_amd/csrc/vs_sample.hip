@@ -462,18 +462,6 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
   return f;
 }
 
-// Rank by counting (unique keys): out[r] = the key of rank r (0 = largest) for r < kout. O(n) per element; used
-// only for small n, where it is cheaper on one CU than a sorting network. `in` and `out` must not overlap.
-__device__ __forceinline__ void block_rank_sort(const u64* in, int n, u64* out, int kout) {
-  for (int i = threadIdx.x; i < n; i += SNT) {
-    const u64 ki = in[i];
-    int r = 0, j = 0;
-    for (; j + 4 <= n; j += 4) r += (in[j] > ki) + (in[j + 1] > ki) + (in[j + 2] > ki) + (in[j + 3] > ki);
-    for (; j < n; ++j) r += in[j] > ki;
-    if (r < kout) out[r] = ki;
-  }
-  __syncthreads();
-}
 
 __device__ __forceinline__ int pow2_ceil(int n) {
   int p = 1;
@@ -482,32 +470,41 @@ __device__ __forceinline__ int pow2_ceil(int n) {
 }
 
 // Descending order by rank: out[#{j : in[j] > in[i]}] = in[i] for ranks below kout (distinct keys get distinct
-// ranks). T lanes of one wave share each key's comparisons, T = the largest power of two <= 64 with T * n <= SNT.
+// ranks). T lanes of one wave share each key's comparisons (T = the largest power of two <= 64 with T * n <= SNT,
+// at least 1); each lane reads 8 keys per step, so 8 LDS reads are in flight instead of one per loop trip.
 // The caller has synchronised after writing `in`; ends with a barrier.
 __device__ __forceinline__ void rank_sort(const u64* in, int n, u64* out, int kout) {
-  if (n > SNT / 2) {
-    block_rank_sort(in, n, out, kout);
-    return;
-  }
   int T = 64;
-  while (T > 2 && T * n > SNT) T >>= 1;
+  while (T > 1 && T * n > SNT) T >>= 1;
   const int t = threadIdx.x;
-  const int i = t / T, sub = t & (T - 1);
-  u64 ki = 0;
-  int r = 0;
-  if (i < n) {
-    ki = in[i];
-    for (int j = sub; j < n; j += T) r += in[j] > ki ? 1 : 0;
+  const int sub = t & (T - 1);
+  const int step = 8 * T;
+  for (int i0 = 0; i0 < n; i0 += SNT / T) {  // uniform trip count
+    const int i = i0 + t / T;
+    const u64 ki = in[i < n ? i : 0];
+    int r = 0;
+    for (int j0 = 0; j0 < n; j0 += step) {  // uniform trip count
+      u64 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u * T + sub;
+        v[u] = in[j < n ? j : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) r += (j0 + u * T + sub < n && v[u] > ki) ? 1 : 0;
+    }
+    if (T > 1) r += lane_xor<1>(r);
+    if (T > 2) r += lane_xor<2>(r);
+    if (T > 4) r += lane_xor<4>(r);
+    if (T > 8) r += lane_xor<8>(r);
+    if (T > 16) r += lane_xor<16>(r);
+    if (T > 32) r += lane_xor<32>(r);
+    if (sub == 0 && i < n && r < kout) out[r] = ki;
   }
-  r += lane_xor<1>(r);
-  if (T > 2) r += lane_xor<2>(r);
-  if (T > 4) r += lane_xor<4>(r);
-  if (T > 8) r += lane_xor<8>(r);
-  if (T > 16) r += lane_xor<16>(r);
-  if (T > 32) r += lane_xor<32>(r);
-  if (sub == 0 && i < n && r < kout) out[r] = ki;
   __syncthreads();
 }
+
+constexpr int SEGW = KEYS_CAP / SNW;  // per-wave candidate segment
 
 // Sort 64*E keys held by one wave descending (lane L holds positions L + 64*i in e[i]); the bitonic network is
 // fully unrolled: partners at distance < 64 are exchanged across lanes (DPP / permlane), the others in-lane.
@@ -548,7 +545,7 @@ __device__ __forceinline__ void wave_sort_desc(u64 (&e)[E]) {
 // barrier); larger n falls back to rank counting over the whole workgroup.
 __device__ __forceinline__ void small_sort(const u64* in, int n, u64* out, int kout) {
   if (n > 256) {
-    block_rank_sort(in, n, out, kout);
+    rank_sort(in, n, out, kout);
     return;
   }
   if (threadIdx.x < WAVE) {
@@ -700,11 +697,10 @@ struct DTraits<VS_F16> {
 
 // ---------------------------------------------------------------------------------------------------------------
 // History counts (the counts Sampler.accept keeps, sampler.py:77-78) for the tokens in [lo, hi): cnt[tok - lo] += 1
-// for every occurrence, and the in-range positions are recorded in `list` (up to lcap of them; *nlist counts all)
-// so the penalties can visit only those. The history is read as 16-byte vectors, HB per lane per batch; the first
-// batch is loaded by hist_prefetch before the logits arrive.
+// for every occurrence. The history is read as 16-byte vectors, HB per lane per batch, HD batches in flight; the
+// first HD batches are loaded before the logits arrive.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int HB = 2;
+constexpr int HB = 2;  // 16-byte vectors per lane per batch (8 ids)
 struct HistWin {
   int64_t b, e, a, nv;  // [b, e): the ids; a: first 16-byte aligned position; nv: whole vectors from a
 };
@@ -717,34 +713,30 @@ __device__ __forceinline__ HistWin hist_window(int64_t b, int64_t e) {
   w.nv = (e - w.a) >> 2;
   return w;
 }
+// Loads vectors v0 + u * SNT (u < HB), the index clamped to the last vector so that every load is unconditional
+// (conditional loads make the compiler wait for all loads at the loop latch); the consumer masks by position.
+// Requires w.nv >= 1.
 __device__ __forceinline__ void hist_load(const int32_t* h, const HistWin& w, int64_t v0, int4 (&r)[HB]) {
   const int4* hv = (const int4*)(h + w.a);
 #pragma unroll
   for (int u = 0; u < HB; ++u) {
     const int64_t vi = v0 + (int64_t)u * SNT;
-    r[u] = vi < w.nv ? hv[vi] : make_int4(-1, -1, -1, -1);
+    r[u] = hv[vi < w.nv ? vi : w.nv - 1];
   }
 }
-// Count n ids per lane (all lanes of the block call this together).
+// Count N ids per lane into cnt[id - lo] for the ids in [lo, hi).
 template <int N>
-__device__ __forceinline__ void hist_take(const int32_t (&tk)[N], int lo, int hi, uint32_t* cnt, uint32_t* list,
-                                          int lcap, int* nlist) {
-  int c = 0;
+__device__ __forceinline__ void hist_add_ids(const int32_t (&tk)[N], int lo, int hi, uint32_t* cnt) {
 #pragma unroll
-  for (int q = 0; q < N; ++q) c += (tk[q] >= lo && tk[q] < hi) ? 1 : 0;
-  int p = wave_alloc(c, nlist);
-  if (c) {
-#pragma unroll
-    for (int q = 0; q < N; ++q)
-      if (tk[q] >= lo && tk[q] < hi) {
-        atomicAdd(&cnt[tk[q] - lo], 1u);
-        if (p < lcap) list[p] = (uint32_t)(tk[q] - lo);
-        ++p;
-      }
+  for (int q = 0; q < N; ++q) {
+    const uint32_t o = (uint32_t)(tk[q] - lo);
+    if (o < (uint32_t)(hi - lo)) atomicAdd(&cnt[o], 1u);
   }
 }
-__device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, const int4 (&pre)[HB], int lo, int hi,
-                                           uint32_t* cnt, uint32_t* list, int lcap, int* nlist) {
+constexpr int HD = 4;  // batches in flight
+// cnt[tok - lo] += 1 for every history id in [lo, hi).
+__device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, int4 (&r)[HD][HB], int lo, int hi,
+                                           uint32_t* cnt) {
   const int t = threadIdx.x;
   {  // the unaligned head (< 4 ids) and tail (< 4 ids), one id per lane
     const int nh = (int)(w.a - w.b);
@@ -753,22 +745,34 @@ __device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, c
     int32_t one[1] = {-1};
     if (t < nh) one[0] = h[w.b + t];
     else if (t - nh < nt) one[0] = h[tb + (t - nh)];
-    hist_take(one, lo, hi, cnt, list, lcap, nlist);
+    hist_add_ids(one, lo, hi, cnt);
   }
-  int4 r[HB];
+  constexpr int64_t BATCH = (int64_t)SNT * HB;  // vectors per batch
+  // One group = HD batches: the first was loaded ahead of time; every later group issues all its loads before
+  // counting (no registers carried across iterations, so the loads of a group are in flight together).
+  auto take = [&](int64_t v0, int4 (&r)[HD][HB]) {
 #pragma unroll
-  for (int u = 0; u < HB; ++u) r[u] = pre[u];
-  for (int64_t v0 = 0; v0 < w.nv; v0 += (int64_t)SNT * HB) {
-    int32_t tk[4 * HB];
+    for (int d = 0; d < HD; ++d) {
+      const int64_t vb = v0 + d * BATCH;
+      if (vb >= w.nv) break;  // uniform
+      int32_t tk[4 * HB];
 #pragma unroll
-    for (int u = 0; u < HB; ++u) {
-      tk[4 * u] = r[u].x;
-      tk[4 * u + 1] = r[u].y;
-      tk[4 * u + 2] = r[u].z;
-      tk[4 * u + 3] = r[u].w;
+      for (int u = 0; u < HB; ++u) {
+        const bool ok = vb + (int64_t)u * SNT + t < w.nv;
+        tk[4 * u] = ok ? r[d][u].x : -1;
+        tk[4 * u + 1] = ok ? r[d][u].y : -1;
+        tk[4 * u + 2] = ok ? r[d][u].z : -1;
+        tk[4 * u + 3] = ok ? r[d][u].w : -1;
+      }
+      hist_add_ids(tk, lo, hi, cnt);
     }
-    if (v0 + (int64_t)SNT * HB < w.nv) hist_load(h, w, v0 + (int64_t)SNT * HB + t, r);  // next batch in flight
-    hist_take(tk, lo, hi, cnt, list, lcap, nlist);
+  };
+  if (w.nv > 0) take(0, r);
+  for (int64_t v0 = BATCH * HD; v0 < w.nv; v0 += BATCH * HD) {
+    int4 q[HD][HB];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) hist_load(h, w, v0 + d * BATCH + t, q[d]);
+    take(v0, q);
   }
 }
 
@@ -803,7 +807,6 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int NV = A.NV;
   VS_TR_DECL(A);
   VS_TR(A, 0);
-  VS_TRC(A, 30);
 
   // ---- load the chunk into VGPRs (one HBM read) ----
   float v[EPT_MAX];
@@ -827,12 +830,14 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
   const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
   HistWin hw;
-  int4 hpre[HB];
+  int4 hpre[HD][HB];
   if (has_pen) {
     hw = hist_window(P.hist_begin, P.hist_end);
-    hist_load(A.hist, hw, t, hpre);
+    if (hw.nv > 0) {
+#pragma unroll
+      for (int d = 0; d < HD; ++d) hist_load(A.hist, hw, (int64_t)d * SNT * HB + t, hpre[d]);
+    }
     for (int i = t; i < A.CH / 4; i += SNT) ((uint4*)s.cnt)[i] = make_uint4(0, 0, 0, 0);
-    if (t == 0) s.misc[13] = 0;
   }
 #define ELEM(j, q) (lo + ((j) * SNT + t) * VEC + (q))
 #define FOR_ELEMS(BODY)                                 \
@@ -876,34 +881,46 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     __syncthreads();
   }
   if (has_pen) {  // :113-122 over the multiset of generated tokens
-    uint32_t* list = s.cnt + A.CH;  // in-range history positions, after the counts in the key area
-    const int lcap = (int)(keys_bytes(A.lds_ch) / 4) - A.CH;
-    hist_count(A.hist, hw, hpre, lo, hi, s.cnt, list, lcap, &s.misc[13]);
+    hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
     __syncthreads();
     VS_TR(A, 24);
     auto penalise = [&](int i, uint32_t c) {
       float y = s.xv[i];
-      if (rep != 1.0f) y = y > 0.0f ? y / rep : y * rep;
+      if (rep != 1.0f) {
+        const float dv = y / rep, ml = y * rep;  // both, then a select: no divergent branch
+        y = y > 0.0f ? dv : ml;
+      }
       const float cf = (float)c;
       const float fc = fpen * cf;
       const float sub = fc + ppen;
       s.xv[i] = y - sub;
     };
-    const int nl = s.misc[13];
-    if (nl <= lcap) {
-      // each distinct token once: the first lane to swap its count out applies the penalty
-      for (int j = t; j < nl; j += SNT) {
-        const int i = (int)list[j];
-        const uint32_t c = atomicExch(&s.cnt[i], 0u);
-        if (c) penalise(i, c);
-      }
-    } else {
-      for (int i = t; i < hi - lo; i += SNT) {
-        const uint32_t c = s.cnt[i];
-        if (c) penalise(i, c);
-      }
+    // Lane L of wave w owns positions w * R + 64 j + L of the counts. It marks its non-zero ones in a bit mask and
+    // visits only those: the loop runs as often as the busiest lane of the wave has distinct tokens, with no
+    // per-position branch (scalar branches and LDS writes dominate a per-position loop).
+    const int R = A.CH / SNW;  // a multiple of WAVE
+    const int w0 = (t / WAVE) * R;
+    const int L = lane_id();
+    constexpr int NJ = EPT_MAX * SNT / SNW / WAVE;  // the largest R / WAVE
+    static_assert(NJ <= 32, "one mask bit per owned position");
+    // Reads are unconditional (a uniform guard would become a scalar branch per read); past R they land in the
+    // next wave's counts or the unused rest of the key area (7 R + NJ * 64 < 16384 words) and are masked out.
+    uint32_t mask = 0;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      const uint32_t c = s.cnt[w0 + jj * WAVE + L];
+      mask |= (uint32_t)(c != 0 && jj * WAVE < R) << jj;
     }
+    VS_TRX(34);
+    while (mask) {
+      const int jj = __builtin_ctz(mask);
+      mask &= mask - 1;
+      const int i = w0 + jj * WAVE + L;
+      penalise(i, s.cnt[i]);
+    }
+    VS_TRX(35);
     __syncthreads();
+    VS_TRX(36);
   }
   if (P.stop_end > P.stop_begin) {  // :123-126
     for (int p = P.stop_begin + t; p < P.stop_end; p += SNT) {
@@ -1036,46 +1053,58 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     if (lb.nlanes > 0) {
       const uint32_t L = lb.L;
       const float Lf = L ? inv_ord32(L) : -__builtin_inff();  // x >= Lf  <=>  ord32(x) >= L for finite x
-      // Every candidate sits in a lane whose maximum reaches the bound (about k lanes): the block scans those
-      // lanes' elements together instead of every lane scanning its own.
-      int* ql = (int*)(s.tk + KCAP);  // <= SNT lane ids
+      // Every candidate sits in a lane whose maximum reaches the bound (about k lanes). Each wave scans its own
+      // qualifying lanes' elements with all its lanes (pair p -> lane q = p / M, element m = p % M) and appends
+      // the candidates to its own segment of the key area with ballots: no atomics, no block barrier.
+      const int wv = t / WAVE, Ln = lane_id();
       const bool qual = tmax != 0 && tmax >= L;
-      const int pq = wave_append(qual, &s.misc[14]);
-      if (qual) ql[pq] = t;
-      __syncthreads();
-      const int nq = s.misc[14];
+      const unsigned long long Q = __ballot(qual);
+      const int nqw = __popcll(Q);
+      int* qlw = (int*)(s.tk + KCAP) + wv * WAVE;  // this wave's qualifying lanes
+      if (qual) qlw[__builtin_amdgcn_mbcnt_hi((uint32_t)(Q >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)Q, 0u))] = Ln;
       const int nel = hi - lo;
       const int M = (nel + SNT - 1) / SNT;  // elements per lane
-      const int total = nq * M;
-      for (int base = 0; base < total; base += SNT) {
-        const int w = base + t;
-        bool c = false;
-        float x = 0.0f;
-        int i = 0;
-        if (w < total) {
-          const int q = w / M, m = w - q * M;
-          i = ql[q] + SNT * m;
-          if (i < nel) {
-            x = s.xv[i];
-            c = x >= Lf && is_finite(x);
-          }
-        }
-        const int p = wave_append(c, &s.misc[4]);
-        if (c && p < KEYS_CAP) s.keys[p] = key64(x, (uint32_t)(lo + i));
+      const float invM = 1.0f / (float)M;
+      const int totw = nqw * M;
+      u64* segw = s.keys + wv * SEGW;
+      int cw = 0;
+      for (int p0 = 0; p0 < totw; p0 += WAVE) {
+        const int pp = p0 + Ln;
+        int q = (int)((float)pp * invM);  // pp < 2^24: corrected to the exact quotient below
+        q -= q * M > pp;
+        q += (q + 1) * M <= pp;
+        const int m = pp - q * M;
+        const int ql = qlw[q < nqw ? q : nqw - 1];
+        const int i = wv * WAVE + ql + SNT * m;
+        const float x = s.xv[i < nel ? i : 0];
+        const bool c = pp < totw && i < nel && x >= Lf && is_finite(x);
+        const unsigned long long mc = __ballot(c);
+        const int pos = cw + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mc, 0u));
+        if (c && pos < SEGW) segw[pos] = key64(x, (uint32_t)(lo + i));
+        cw += __popcll(mc);
       }
+      int* segc = s.misc + 24;  // [SNW] candidates per wave
+      if (Ln == 0) segc[wv] = cw;
       __syncthreads();
-      C = s.misc[4];
+      C = 0;
+#pragma unroll
+      for (int v = 0; v < SNW; ++v) C += segc[v];
       VS_TR(A, 12);
       VS_TRV(A, 19, C);
       kc = C < k ? C : k;
       if (C <= RANK_MAX) {
-        rank_sort(s.keys, C, s.tk, kc);  // the local top-k, sorted descending
+        // the segments, made contiguous in the chunk area (no longer needed on this path), then ranked
+        u64* ck = (u64*)s.xv;
+        int off = 0;
+#pragma unroll
+        for (int v = 0; v < SNW; ++v) off += v < wv ? segc[v] : 0;
+        for (int j = Ln; j < cw; j += WAVE) ck[off + j] = segw[j];
+        __syncthreads();
+        rank_sort(ck, C, s.tk, kc);  // the local top-k, sorted descending
       } else {
         // Many keys above the bound (few lanes hold finite values): radix select, then rank the k survivors.
         u64 T;
-        if (C <= KEYS_CAP) {
-          T = block_kth(s, s.keys, C, k);
-        } else {
+        {
           u64 prefix = 0;
           int shift = 56, krem = k;
           for (;;) {
@@ -1122,7 +1151,6 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     // min(k, finite count) exactly.
     put_part(am, (uint32_t)C, (uint32_t)kc, 0.0f, 0.0);
     VS_TR(A, 3);
-    VS_TRC(A, 31);
     if (arrive_done()) {
       VS_TR(A, 4);
       // ---- merge (last workgroup of the row). Each list holds its workgroup's sorted local top-kc. With r =
@@ -1568,6 +1596,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 }
               })
               __syncthreads();
+              VS_TR(A, 15);
               HistSlot* h2 = hslots + slot;
               slot += ns;
               for (int i = t; i < ns * NBIN; i += SNT) {
@@ -1579,8 +1608,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   unsafeAtomicAdd(&hs->f64[b2], s.ff64[i]);
                 }
               }
+              VS_TR(A, 16);
               ++nbar;
               ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+              VS_TR(A, 18);
               if (ok) {
                 for (int i = t; i < ns * NBIN; i += SNT) {
                   const HistSlot* hs = h2 + i / NBIN;
