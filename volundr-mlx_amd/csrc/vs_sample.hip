@@ -336,14 +336,14 @@ struct Final {
   int32_t keep;
 };
 
-// sampler.py:141-156 on n <= 256 keys sorted descending in LDS (a[0] is the row maximum), in one wave: lane L
-// owns positions [L*E, L*E+E), so every sum and prefix is a lane-sequential loop plus one wave scan. The result is
-// broadcast to the whole workgroup.
-__device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n, const vs_row_params& P) {
-  constexpr int EM = 4;  // n <= 256
-  if (threadIdx.x < WAVE) {
+// sampler.py:141-156 on n <= 64 * EM keys sorted descending in LDS (a[0] is the row maximum), in one wave: lane
+// L owns positions [L*E, L*E+E), E = ceil(n / 64) <= EM, so every sum and prefix is a lane-sequential loop plus one
+// wave scan. Lane 0 leaves the result in LDS for wave_sample.
+template <int EM>  // n <= 64 * EM
+__device__ __forceinline__ void wave_sample_em(const Smem& s, const u64* a, int n, const vs_row_params& P) {
+  {
     const int L = threadIdx.x;
-    const int E = (n + WAVE - 1) / WAVE;
+    const int E = EM == 1 ? 1 : (n + WAVE - 1) / WAVE;
     const int i0 = L * E;
     const float tt = P.temperature;
     const float xs0 = key_value(a[0]) / tt;  // sampler.py:141 xs[0]
@@ -360,6 +360,7 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
       }
     }
     const double S = wave_sum(ls);  // :143
+    VS_TRX(40);
     double lp = 0.0;
 #pragma unroll
     for (int q = 0; q < EM; ++q) {
@@ -367,6 +368,7 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
       lp += pr[q];
     }
     const double base = wave_scan(lp) - lp;  // cumulative mass before this lane's first position
+    VS_TRX(41);
     int keep = n;
     uint32_t flags = 0;
     if (P.top_p < 1.0) {  // :145-148 first position with cumsum >= top_p
@@ -403,6 +405,7 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
       cnt = cnt > 1 ? cnt : 1;
       keep = keep < cnt ? keep : cnt;
     }
+    VS_TRX(42);
     double lz = 0.0;
 #pragma unroll
     for (int q = 0; q < EM; ++q)
@@ -443,6 +446,7 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
       hp = lane_bcast(pp, owner);
       hc = lane_bcast(cc, owner);
     }
+    VS_TRX(43);
     if (L == 0) {
       const double tol = 1e-6 * z;
       if (fabs(hc - uz) < tol || (j >= 1 && fabs(hc - hp - uz) < tol)) flags |= VS_OUT_DRAW_BOUNDARY;
@@ -451,6 +455,14 @@ __device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n,
       s.misc[3] = (int)flags;
       s.redf[0] = log(hp / z);
     }
+  }
+}
+// sampler.py:141-156 on n <= 256 keys sorted descending in LDS (see wave_sample_em); all threads call it.
+__device__ __forceinline__ Final wave_sample(const Smem& s, const u64* a, int n, const vs_row_params& P) {
+  if (threadIdx.x < WAVE) {
+    if (n <= WAVE) wave_sample_em<1>(s, a, n, P);
+    else if (n <= 2 * WAVE) wave_sample_em<2>(s, a, n, P);
+    else wave_sample_em<4>(s, a, n, P);
   }
   __syncthreads();
   Final f;
@@ -474,8 +486,10 @@ __device__ __forceinline__ int pow2_ceil(int n) {
 // at least 1); each lane reads 8 keys per step, so 8 LDS reads are in flight instead of one per loop trip.
 // The caller has synchronised after writing `in`; ends with a barrier.
 __device__ __forceinline__ void rank_sort(const u64* in, int n, u64* out, int kout) {
-  int T = 64;
-  while (T > 1 && T * n > SNT) T >>= 1;
+  // T = SNT / 2^ceil(log2 n), clamped to [1, 64]
+  const int lg = n > 1 ? 32 - __builtin_clz((unsigned)(n - 1)) : 0;
+  int T = lg >= 9 ? 1 : (SNT >> lg);
+  T = T > 64 ? 64 : T;
   const int t = threadIdx.x;
   const int sub = t & (T - 1);
   const int step = 8 * T;
@@ -595,6 +609,7 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
       if (__popcll(__ballot(tmax >= c)) >= got) wb = c;
     }
   }
+  VS_TRX(37);
   const int w = threadIdx.x / WAVE;
   uint32_t* wbs = (uint32_t*)(s.misc + 180);
   if (lane_id() == 0) {
@@ -603,14 +618,24 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
     s.redi[SNW + w] = nz;
   }
   __syncthreads();
+  VS_TRX(38);
   LaneBound r;
   uint32_t L = ~0u;
   int tot = 0, nl = 0;
+  int gw[SNW], nw[SNW];
+  uint32_t bw[SNW];
+#pragma unroll
+  for (int i = 0; i < SNW; ++i) {  // all reads first, then selects (a guarded read becomes a branch per wave)
+    gw[i] = s.redi[i];
+    nw[i] = s.redi[SNW + i];
+    bw[i] = wbs[i];
+  }
 #pragma unroll
   for (int i = 0; i < SNW; ++i) {
-    tot += s.redi[i];
-    nl += s.redi[SNW + i];
-    if (s.redi[i] > 0) L = wbs[i] < L ? wbs[i] : L;
+    tot += gw[i];
+    nl += nw[i];
+    const uint32_t b = gw[i] > 0 ? bw[i] : ~0u;
+    L = b < L ? b : L;
   }
   __syncthreads();
   r.L = tot >= k ? L : 0u;
