@@ -26,7 +26,7 @@ namespace vs {
 constexpr int SNT = 512;         // threads per workgroup
 constexpr int SNW = SNT / WAVE;  // waves per workgroup
 constexpr int NRED = 16;         // entries of each LDS reduction/broadcast array (>= SNW and >= 6)
-constexpr int NMISC = 192;       // LDS scalar slots
+static_assert(NRED >= SNW, "one reduction slot per wave");
 constexpr int EPT_MAX = 24;      // logits per lane in flight during the load
 constexpr int NBIN = 256;        // radix digit = 8 bits
 constexpr int MAX_ROUNDS = 32;   // histogram slots per row (8 count + 1 coarse + 4 fine + 1 + 7 + 7 radix rounds)
@@ -39,6 +39,16 @@ constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
 constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
+// LDS scalar slots (misc): 0-17 single counters and flags, then arrays
+constexpr int M_SEGC = 24;                         // [SNW] candidates per wave (TOPK)
+constexpr int M_CNTS = M_SEGC + SNW;               // [GMAX] kept count per workgroup (FULL, small kept set)
+constexpr int M_OFFS = M_CNTS + GMAX;              // [GMAX] their offsets
+constexpr int M_XCH = (M_OFFS + GMAX + 1) & ~1;    // 2 x u64 exchange slots (8-byte aligned)
+constexpr int M_STAT1 = M_XCH + 4;                 // [SNW] block_stats maxima
+constexpr int M_STAT2 = M_STAT1 + SNW;             // [SNW]
+constexpr int M_WB = M_STAT2 + SNW;                // [SNW] lane_max_bound per-wave bounds
+constexpr int M_NZ = M_WB + SNW;                   // [SNW] lane_max_bound lanes with a finite logit
+constexpr int NMISC = M_NZ + SNW;
 
 enum RowClass { CLS_GREEDY = 0, CLS_TOPK = 1, CLS_FULL = 2 };
 
@@ -611,11 +621,11 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
   }
   VS_TRX(37);
   const int w = threadIdx.x / WAVE;
-  uint32_t* wbs = (uint32_t*)(s.misc + 180);
+  uint32_t* wbs = (uint32_t*)(s.misc + M_WB);
   if (lane_id() == 0) {
     wbs[w] = wb;
     s.redi[w] = got;
-    s.redi[SNW + w] = nz;
+    s.misc[M_NZ + w] = nz;
   }
   __syncthreads();
   VS_TRX(38);
@@ -627,7 +637,7 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
 #pragma unroll
   for (int i = 0; i < SNW; ++i) {  // all reads first, then selects (a guarded read becomes a branch per wave)
     gw[i] = s.redi[i];
-    nw[i] = s.redi[SNW + i];
+    nw[i] = s.misc[M_NZ + i];
     bw[i] = wbs[i];
   }
 #pragma unroll
@@ -655,8 +665,8 @@ __device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, 
   mx2 = wave_max(mx2);
   am = wave_max(am);
   const int w = threadIdx.x / WAVE;
-  uint32_t* m1 = (uint32_t*)(s.misc + 164);
-  uint32_t* m2 = (uint32_t*)(s.misc + 172);
+  uint32_t* m1 = (uint32_t*)(s.misc + M_STAT1);
+  uint32_t* m2 = (uint32_t*)(s.misc + M_STAT2);
   __syncthreads();
   if (lane_id() == 0) {
     s.redi[w] = n;
@@ -1108,7 +1118,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (c && pos < SEGW) segw[pos] = key64(x, (uint32_t)(lo + i));
         cw += __popcll(mc);
       }
-      int* segc = s.misc + 24;  // [SNW] candidates per wave
+      int* segc = s.misc + M_SEGC;  // [SNW] candidates per wave
       if (Ln == 0) segc[wv] = cw;
       __syncthreads();
       C = 0;
@@ -1527,8 +1537,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (total <= GSMALL && gmax <= GB) {
             // ---- small kept set: one workgroup ranks it and finishes as for TOPK ----
             if (g == 0) {
-              int* offs = s.misc + 96;  // [G]
-              int* cnts = s.misc + 32;  // [G]
+              int* offs = s.misc + M_OFFS;  // [G]
+              int* cnts = s.misc + M_CNTS;  // [G]
               if (t < WAVE) {
                 const int c = t < G ? (int)ld_dev(&parts[t].kc) : 0;
                 const int incl = wave_scan(c);
@@ -1725,7 +1735,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   int* fi = (int*)(s.keys + GCAP2);
                   u64* fxs = s.keys + GCAP2 + GCAP2 / 2;
                   double* fds = (double*)(s.keys + 2 * GCAP2 + GCAP2 / 2);
-                  u64* xch = (u64*)(s.misc + 160);  // two 8-byte exchange slots
+                  u64* xch = (u64*)(s.misc + M_XCH);  // two 8-byte exchange slots
                   for (int i = t; i < m; i += SNT) {
                     const u64 kk = ld_dev(&gather[i]);
                     const float x = key_value(kk);
