@@ -970,6 +970,25 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     const float x = s.xv[i_];                                     \
     BODY                                                          \
   }
+  // The chunk in LDS, four positions per lane at a time: the four reads are issued before any of them is used, so
+  // branches in BODY do not serialise the LDS latency. Past the chunk's end a read lands on position 0 and is not
+  // processed.
+#define FOR_XV4(BODY)                                                                 \
+  for (int i0_ = t; i0_ < hi - lo; i0_ += 4 * SNT) {                                 \
+    float xq_[4];                                                                    \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                               \
+      const int iq_ = i0_ + u_ * SNT;                                                \
+      xq_[u_] = s.xv[iq_ < hi - lo ? iq_ : 0];                                       \
+    }                                                                                \
+    _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                               \
+      const int i_ = i0_ + u_ * SNT;                                                 \
+      if (i_ < hi - lo) {                                                            \
+        const int e = lo + i_;                                                       \
+        const float x = xq_[u_];                                                     \
+        BODY                                                                         \
+      }                                                                              \
+    }                                                                                \
+  }
   // np.argmax key of the chunk; only needed when a whole row has no finite logit (sampler.py:131-132)
   auto chunk_amkey = [&]() -> u64 {
     u64 am = 0;
@@ -1442,29 +1461,37 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }                                                                       \
     }                                                                         \
   } else {                                                                    \
-    FOR_XV({                                                                  \
+    FOR_XV4({                                                                 \
       if (x >= xlb) {                                                         \
         BODY                                                                  \
       }                                                                       \
     })                                                                        \
   }
       if (ok) {
-#define IS_CAND(x, kk) \
-  (is_finite(x) && (mode == 0 || (mode == 1 ? (kk) >= Tk : ((x) >= xhi || ((x) / tt) >= thr))))
+        // The per-element test of every pass: xs = x / t (float32, sampler.py:141, computed once and reused for
+        // the bin and the mass), the key, and whether x is in the kept set; mode is uniform, combined with bit
+        // operations so that no pass branches on it.
+        auto keep_xs = [&](float x, int e, u64& kk, float& xs) -> bool {
+          xs = x / tt;
+          kk = key64(x, (uint32_t)e);
+          const bool m1 = (mode == 1) & (kk >= Tk);
+          const bool m2 = (mode == 2) & ((x >= xhi) | (xs >= thr));
+          return is_finite(x) & ((mode == 0) | m1 | m2);
+        };
         const double scale = A.fix_scale;
         // Value bins: u = xs0 - x/t >= 0 is monotone in the logit, so the fine index f = u * 65536 / span splits
         // the kept set, in sampler.py:140 order, into contiguous ranges. Bins are stored by digit 255 - c (coarse
         // c = f >> 8) and 255 - (f & 255) (fine), so that the 256-bin scan walks them in descending-logit order.
         const float span = xs0 - xs_lo;
         const float fscale = span > 0.0f ? 65536.0f / span : 0.0f;
-        auto fine_of = [&](float x) -> int {
-          const float u = xs0 - x / tt;
+        auto fine_of = [&](float xs) -> int {  // xs = x / t
+          const float u = xs0 - xs;
           int f = (int)(u * fscale);
           f = f < 0 ? 0 : (f > 65535 ? 65535 : f);
           return 65535 - f;  // (coarse digit << 8) | fine digit
         };
-        auto mass = [&](float x, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
-          const float d = x / tt - xs0;
+        auto mass = [&](float xs, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
+          const float d = xs - xs0;
           const double pr = (double)expf(d);
           *fx = (u64)(pr * scale + 0.5);
           return pr;
@@ -1478,12 +1505,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         const bool few = nq * 4 <= SNT;
         int cbr = 0;
         FOR_KEPT({
-          const u64 kk = key64(x, (uint32_t)e);
-          if (IS_CAND(x, kk)) {
+          u64 kk;
+          float xs;
+          if (keep_xs(x, e, kk, xs)) {
             ++cbr;
             u64 fx;
-            const double pr = mass(x, &fx);
-            const int c = fine_of(x) >> 8;
+            const double pr = mass(xs, &fx);
+            const int c = fine_of(xs) >> 8;
             atomicAdd(&s.hc[c], 1u);
             atomicAdd(&s.hfix[c], fx);
             unsafeAtomicAdd(&s.hf64[c], pr);
@@ -1513,8 +1541,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             if (t == 0) s.misc[15] = 0;
             __syncthreads();
             FOR_KEPT({
-              const u64 kk = key64(x, (uint32_t)e);
-              if (IS_CAND(x, kk)) s.keys[atomicAdd(&s.misc[15], 1)] = kk;
+              u64 kk;
+              float xs;
+              if (keep_xs(x, e, kk, xs)) s.keys[atomicAdd(&s.misc[15], 1)] = kk;
             })
             __syncthreads();
           }
@@ -1581,6 +1610,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             __syncthreads();
             const u64 Sfix = block_sum<SNT>(t < NBIN ? s.hfix[t] : (u64)0, s.red64);
             const double Sf = block_sum<SNT>(t < NBIN ? s.hf64[t] : 0.0, s.redf);
+            VS_TRX(44);
             const bool has_tp = P.top_p < 1.0;
             const double tgt_p = P.top_p * (double)Sfix;
             ScanOut cpo;
@@ -1602,6 +1632,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               if (ns < NSET) set[ns] = d;
               ++ns;
             }
+            VS_TRX(45);
             if (ns > NSET) {
               radix = true;
             } else {
@@ -1612,17 +1643,19 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 s.ff64[i] = 0.0;
               }
               __syncthreads();
+              VS_TRX(46);
               FOR_KEPT({
-                const u64 kk = key64(x, (uint32_t)e);
-                if (IS_CAND(x, kk)) {
-                  const int id = fine_of(x);
+                u64 kk;
+                float xs;
+                if (keep_xs(x, e, kk, xs)) {
+                  const int id = fine_of(xs);
                   const int c = id >> 8;
                   int j = -1;
                   for (int q = 0; q < NSET; ++q)
                     if (q < ns && set[q] == c) j = q;
                   if (j >= 0) {
                     u64 fx;
-                    const double pr = mass(x, &fx);
+                    const double pr = mass(xs, &fx);
                     const int b2 = j * NBIN + (id & 0xFF);
                     atomicAdd(&s.fc[b2], 1u);
                     atomicAdd(&s.ffix[b2], fx);
@@ -1708,9 +1741,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   if (t == 0) s.misc[16] = 0;
                   __syncthreads();
                   FOR_KEPT({
-                    const u64 kk = key64(x, (uint32_t)e);
-                    if (IS_CAND(x, kk)) {
-                      const int id = fine_of(x);
+                    u64 kk;
+                    float xs;
+                    if (keep_xs(x, e, kk, xs)) {
+                      const int id = fine_of(xs);
                       if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id)) {
                         const int p = atomicAdd(&s.misc[16], 1);
                         if (p < KEYS_CAP) s.keys[p] = kk;
@@ -1740,8 +1774,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     const u64 kk = ld_dev(&gather[i]);
                     const float x = key_value(kk);
                     fk[i] = kk;
-                    fi[i] = fine_of(x);
-                    fds[i] = mass(x, &fxs[i]);
+                    const float xs = x / tt;
+                    fi[i] = fine_of(xs);
+                    fds[i] = mass(xs, &fxs[i]);
                   }
                   __syncthreads();
                   // First element (descending key) of fine bin `id` whose cumulative mass inside the bin reaches
@@ -1828,10 +1863,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             // ---- radix fallback: cooperative mass-weighted radix select on the 64-bit keys ----
             hist_clear(s);
             FOR_KEPT({
-              const u64 kk = key64(x, (uint32_t)e);
-              if (IS_CAND(x, kk)) {
+              u64 kk;
+              float xs;
+              if (keep_xs(x, e, kk, xs)) {
                 u64 fx;
-                const double pr = mass(x, &fx);
+                const double pr = mass(xs, &fx);
                 hist_add(s, kk, 56, fx, pr);
               }
             })
@@ -1886,10 +1922,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   shift -= 8;
                   hist_clear(s);
                   FOR_KEPT({
-                    const u64 kk = key64(x, (uint32_t)e);
-                    if (IS_CAND(x, kk) && (kk >> (shift + 8)) == prefix) {
+                    u64 kk;
+                    float xs;
+                    if (keep_xs(x, e, kk, xs) && (kk >> (shift + 8)) == prefix) {
                       u64 fx;
-                      const double pr = mass(x, &fx);
+                      const double pr = mass(xs, &fx);
                       hist_add(s, kk, shift, fx, pr);
                     }
                   })
@@ -1930,10 +1967,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 u64 mfx = 0;
                 double mff = 0.0;
                 FOR_KEPT({
-                  const u64 kk = key64(x, (uint32_t)e);
-                  if (IS_CAND(x, kk)) {
+                  u64 kk;
+                  float xs;
+                  if (keep_xs(x, e, kk, xs)) {
                     u64 fx;
-                    const double pr = mass(x, &fx);
+                    const double pr = mass(xs, &fx);
                     if (!(pr / Sf < pthr)) {
                       ++mc;
                       mfx += fx;
@@ -1984,12 +2022,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             }
           }
         }
-#undef IS_CAND
 #undef FOR_KEPT
       }
     }
   }
 #undef FOR_XV
+#undef FOR_XV4
   VS_TR(A, 9);
   // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree.
   if (g == 0 && g0_writes) write_out(A, row, fin);
