@@ -33,7 +33,8 @@ constexpr int MAX_ROUNDS = 32;   // histogram slots per row (8 count + 1 coarse 
 constexpr int GMAX = 64;         // workgroups per row
 constexpr int GCAP = 1024;       // gather area of the FULL path (keys)
 constexpr int GSMALL = 128;      // kept sets up to this size are finished in one workgroup
-constexpr int GCAP2 = 512;       // elements gathered from the located value bins
+constexpr int GCAP2 = 512;       // elements gathered from the located value bins (<= SNT: one per thread in the final scans)
+static_assert(GCAP2 <= SNT, "the final in-bin scans hold one gathered element per thread");
 constexpr int NSET = 4;          // coarse value bins refined in the second histogram round
 constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
@@ -1786,42 +1787,83 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     double f64_in, f64;
                   };
                   auto pick = [&](int id, double tgt) -> Pick {
-                    u64 best = 0, low = ~0ull;
-                    for (int i = t; i < m; i += SNT) {
-                      if (fi[i] != id) continue;
-                      const u64 ki = fk[i];
-                      u64 cum = 0;
-                      for (int j = 0; j < m; ++j)
-                        if (fi[j] == id && fk[j] > ki) cum += fxs[j];
-                      if ((double)(cum + fxs[i]) >= tgt) best = ki > best ? ki : best;
-                      low = ki < low ? ki : low;
-                    }
-                    best = block_max<SNT>(best, s.red64);
-                    low = block_min<SNT>(low, s.red64);
-                    const u64 win = best ? best : low;
-                    Pick pk;
-                    pk.key = win;
-                    u64 cnt = 0, fx = 0;
-                    double fd = 0.0;
-                    for (int i = t; i < m; i += SNT) {
-                      if (fi[i] == id && fk[i] > win) {
-                        ++cnt;
-                        fx += fxs[i];
-                        fd += fds[i];
-                      }
-                      if (fk[i] == win) {
-                        xch[0] = fxs[i];
-                        ((double*)xch)[1] = fds[i];
+                    // the bin's members, ranked by key (descending) with their masses, then prefix sums
+                    int* mem = (int*)(s.keys + 2048);      // [GCAP2] member positions
+                    u64* mkey = s.keys + 2304;             // [GCAP2] member keys (dense)
+                    u64* sk = mkey + GCAP2;                // [GCAP2] sorted keys
+                    u64* sf = sk + GCAP2;                  // [GCAP2] their fixed-point masses
+                    double* sd = (double*)(sf + GCAP2);    // [GCAP2] their float64 masses
+                    if (t == 0) s.misc[18] = 0;
+                    __syncthreads();
+                    for (int i0 = 0; i0 < m; i0 += SNT) {  // uniform trip count
+                      const int i = i0 + t;
+                      const bool in = i < m && fi[i] == id;
+                      const int p = wave_append(in, &s.misc[18]);
+                      if (in) {
+                        mem[p] = i;
+                        mkey[p] = fk[i];
                       }
                     }
                     __syncthreads();
-                    const u64 wfix = xch[0];
-                    const double wf = ((double*)xch)[1];
-                    pk.cnt_in = block_sum<SNT>(cnt, s.red64);
-                    pk.fix_in = block_sum<SNT>(fx, s.red64);
-                    pk.f64_in = block_sum<SNT>(fd, s.redf);
-                    pk.fix = wfix;
-                    pk.f64 = wf;
+                    const int nb = s.misc[18];
+                    {  // rank of each member among the members: T lanes per member, 8 reads in flight per lane
+                      const int lg = nb > 1 ? 32 - __builtin_clz((unsigned)(nb - 1)) : 0;
+                      int T = lg >= 9 ? 1 : (SNT >> lg);
+                      T = T > 64 ? 64 : T;
+                      const int sub = t & (T - 1);
+                      for (int q0 = 0; q0 < nb; q0 += SNT / T) {
+                        const int q = q0 + t / T;
+                        const u64 kq = mkey[q < nb ? q : 0];
+                        int r = 0;
+                        for (int j0 = 0; j0 < nb; j0 += 8 * T) {
+                          u64 v[8];
+#pragma unroll
+                          for (int u = 0; u < 8; ++u) {
+                            const int j = j0 + u * T + sub;
+                            v[u] = mkey[j < nb ? j : 0];
+                          }
+#pragma unroll
+                          for (int u = 0; u < 8; ++u) r += (j0 + u * T + sub < nb && v[u] > kq) ? 1 : 0;
+                        }
+                        if (T > 1) r += lane_xor<1>(r);
+                        if (T > 2) r += lane_xor<2>(r);
+                        if (T > 4) r += lane_xor<4>(r);
+                        if (T > 8) r += lane_xor<8>(r);
+                        if (T > 16) r += lane_xor<16>(r);
+                        if (T > 32) r += lane_xor<32>(r);
+                        if (sub == 0 && q < nb) {
+                          const int i = mem[q];
+                          sk[r] = kq;
+                          sf[r] = fxs[i];
+                          sd[r] = fds[i];
+                        }
+                      }
+                    }
+                    __syncthreads();
+                    // inclusive prefix sums in key order (nb <= GCAP2 <= SNT: one position per thread)
+                    const u64 myf = t < nb ? sf[t] : (u64)0;
+                    const double myd = t < nb ? sd[t] : 0.0;
+                    u64 totf;
+                    double totd;
+                    const u64 incf = block_scan<SNT>(myf, s.red64, &totf);
+                    const double incd = block_scan<SNT>(myd, s.redf, &totd);
+                    // the first position whose cumulative mass reaches tgt, else the last one
+                    const int cand = (t < nb && (double)incf >= tgt) ? t : 0x7FFFFFFF;
+                    int rs = block_min<SNT>(cand, s.redi);
+                    if (rs == 0x7FFFFFFF) rs = nb - 1;
+                    if (t == rs) {
+                      xch[0] = incf - myf;
+                      ((double*)xch)[1] = incd - myd;
+                    }
+                    __syncthreads();
+                    Pick pk;
+                    pk.key = nb ? sk[rs] : (u64)0;
+                    pk.cnt_in = (u64)(rs > 0 ? rs : 0);
+                    pk.fix_in = nb ? xch[0] : (u64)0;
+                    pk.f64_in = nb ? ((double*)xch)[1] : 0.0;
+                    pk.fix = nb ? sf[rs] : (u64)0;
+                    pk.f64 = nb ? sd[rs] : 0.0;
+                    __syncthreads();
                     return pk;
                   };
                   uint32_t flags = VS_OUT_COOP;
