@@ -294,6 +294,84 @@ __device__ __forceinline__ ScanOut hist_scan(const Smem& s, bool count_mode, dou
   return scan256(s, s.hc, s.hfix, s.hf64, s.hmk, count_mode, target);
 }
 
+// Prefix sums of a 256-bin histogram in scan order (digit 255 first, the order scan256 walks): pc[d] and pw[d] hold
+// the count and fixed-point sums over digits 255 .. d (inclusive), pf[d] the float64 sum over digits 255 .. d+1
+// (exclusive). Called by one whole wave.
+__device__ __forceinline__ void hist_prefix(const uint32_t* hc, const u64* hw, const double* hf, u64* pc, u64* pw,
+                                            double* pf) {
+  const int L = lane_id();
+  u64 c[4], w[4];
+  double f[4];
+  u64 lc = 0, lw = 0;
+  double lf = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = NBIN - 1 - (4 * L + i);
+    c[i] = hc[d];
+    w[i] = hw[d];
+    f[i] = hf[d];
+    lc += c[i];
+    lw += w[i];
+    lf += f[i];
+  }
+  u64 cc = wave_scan(lc) - lc, cw = wave_scan(lw) - lw;
+  double cf = wave_scan(lf) - lf;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = NBIN - 1 - (4 * L + i);
+    pf[d] = cf;
+    cc += c[i];
+    cw += w[i];
+    cf += f[i];
+    pc[d] = cc;
+    pw[d] = cw;
+  }
+}
+
+// scan256's answer from prefix arrays (hist_prefix): the first digit in scan order whose bin is non-empty and whose
+// inclusive weight reaches `target` (the last non-empty digit when none does, which only rounding can cause), with
+// the sums before it. Every wave computes it on its own, so no barrier is needed; the caller has synchronised after
+// hist_prefix.
+__device__ __forceinline__ ScanOut hist_find(const uint32_t* hc, const u64* hw, const double* hf, const u64* pc,
+                                             const u64* pw, const double* pf, double target) {
+  const int L = lane_id();
+  uint32_t c[4];
+  u64 w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = NBIN - 1 - (4 * L + i);
+    c[i] = hc[d];
+    w[i] = pw[d];
+  }
+  int hit = 4, last = -1;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    hit = (c[i] > 0 && (double)w[i] >= target) ? i : hit;
+    last = (last < 0 && c[i] > 0) ? i : last;
+  }
+  const unsigned long long hb = __ballot(hit < 4);
+  int lane_sel, i_sel;
+  if (hb) {
+    lane_sel = __ffsll((long long)hb) - 1;
+    i_sel = lane_bcast(hit, lane_sel);
+  } else {
+    const unsigned long long lb = __ballot(last >= 0);
+    lane_sel = lb ? 63 - __clzll((long long)lb) : 0;
+    i_sel = lb ? lane_bcast(last, lane_sel) : 0;
+  }
+  const int d = NBIN - 1 - (4 * lane_sel + i_sel);
+  ScanOut o;
+  o.digit = d;
+  o.cnt = hc[d];
+  o.fix = hw[d];
+  o.f64 = hf[d];
+  o.cnt_before = pc[d] - o.cnt;
+  o.fix_before = pw[d] - o.fix;
+  o.f64_before = pf[d];
+  o.mk = 0;
+  return o;
+}
+
 __device__ __forceinline__ void hist_clear(const Smem& s) {
   const int t = threadIdx.x;
   if (t < NBIN) {
@@ -530,6 +608,10 @@ __device__ __forceinline__ void rank_sort(const u64* in, int n, u64* out, int ko
 }
 
 constexpr int SEGW = KEYS_CAP / SNW;  // per-wave candidate segment
+// Key-area offset (u64 words) of the value-bin prefix sums: above what the final in-bin resolution uses
+// (4352 words), 3 * 256 coarse + 3 * NSET * 256 fine words.
+constexpr int PFX_OFF = 4352;
+static_assert(PFX_OFF + 3 * NBIN * (1 + NSET) <= KEYS_CAP, "prefix sums fit the key area");
 
 // Sort 64*E keys held by one wave descending (lane L holds positions L + 64*i in e[i]); the bitonic network is
 // fully unrolled: partners at distance < 64 are exchanged across lanes (DPP / permlane), the others in-lane.
@@ -1609,8 +1691,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               s.hf64[t] = ld_relaxed_f64(&h1->f64[t]);
             }
             __syncthreads();
-            const u64 Sfix = block_sum<SNT>(t < NBIN ? s.hfix[t] : (u64)0, s.red64);
-            const double Sf = block_sum<SNT>(t < NBIN ? s.hf64[t] : 0.0, s.redf);
+            // prefix sums of the coarse histogram (kept in the key area for every later lookup of this row)
+            u64* cpc = s.keys + PFX_OFF;
+            u64* cpw = cpc + NBIN;
+            double* cpf = (double*)(cpw + NBIN);
+            if (t < WAVE) hist_prefix(s.hc, s.hfix, s.hf64, cpc, cpw, cpf);
+            __syncthreads();
+            auto cfind = [&](double target) -> ScanOut {
+              return hist_find(s.hc, s.hfix, s.hf64, cpc, cpw, cpf, target);
+            };
+            const u64 Sfix = cpw[0];
+            const double Sf = cpf[0] + s.hf64[0];
             VS_TRX(44);
             const bool has_tp = P.top_p < 1.0;
             const double tgt_p = P.top_p * (double)Sfix;
@@ -1618,12 +1709,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             cpo.digit = -1;
             u64 zlo = Sfix, zhi = Sfix;
             if (has_tp) {
-              cpo = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, tgt_p);
+              cpo = cfind(tgt_p);
               zlo = cpo.fix_before;
               zhi = cpo.fix_before + cpo.fix;
             }
-            const int dlo = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, P.u * (double)zlo).digit;
-            const int dhi = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, P.u * (double)zhi).digit;
+            const int dlo = cfind(P.u * (double)zlo).digit;
+            const int dhi = cfind(P.u * (double)zhi).digit;
             // coarse digits to refine: the top-p bin and the draw's range dlo >= d >= dhi
             int set[NSET];
             int ns = 0;
@@ -1690,6 +1781,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   s.ff64[i] = ld_relaxed_f64(&hs->f64[b2]);
                 }
                 __syncthreads();
+                // prefix sums of each fine set, one wave per set
+                u64* fpc = cpc + 3 * NBIN;  // [NSET][NBIN] each
+                u64* fpw = fpc + NSET * NBIN;
+                double* fpf = (double*)(fpw + NSET * NBIN);
+                {
+                  const int j = t / WAVE;
+                  if (j < ns)
+                    hist_prefix(s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN, fpc + j * NBIN,
+                                fpw + j * NBIN, fpf + j * NBIN);
+                }
+                __syncthreads();
                 // Locate a target in the two-level histogram: the fine bin id and the sums before it.
                 struct Loc {
                   int id, set_j;
@@ -1698,7 +1800,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 };
                 auto locate = [&](double target) -> Loc {
                   Loc r;
-                  const ScanOut co = scan256(s, s.hc, s.hfix, s.hf64, nullptr, false, target);
+                  const ScanOut co = cfind(target);
                   int j = -1;
 #pragma unroll
                   for (int q = 0; q < NSET; ++q)
@@ -1709,8 +1811,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   r.f64_before = co.f64_before;
                   r.id = co.digit << 8;
                   if (j >= 0) {
-                    const ScanOut fo = scan256(s, s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN, nullptr,
-                                               false, target - (double)co.fix_before);
+                    const ScanOut fo = hist_find(s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN,
+                                                 fpc + j * NBIN, fpw + j * NBIN, fpf + j * NBIN,
+                                                 target - (double)co.fix_before);
                     r.id |= fo.digit;
                     r.cnt_before += fo.cnt_before;
                     r.fix_before += fo.fix_before;
