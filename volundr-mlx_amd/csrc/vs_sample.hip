@@ -612,6 +612,10 @@ constexpr int SEGW = KEYS_CAP / SNW;  // per-wave candidate segment
 // (4352 words), 3 * 256 coarse + 3 * NSET * 256 fine words.
 constexpr int PFX_OFF = 4352;
 static_assert(PFX_OFF + 3 * NBIN * (1 + NSET) <= KEYS_CAP, "prefix sums fit the key area");
+// Key-area layout of the value-bin path below the prefix sums: words 0-511 gathered keys, then from word 512 the
+// fine-bin id of every chunk position (u16; 0xFFFF = not in the kept set).
+constexpr int FID_OFF = 512;
+static_assert(FID_OFF * 8 + EPT_MAX * SNT * 2 <= PFX_OFF * 8, "fine-bin ids fit below the prefix sums");
 
 // Sort 64*E keys held by one wave descending (lane L holds positions L + 64*i in e[i]); the bitonic network is
 // fully unrolled: partners at distance < 64 are exchanged across lanes (DPP / permlane), the others in-lane.
@@ -1570,8 +1574,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         auto fine_of = [&](float xs) -> int {  // xs = x / t
           const float u = xs0 - xs;
           int f = (int)(u * fscale);
-          f = f < 0 ? 0 : (f > 65535 ? 65535 : f);
-          return 65535 - f;  // (coarse digit << 8) | fine digit
+          f = f < 1 ? 1 : (f > 65535 ? 65535 : f);
+          return 65535 - f;  // (coarse digit << 8) | fine digit, at most 0xFFFE
         };
         auto mass = [&](float xs, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
           const float d = xs - xs0;
@@ -1582,7 +1586,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         VS_TR(A, 4);
         // ---- round 1: coarse mass histogram of the kept set + its size + a bounded gather ----
         if (t == 0) s.misc[15] = 0;
+        // every position's fine-bin id (0xFFFF = not kept), so that the later rounds test a u16 per position
+        uint16_t* fid = (uint16_t*)(s.keys + FID_OFF);
+        for (int v = t; v < A.CH / 8; v += SNT) ((uint4*)fid)[v] = make_uint4(~0u, ~0u, ~0u, ~0u);
         hist_clear(s);
+        __syncthreads();
         // With few qualifying lanes the kept logits are also listed in LDS for the gather below; otherwise the
         // kept count exceeds GSMALL and no gather happens.
         const bool few = nq * 4 <= SNT;
@@ -1594,13 +1602,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             ++cbr;
             u64 fx;
             const double pr = mass(xs, &fx);
-            const int c = fine_of(xs) >> 8;
+            const int fo = fine_of(xs);
+            fid[e - lo] = (uint16_t)fo;
+            const int c = fo >> 8;
             atomicAdd(&s.hc[c], 1u);
             atomicAdd(&s.hfix[c], fx);
             unsafeAtomicAdd(&s.hf64[c], pr);
             if (few) {
               const int p = atomicAdd(&s.misc[15], 1);
-              if (p < KEYS_CAP) s.keys[p] = kk;
+              if (p < FID_OFF) s.keys[p] = kk;
             }
           }
         })
@@ -1736,25 +1746,21 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               __syncthreads();
               VS_TRX(46);
-              FOR_KEPT({
-                u64 kk;
-                float xs;
-                if (keep_xs(x, e, kk, xs)) {
-                  const int id = fine_of(xs);
-                  const int c = id >> 8;
-                  int j = -1;
-                  for (int q = 0; q < NSET; ++q)
-                    if (q < ns && set[q] == c) j = q;
-                  if (j >= 0) {
-                    u64 fx;
-                    const double pr = mass(xs, &fx);
-                    const int b2 = j * NBIN + (id & 0xFF);
-                    atomicAdd(&s.fc[b2], 1u);
-                    atomicAdd(&s.ffix[b2], fx);
-                    unsafeAtomicAdd(&s.ff64[b2], pr);
-                  }
+              for (int i = t; i < hi - lo; i += SNT) {
+                const uint32_t id = fid[i];
+                const int c = (int)(id >> 8);
+                int j = -1;
+#pragma unroll
+                for (int q = 0; q < NSET; ++q) j = (q < ns && set[q] == c) ? q : j;
+                if (id != 0xFFFFu && j >= 0) {
+                  u64 fx;
+                  const double pr = mass(s.xv[i] / tt, &fx);
+                  const int b2 = j * NBIN + (int)(id & 0xFF);
+                  atomicAdd(&s.fc[b2], 1u);
+                  atomicAdd(&s.ffix[b2], fx);
+                  unsafeAtomicAdd(&s.ff64[b2], pr);
                 }
-              })
+              }
               __syncthreads();
               VS_TR(A, 15);
               HistSlot* h2 = hslots + slot;
@@ -1844,17 +1850,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 } else {
                   if (t == 0) s.misc[16] = 0;
                   __syncthreads();
-                  FOR_KEPT({
-                    u64 kk;
-                    float xs;
-                    if (keep_xs(x, e, kk, xs)) {
-                      const int id = fine_of(xs);
-                      if ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id)) {
-                        const int p = atomicAdd(&s.misc[16], 1);
-                        if (p < KEYS_CAP) s.keys[p] = kk;
-                      }
+                  for (int i = t; i < hi - lo; i += SNT) {
+                    const int id = (int)fid[i];
+                    if (id != 0xFFFF && ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id))) {
+                      const int p = atomicAdd(&s.misc[16], 1);
+                      if (p < FID_OFF) s.keys[p] = key64(s.xv[i], (uint32_t)(lo + i));
                     }
-                  })
+                  }
                   __syncthreads();
                   const int nloc = s.misc[16];  // <= gcount <= GCAP2
                   if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
