@@ -185,6 +185,28 @@ def test_edits(dev):
     assert out.ids[0].item() == 5 and out.ids[3].item() == V - 1
 
 
+@pytest.mark.parametrize("V", [40000, 163840])
+def test_topk_edits_move_lane_maxima(dev, V):
+    """Top-k rows whose edits move the largest logits: heavy penalties on the row's top tokens (the bound taken
+    before the edits is then too high and the kernel must redo it) and edits that raise logits (repetition penalty
+    below 1, negative penalties, positive biases)."""
+    rng = np.random.default_rng(V + 5)
+    B = 8
+    x = rng.standard_normal((B, V)).astype(np.float32) * 2.0
+    order = np.argsort(-x, axis=1)
+    ps, hists = [], []
+    for b in range(B):
+        k = [5, 20, 50, 200][b % 4]
+        if b < 4:  # push the top tokens down hard
+            ps.append(Sampling(top_k=k, repetition_penalty=3.0, frequency_penalty=2.0, presence_penalty=4.0))
+            hists.append(list(order[b, :3 * k]) * 2)
+        else:  # raise low tokens above the rest
+            ps.append(Sampling(top_k=k, repetition_penalty=0.25, presence_penalty=-6.0, frequency_penalty=-1.0,
+                               logit_bias=[(int(order[b, -1 - j]), 40.0) for j in range(3)]))
+            hists.append(list(order[b, V // 2:V // 2 + k]) + list(rng.integers(0, V, size=50)))
+    run(dev, x, ps, rng.random(B), hists, label=f"topk edits V{V}")
+
+
 def test_long_and_unaligned_histories(dev):
     # histories beyond the in-register prefetch (32768 tokens) and rows whose history starts unaligned
     rng = np.random.default_rng(23)
