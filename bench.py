@@ -9,7 +9,8 @@ Infinity Cache. Printed (one JSON line on stdout):
   value       end-to-end microseconds per step (host-issued launches back to back, HIP events on the launch stream)
   roofline    algorithmic bytes per launch / average kernel duration (event pairs around each launch) vs 8 TB/s
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
-The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method.
+The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
+is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts).
 """
 import argparse
 import json
@@ -80,6 +81,31 @@ def bench_sample(torch, dev, d, steps, warmup, nslots):
     cold = time_calls(torch, call, nslots, steps, warmup)
     warm = time_calls(torch, call, 1, steps, warmup)
     flags = call.out.flags.cpu().numpy()
+    assert not any((int(f) & 0xFFFFFFFF) >> 31 for f in flags), "timeout flag set"
+    return cold, warm, algo_bytes_sample(d, B)
+
+
+def bench_state(torch, dev, d, steps, warmup, nslots):
+    """C3 through vs_sample_batch_state: the same rows with the sampler state (draw, history, produced) on the
+    device, each call also accepting its token; the history pool has room for every call of the run."""
+    from volundr_amd import DeviceSamplers, Sampler
+
+    B, V = d["logits"].shape
+    samplers = []
+    for r, sp in enumerate(d["params"]):
+        s = Sampler(sp, vocab_valid=V, request_id=r)
+        s.rng = 0x9E3779B97F4A7C15 ^ r
+        for tok in (d["hists"][r] if d["hists"] is not None else ()):
+            s.accept(int(tok))
+        samplers.append(s)
+    h0 = 0 if d["hists"] is None else d["hists"].shape[1]
+    ds = DeviceSamplers(samplers, V, hist_cap=h0 + 4 * (steps + warmup) + 64, device=dev)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    slots = [x] + [x.clone() for _ in range(nslots - 1)]
+    call = ds.bind(slots)
+    cold = time_calls(torch, call, nslots, steps, warmup)
+    warm = time_calls(torch, call, 1, steps, warmup)
+    flags = ds.out.flags.cpu().numpy()
     assert not any((int(f) & 0xFFFFFFFF) >> 31 for f in flags), "timeout flag set"
     return cold, warm, algo_bytes_sample(d, B)
 
@@ -183,6 +209,9 @@ def main():
             dd = synth.CONFIGS[name](seed=0)
             (oe, ok), (we, wk), ab = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
+        dd = synth.CONFIGS["c3"](seed=0)
+        (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)
+        others["c3_state"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         for name in ("c2", "c4"):
             if name == a.config:
                 continue

@@ -3,6 +3,9 @@
  * The library replaces the token-selection hot path of volundr-mlx:
  *   - vs_sample_batch   : Sampler.sample for a batch of rows (volundr-mlx/sampler.py:100-156), called per row
  *                         by scheduler.py:424 / session.py:615 through Sampler.choose (sampler.py:83-98);
+ *   - vs_sample_batch_state : the same with the per-request sampler state kept on the device (the xorshift64*
+ *                         draw, Sampler.counts as a token history in a device pool, Sampler.produced), so that a
+ *                         serving loop uploads nothing per step (sampler.py:58-81, SURVEY next-row state);
  *   - vs_verify_greedy  : the greedy verify step of speculative decoding: first-max argmax over the valid
  *                         vocabulary and the accept prefix (volundr-mlx/spec/specdec.py:326-336 for B=1,
  *                         volundr-mlx/scheduler.py:462-470 for B<=4), plus the chosen-token logprob.
@@ -48,6 +51,8 @@ enum {
   VS_OUT_NOFINITE = 1u << 4,      /* no finite logit: np.argmax of the row (sampler.py:131-132) */
   VS_OUT_COOP = 1u << 5,          /* the distribution was resolved by the row-cooperative radix select */
   VS_OUT_GATHER = 1u << 6,        /* the distribution was resolved in one workgroup after a gather */
+  VS_OUT_HIST_FULL = 1u << 7,     /* vs_sample_batch_state: the request's history slots were full, the token was
+                                     not recorded (later penalties miss it) */
   VS_OUT_TIMEOUT = 1u << 31       /* an inter-workgroup wait hit its spin limit: results of this row are invalid */
 };
 
@@ -90,6 +95,30 @@ int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, con
 
 size_t vs_sample_workspace_bytes(int B, int V);
 
+/* Per-request sampler state kept on the device (Sampler, sampler.py:58-81). 32 bytes, 8-byte aligned. */
+typedef struct vs_row_state {
+  uint64_t rng;           /* xorshift64* state (Sampler.rng); the host seeds it as Sampler.__init__ does */
+  int64_t hist_off;       /* first slot of this request's token history in the pool */
+  int32_t hist_len;       /* tokens recorded so far (the multiset behind Sampler.counts) */
+  int32_t hist_cap;       /* slots reserved from hist_off */
+  int32_t produced;       /* Sampler.produced */
+  int32_t min_new_tokens; /* the stop range of the row's params applies while produced < min_new_tokens */
+} vs_row_state;
+
+/* vs_sample_batch with the state on the device: for each row r the draw is Sampler.uniform() on state[r].rng,
+ * the history is pool[hist_off, hist_off + hist_len), and the stop mask applies while produced < min_new_tokens
+ * (params[r].u, hist_begin/hist_end are ignored; the stop range gives the stop ids). After the choice the row's
+ * state is advanced as Sampler.accept does (sampler.py:75-79): the token is appended to the history (flag
+ * VS_OUT_HIST_FULL when hist_len == hist_cap), produced += 1, and the xorshift64* state moves on when the row drew
+ * (not for greedy rows or rows with no finite logit, which return before self.uniform(), sampler.py:127-133).
+ * Rows flagged VS_OUT_TIMEOUT leave their state unchanged. Rows of one call must not share history slots.
+ * Replaces: Sampler.choose (sampler.py:83-98) for requests without a reasoning budget, with uniform() and accept()
+ * on the device. */
+int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                          vs_row_state* state, int32_t* pool, const int32_t* bias_ids, const float* bias_vals,
+                          const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
+                          int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream);
+
 /* Greedy speculative verify over logits [B, T, V] (row (b,t) starts at element (b*T + t)*ld).
  *   drafts     : int32 [B, T-1], the draft tokens inp[:, 1:] of the verify input
  *   out_argmax : int32 [B, T], first-max argmax over [0, vocab_valid)
@@ -108,7 +137,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change). */
+/* Library ABI version (increments on any signature or struct change): 2. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -87,6 +87,18 @@ __device__ __forceinline__ float inv_ord32(uint32_t k) {
 __device__ __forceinline__ u64 key64(float x, uint32_t idx) {
   return ((u64)ord32(x) << 32) | (u64)(0xFFFFFFFFu - idx);
 }
+// xorshift64* of Sampler.uniform (volundr-mlx/sampler.py:67-73): one state step, and the uniform of a stepped state
+// (the top 53 bits of the multiplied state over 2^53).
+__host__ __device__ __forceinline__ u64 xorshift64s_step(u64 r) {
+  r ^= r >> 12;
+  r ^= r << 25;
+  r ^= r >> 27;
+  return r;
+}
+__host__ __device__ __forceinline__ double xorshift64s_uniform(u64 r) {
+  return (double)((r * 0x2545F4914F6CDD1DULL) >> 11) / 9007199254740992.0;
+}
+
 __device__ __forceinline__ u64 amkey64(float x, uint32_t idx) {
   uint32_t o = (x != x) ? 0xFFFFFFFFu : ord32(x);
   return ((u64)o << 32) | (u64)(0xFFFFFFFFu - idx);

@@ -111,6 +111,8 @@ struct SampleArgs {
   uint32_t spin_limit;
   double fix_scale;  // probability -> fixed point
   const vs_row_params* params;
+  vs_row_state* state;  // device-resident request state, or null
+  int32_t* pool;        // history pool of the state entry point
   const int32_t* hist;
   const int32_t* bias_ids;
   const float* bias_vals;
@@ -774,12 +776,31 @@ __device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, 
   return r;
 }
 
-__device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Final& f) {
+// The state entry point's Sampler.accept (sampler.py:75-79) and the draw's state advance, by the one thread that
+// writes the row's result; the launch boundary orders it before the next call's reads.
+__device__ __forceinline__ uint32_t commit_state(const SampleArgs& A, int r, int32_t token, uint32_t flags,
+                                                 const vs_row_state& st, uint64_t rng_next) {
+  if (!A.state || (flags & VS_OUT_TIMEOUT)) return flags;
+  vs_row_state* S = A.state + r;
+  if (!(flags & (VS_OUT_GREEDY | VS_OUT_NOFINITE))) S->rng = rng_next;
+  if (st.hist_len < st.hist_cap) {
+    A.pool[st.hist_off + st.hist_len] = token;
+    S->hist_len = st.hist_len + 1;
+  } else {
+    flags |= VS_OUT_HIST_FULL;
+  }
+  S->produced = st.produced + 1;
+  return flags;
+}
+
+__device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Final& f, const vs_row_state& st,
+                                          uint64_t rng_next) {
   if (threadIdx.x == 0) {
     const int r = A.row0 + row;
+    const uint32_t flags = commit_state(A, r, f.token, f.flags, st, rng_next);
     A.out_ids[r] = f.token;
     A.out_lp[r] = f.lp;
-    if (A.out_flags) A.out_flags[r] = f.flags;
+    if (A.out_flags) A.out_flags[r] = flags;
     if (A.out_keep) A.out_keep[r] = f.keep;
   }
 }
@@ -915,7 +936,18 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int row = l / G, g = l % G;
   const int grow = A.row0 + row;
-  const vs_row_params P = A.params[grow];
+  vs_row_params P = A.params[grow];
+  // state entry point: the draw, the history range and the stop mask come from the request's device state
+  vs_row_state st = {0, 0, 0, 0, 0, 0};
+  uint64_t rng_next = 0;
+  if (A.state) {
+    st = A.state[grow];
+    rng_next = xorshift64s_step(st.rng);
+    P.u = xorshift64s_uniform(rng_next);
+    P.hist_begin = st.hist_off;
+    P.hist_end = st.hist_off + st.hist_len;
+    if (st.produced >= st.min_new_tokens) P.stop_end = P.stop_begin;
+  }
   char* rws = A.ws + (size_t)row * ROW_WS;
   RowCtl* ctl = (RowCtl*)rws;
   Part* parts = (Part*)(rws + OFF_PART);
@@ -1156,9 +1188,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (t == 0) {
           const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
           const int r = A.row0 + row;
+          const uint32_t fl = commit_state(A, r, (int32_t)key_index(bam), VS_OUT_GREEDY, st, rng_next);
           A.out_ids[r] = (int32_t)key_index(bam);
           A.out_lp[r] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
-          if (A.out_flags) A.out_flags[r] = VS_OUT_GREEDY;
+          if (A.out_flags) A.out_flags[r] = fl;
           if (A.out_keep) A.out_keep[r] = 0;
         }
       }
@@ -1348,7 +1381,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         f.lp = 0.0f;
         f.flags = VS_OUT_NOFINITE;
         f.keep = 0;
-        write_out(A, row, f);
+        write_out(A, row, f, st, rng_next);
       } else {
         u64 M = 0;  // 0: fewer than keff heads, no bound
         if (nzh >= keff) {
@@ -1395,7 +1428,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         VS_TR(A, 6);
         const Final f = wave_sample(s, s.tk, keff, P);
         VS_TR(A, 7);
-        write_out(A, row, f);
+        write_out(A, row, f, st, rng_next);
       }
       cleanup(0);
     }
@@ -1998,7 +2031,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   fin.keep = keep;
                   fin.flags = flags;
                   VS_TR(A, 8);
-                  write_out(A, row, fin);
+                  write_out(A, row, fin, st, rng_next);
                   cleanup(slot);
                   VS_TR_FLUSH(A);
                   return;
@@ -2177,7 +2210,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #undef FOR_XV4
   VS_TR(A, 9);
   // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree.
-  if (g == 0 && g0_writes) write_out(A, row, fin);
+  if (g == 0 && g0_writes) write_out(A, row, fin, st, rng_next);
   if (!ok && t == 0) atomicOr(&ctl->err, 1u);  // a timed-out row clears every histogram slot
   if (arrive_done()) {
     const bool err = ld_relaxed(&ctl->err) != 0;
@@ -2209,10 +2242,10 @@ extern "C" size_t vs_sample_workspace_bytes(int B, int V) {
   return (size_t)rows * ROW_WS;
 }
 
-extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
-                               const int32_t* hist, const int32_t* bias_ids, const float* bias_vals,
-                               const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
-                               int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
+static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                         vs_row_state* state, int32_t* pool, const int32_t* hist, const int32_t* bias_ids,
+                         const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
+                         uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
   if (B == 0) return VS_OK;
   if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
@@ -2236,7 +2269,8 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
   CH = (CH + unit - 1) / unit * unit;
   G = (V + CH - 1) / CH;
   const int NV = CH / unit;
-  const int has_hist = hist != nullptr;
+  if (state && !pool) return fail(VS_EINVAL, "vs_sample_batch_state: null state pool");
+  const int has_hist = state ? 1 : (hist != nullptr);
   const int lds_ch = CH;
   const size_t lds = smem_bytes(lds_ch);
   if (lds > dv->lds_per_block) return fail(VS_EINVAL, "vs_sample_batch: LDS need exceeds the device limit");
@@ -2271,7 +2305,9 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
   a.spin_limit = 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.params = params;
-  a.hist = hist;
+  a.state = state;
+  a.pool = pool;
+  a.hist = state ? pool : hist;
   a.bias_ids = bias_ids;
   a.bias_vals = bias_vals;
   a.mask_ids = mask_ids;
@@ -2296,4 +2332,22 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
     if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: launch");
   }
   return VS_OK;
+}
+
+extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                               const int32_t* hist, const int32_t* bias_ids, const float* bias_vals,
+                               const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
+                               int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
+  return sample_launch(logits, dtype, B, V, ld, params, nullptr, nullptr, hist, bias_ids, bias_vals, mask_ids, out_ids,
+                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream);
+}
+
+extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld,
+                                     const vs_row_params* params, vs_row_state* state, int32_t* pool,
+                                     const int32_t* bias_ids, const float* bias_vals, const int32_t* mask_ids,
+                                     int32_t* out_ids, float* out_logprob, uint32_t* out_flags, int32_t* out_keep,
+                                     void* ws, size_t ws_bytes, vs_stream_t stream) {
+  if (!state) return fail(VS_EINVAL, "vs_sample_batch_state: null state");
+  return sample_launch(logits, dtype, B, V, ld, params, state, pool, nullptr, bias_ids, bias_vals, mask_ids, out_ids,
+                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream);
 }

@@ -10,7 +10,8 @@ from .session import Sampling
 from .sampler import Budget, Sampler, sample_rows_for
 from .ops import (DeviceRows, PackedRows, SampleOut, VerifyOut, emitted, pack_rows, sample_batch, sample_rows,
                   verify_greedy)
+from .state import DeviceSamplers
 from ._lib import LIB_PATH, VsError
 
 __all__ = ["Sampling", "Sampler", "Budget", "sample_rows_for", "sample_batch", "sample_rows", "pack_rows",
-           "PackedRows", "DeviceRows", "SampleOut", "VerifyOut", "verify_greedy", "emitted", "LIB_PATH", "VsError"]
+           "PackedRows", "DeviceRows", "SampleOut", "VerifyOut", "verify_greedy", "emitted", "DeviceSamplers", "LIB_PATH", "VsError"]

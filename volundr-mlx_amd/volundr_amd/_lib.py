@@ -21,6 +21,7 @@ OUT_GREEDY = 1 << 3
 OUT_NOFINITE = 1 << 4
 OUT_COOP = 1 << 5
 OUT_GATHER = 1 << 6
+OUT_HIST_FULL = 1 << 7
 OUT_TIMEOUT = 1 << 31
 
 # vs_row_params, 88 bytes (layout fixed by the C header)
@@ -33,8 +34,14 @@ ROW_DTYPE = np.dtype([
 ])
 assert ROW_DTYPE.itemsize == 88
 
-EXPORTS = ("vs_sample_batch", "vs_sample_workspace_bytes", "vs_verify_greedy", "vs_verify_workspace_bytes",
-           "vs_workspace_init", "vs_last_error", "vs_version")
+# vs_row_state, 32 bytes: the per-request sampler state of vs_sample_batch_state
+STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4"), ("hist_cap", "<i4"),
+                        ("produced", "<i4"), ("min_new_tokens", "<i4")])
+assert STATE_DTYPE.itemsize == 32
+
+ABI_VERSION = 2
+EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
+           "vs_verify_workspace_bytes", "vs_workspace_init", "vs_last_error", "vs_version")
 
 _lib = None
 
@@ -54,6 +61,8 @@ def load():
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     L.vs_sample_batch.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     L.vs_sample_batch.restype = i32
+    L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    L.vs_sample_batch_state.restype = i32
     L.vs_sample_workspace_bytes.argtypes = [i32, i32]
     L.vs_sample_workspace_bytes.restype = sz
     L.vs_verify_greedy.argtypes = [vp, i32, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp, sz, vp]

@@ -91,13 +91,16 @@ class DeviceRows:
     B: int
 
 
-def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, extras=None) -> PackedRows:
+def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, extras=None,
+              stop_always: bool = False) -> PackedRows:
     """Pack the per-row parameters the way Sampler.sample reads them (volundr-mlx/sampler.py:100-156).
 
     samplings : Sampling-like objects (session.Sampling); u : B uniform draws in [0, 1)
     histories : per-row token histories (iterables of ints: the tokens Sampler.accept recorded) or None
     produced  : per-row Sampler.produced (the min_new_tokens stop mask, sampler.py:123), default 0
     extras    : per-row budget biases [(id, bias)] applied before logit_bias (sampler.py:104-106)
+    stop_always : pack the stop ids of every row with min_new_tokens > 0 whatever `produced` is (the state entry
+                  point applies them while its device-side produced < min_new_tokens)
     """
     B = len(samplings)
     P = np.zeros(B, dtype=ROW_DTYPE)
@@ -146,7 +149,7 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
         mpos += len(sup)
         pr = 0 if produced is None else int(produced[r])
         st = []
-        if pr < sp.min_new_tokens and sp.stop_token_ids:
+        if (stop_always or pr < sp.min_new_tokens) and sp.min_new_tokens > 0 and sp.stop_token_ids:
             st = sorted({w for w in (_wrap_id(t, V) for t in sp.stop_token_ids) if w is not None})
         p["stop_begin"], p["stop_end"] = mpos, mpos + len(st)
         mask.append(np.asarray(st, dtype=np.int32))
