@@ -5,7 +5,7 @@
  *                         by scheduler.py:424 / session.py:615 through Sampler.choose (sampler.py:83-98);
  *   - vs_sample_batch_state : the same with the per-request sampler state kept on the device (the xorshift64*
  *                         draw, Sampler.counts as a token history in a device pool, Sampler.produced), so that a
- *                         serving loop uploads nothing per step (sampler.py:58-81, SURVEY next-row state);
+ *                         serving loop uploads nothing per step (sampler.py:58-81);
  *   - vs_verify_greedy  : the greedy verify step of speculative decoding: first-max argmax over the valid
  *                         vocabulary and the accept prefix (volundr-mlx/spec/specdec.py:326-336 for B=1,
  *                         volundr-mlx/scheduler.py:462-470 for B<=4), plus the chosen-token logprob.
