@@ -3,11 +3,12 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
 
 A step is one vs_sample_batch call over the B=16 x V=163840 mixed-parameter batch (configuration C3, the one
-BASELINE.json's metric names), with logits, parameters and histories already resident in HBM. Logits rotate over
+the headline metric is quoted on), with logits, parameters and histories already resident in HBM. Logits rotate over
 `--slots` device buffers (> 256 MB in total by default), so every step reads them from HBM and not from the 256 MB
 Infinity Cache. Printed (one JSON line on stdout):
   value       end-to-end microseconds per step (host-issued launches back to back, HIP events on the launch stream)
-  roofline    algorithmic bytes per launch / average kernel duration (event pairs around each launch) vs 8 TB/s
+  roofline    algorithmic bytes per launch / per-launch time (HIP events around the K back-to-back launches on the
+              launch stream; rocprofv3's average kernel duration agrees within a few percent) vs 8 TB/s
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
 is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts).

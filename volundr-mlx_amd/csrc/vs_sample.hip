@@ -1617,9 +1617,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           return pr;
         };
         VS_TR(A, 4);
-        // ---- round 1: coarse mass histogram of the kept set + its size + a bounded gather ----
+        // ---- value-bin pass 1: coarse mass histogram of the kept set + its size + a bounded gather ----
         if (t == 0) s.misc[15] = 0;
-        // every position's fine-bin id (0xFFFF = not kept), so that the later rounds test a u16 per position
+        // every position's fine-bin id (0xFFFF = not kept), so that the later passes test a u16 per position
         uint16_t* fid = (uint16_t*)(s.keys + FID_OFF);
         for (int v = t; v < A.CH / 8; v += SNT) ((uint4*)fid)[v] = make_uint4(~0u, ~0u, ~0u, ~0u);
         hist_clear(s);
@@ -1771,7 +1771,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             if (ns > NSET) {
               radix = true;
             } else {
-              // ---- round 2: fine histograms of the selected coarse bins ----
+              // ---- value-bin pass 2: fine histograms of the selected coarse bins ----
               for (int i = t; i < NSET * NBIN; i += SNT) {
                 s.fc[i] = 0;
                 s.ffix[i] = 0;
