@@ -131,13 +131,45 @@ int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t
 
 size_t vs_verify_workspace_bytes(int B, int T, int V);
 
+/* The k largest logits of each of B rows, value descending, ties to the lower id (rows with fewer than k finite
+ * logits pad with id -1 and value -inf). 1 <= k <= 256 (less when V needs many workgroups per row; the call fails
+ * with VS_EINVAL above the shape's limit). Values are the logits widened to float32.
+ *   out_ids : int32 [B, k];  out_vals : float32 [B, k]
+ *   ws      : as for vs_sample_batch (vs_sample_workspace_bytes(B, V), zeroed once)
+ * Replaces: volundr-mlx/spec/dflash.py:232-236 (argpartition + take_along_axis + argsort of the drafter logits). */
+int vs_topk_batch(const void* logits, int dtype, int B, int V, int64_t ld, int k, int32_t* out_ids, float* out_vals,
+                  void* ws, size_t ws_bytes, vs_stream_t stream);
+
+/* The drafter's greedy candidate walk for n blocks of S <= 8 slots with K <= 16 candidates each:
+ *   pred = anchor[b]; for e < S: s[c] = uval[b,e,c] + sum_r B[cid[b,e,c]][r] * float32(A[pred][r] * hp[b,e,r]);
+ *   pred = cid[b,e, first argmax of s]; out[b,e] = pred.
+ *   uval, cid : float32 / int32 [n, S, ldk] (ldk >= K);  hp : float32 [n, S, R];  anchor : int32 [n] (device)
+ *   A, B      : bf16 [vocab, R] codebooks, R a multiple of 16 in [16, 256], A 4-byte aligned
+ * Candidates with ids outside [0, vocab) never win; a slot with no valid candidate, and every slot after it,
+ * outputs -1 (as does every slot of a block whose anchor is outside [0, vocab)). Sums are fp32 in a fixed order
+ * of this build (the reference's matmul order is its own): picks agree except between scores within rounding.
+ * Replaces: volundr-mlx/spec/dflash.py:50-60 (_walk). */
+int vs_draft_walk(const float* uval, const int32_t* cid, int ldk, const float* hp, const void* A, const void* B,
+                  int vocab, int R, const int32_t* anchor, int n, int S, int K, int32_t* out, vs_stream_t stream);
+
+/* DFlash2 propose for n blocks: the top-16 of each of the n*S logit rows (row (b,e) starts at element
+ * (b*S + e)*ld, the first V entries are the valid vocabulary), then vs_draft_walk over them. out : int32 [n, S].
+ *   ws : device workspace of at least vs_draft_workspace_bytes(n, S, V) bytes (about 20 MB + 128 B per row),
+ *        zeroed once beforehand
+ * Replaces: volundr-mlx/spec/dflash.py:228-240 (DFlash2Drafter.propose after the head: top-16, sort, _walk). */
+int vs_draft_propose(const void* logits, int dtype, int n, int S, int V, int64_t ld, const float* hp, const void* A,
+                     const void* B, int vocab, int R, const int32_t* anchor, int32_t* out, void* ws, size_t ws_bytes,
+                     vs_stream_t stream);
+
+size_t vs_draft_workspace_bytes(int n, int S, int V);
+
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 2. */
+/* Library ABI version (increments on any signature or struct change): 3. */
 int vs_version(void);
 
 #ifdef __cplusplus

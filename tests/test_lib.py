@@ -83,3 +83,16 @@ def test_budget_logic():
     b = Budget(10, 1.5, [], 7, 8)
     b.accept(0, 7)
     assert b.open == 1 and b.act(9) == ("bias", [(8, 1.5)]) and b.act(5) == ("none", None)
+
+
+def test_draft_entry_points_reject_bad_shapes_without_device_calls():
+    L = _lib.load()
+    # more than 8 slots, more than 16 candidates, rank not a multiple of 16: rejected before any launch
+    assert L.vs_draft_walk(1, 1, 16, 1, 4, 4, 10, 256, 1, 1, 9, 16, 1, 0) == _lib.VS_EINVAL
+    assert L.vs_draft_walk(1, 1, 17, 1, 4, 4, 10, 256, 1, 1, 7, 17, 1, 0) == _lib.VS_EINVAL
+    assert L.vs_draft_walk(1, 1, 16, 1, 4, 4, 10, 250, 1, 1, 7, 16, 1, 0) == _lib.VS_EINVAL
+    assert L.vs_draft_walk(0, 1, 16, 1, 4, 4, 10, 256, 1, 1, 7, 16, 1, 0) == _lib.VS_EINVAL
+    assert L.vs_draft_walk(1, 1, 16, 1, 4, 4, 10, 256, 1, 0, 7, 16, 1, 0) == _lib.VS_OK  # n = 0: nothing to do
+    assert L.vs_topk_batch(1, 0, 1, 10, 10, 0, 1, 1, 1, 1 << 20, 0) == _lib.VS_EINVAL  # k < 1
+    assert L.vs_draft_workspace_bytes(2, 7, 163840) > L.vs_sample_workspace_bytes(14, 163840)
+    assert L.vs_draft_propose(1, 0, 1, 7, 10, 10, 1, 4, 4, 10, 256, 1, 1, 0, 0, 0) == _lib.VS_EINVAL  # null ws

@@ -112,6 +112,9 @@ struct SampleArgs {
   double fix_scale;  // probability -> fixed point
   const vs_row_params* params;
   vs_row_state* state;  // device-resident request state, or null
+  int list_k;           // > 0: top-list mode (vs_topk_batch): every row publishes its list_k largest logits, sorted
+  int32_t* list_ids;    // [B, list_k]
+  float* list_vals;     // [B, list_k]
   int32_t* pool;        // history pool of the state entry point
   const int32_t* hist;
   const int32_t* bias_ids;
@@ -936,7 +939,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int row = l / G, g = l % G;
   const int grow = A.row0 + row;
-  vs_row_params P = A.params[grow];
+  vs_row_params P;
+  if (A.params) {
+    P = A.params[grow];
+  } else {  // top-list mode: plain logits, top_k = list_k, no edits
+    P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0};
+  }
   // state entry point: the draw, the history range and the stop mask come from the request's device state
   vs_row_state st = {0, 0, 0, 0, 0, 0};
   uint64_t rng_next = 0;
@@ -1375,13 +1383,25 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       const u64 bam = s.red64[0];
       int keff = k < n ? k : n;  // sampler.py:133-134
       if (keff < 1) keff = 1;
+      // top-list mode (vs_topk_batch): the sorted list, id -1 and value -inf past the row's finite logits
+      auto write_list = [&](int have) {
+        const int r = A.row0 + row;
+        for (int i = t; i < A.list_k; i += SNT) {
+          A.list_ids[(size_t)r * A.list_k + i] = i < have ? (int32_t)key_index(s.tk[i]) : -1;
+          A.list_vals[(size_t)r * A.list_k + i] = i < have ? key_value(s.tk[i]) : -__builtin_inff();
+        }
+      };
       if (n == 0) {  // sampler.py:131-132
-        Final f;
-        f.token = (int32_t)key_index(bam);
-        f.lp = 0.0f;
-        f.flags = VS_OUT_NOFINITE;
-        f.keep = 0;
-        write_out(A, row, f, st, rng_next);
+        if (A.list_k > 0) {
+          write_list(0);
+        } else {
+          Final f;
+          f.token = (int32_t)key_index(bam);
+          f.lp = 0.0f;
+          f.flags = VS_OUT_NOFINITE;
+          f.keep = 0;
+          write_out(A, row, f, st, rng_next);
+        }
       } else {
         u64 M = 0;  // 0: fewer than keff heads, no bound
         if (nzh >= keff) {
@@ -1426,9 +1446,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           rank_sort(sel, keff, s.tk, keff);
         }
         VS_TR(A, 6);
-        const Final f = wave_sample(s, s.tk, keff, P);
-        VS_TR(A, 7);
-        write_out(A, row, f, st, rng_next);
+        if (A.list_k > 0) {
+          write_list(keff);
+        } else {
+          const Final f = wave_sample(s, s.tk, keff, P);
+          VS_TR(A, 7);
+          write_out(A, row, f, st, rng_next);
+        }
       }
       cleanup(0);
     }
@@ -2245,14 +2269,18 @@ extern "C" size_t vs_sample_workspace_bytes(int B, int V) {
 static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
                          vs_row_state* state, int32_t* pool, const int32_t* hist, const int32_t* bias_ids,
                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
-                         uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
+                         uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream,
+                         int list_k = 0, int32_t* list_ids = nullptr, float* list_vals = nullptr) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
   if (B == 0) return VS_OK;
   if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
   if (ld < V) return fail(VS_EINVAL, "vs_sample_batch: ld < V");
   if (dtype != VS_F32 && dtype != VS_BF16 && dtype != VS_F16) return fail(VS_EINVAL, "vs_sample_batch: bad dtype");
-  if (!logits || !params || !out_ids || !out_logprob || !ws)
+  if (list_k > 0) {
+    if (!logits || !list_ids || !list_vals || !ws) return fail(VS_EINVAL, "vs_topk_batch: null pointer argument");
+  } else if (!logits || !params || !out_ids || !out_logprob || !ws) {
     return fail(VS_EINVAL, "vs_sample_batch: null logits/params/out_ids/out_logprob/ws");
+  }
   const DevInfo* dv = dev_info();
   if (!dv) return fail(VS_EHIP, "vs_sample_batch: no HIP device");
   const int VEC = dtype == VS_F32 ? 4 : 8;
@@ -2288,6 +2316,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   int kcap = 1;  // list capacity per workgroup: a power of two <= KEYS_CAP / G
   while (kcap * 2 <= KEYS_CAP / G && kcap * 2 <= 1024) kcap *= 2;
   const int kmax = kcap < KCAP ? kcap : KCAP;
+  if (list_k > kmax) return fail(VS_EINVAL, "vs_topk_batch: k above the largest list this shape supports");
   int bits = 0;
   while ((1ll << bits) < (long long)V) ++bits;
   SampleArgs a;
@@ -2304,7 +2333,10 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.kmax = kmax;
   a.spin_limit = 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
-  a.params = params;
+  a.params = list_k > 0 ? nullptr : params;
+  a.list_k = list_k;
+  a.list_ids = list_ids;
+  a.list_vals = list_vals;
   a.state = state;
   a.pool = pool;
   a.hist = state ? pool : hist;
@@ -2340,6 +2372,13 @@ extern "C" int vs_sample_batch(const void* logits, int dtype, int B, int V, int6
                                int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream) {
   return sample_launch(logits, dtype, B, V, ld, params, nullptr, nullptr, hist, bias_ids, bias_vals, mask_ids, out_ids,
                        out_logprob, out_flags, out_keep, ws, ws_bytes, stream);
+}
+
+extern "C" int vs_topk_batch(const void* logits, int dtype, int B, int V, int64_t ld, int k, int32_t* out_ids,
+                             float* out_vals, void* ws, size_t ws_bytes, vs_stream_t stream) {
+  if (k < 1) return fail(VS_EINVAL, "vs_topk_batch: k < 1");
+  return sample_launch(logits, dtype, B, V, ld, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, nullptr, ws, ws_bytes, stream, k, out_ids, out_vals);
 }
 
 extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld,

@@ -1,4 +1,4 @@
-"""volundr_amd - MI355X-native token selection for volundr-mlx (sampler.py path + greedy speculative verify).
+"""volundr_amd - MI355X-native token selection for volundr-mlx (sampler.py path, greedy speculative verify, DFlash2 candidate walk).
 
     from volundr_amd import Sampling, Sampler, sample_batch, verify_greedy
 
@@ -8,10 +8,11 @@ runs in libvolundr_sampling.so (hand-written HIP for gfx950, C ABI in include/vo
 """
 from .session import Sampling
 from .sampler import Budget, Sampler, sample_rows_for
-from .ops import (DeviceRows, PackedRows, SampleOut, VerifyOut, emitted, pack_rows, sample_batch, sample_rows,
-                  verify_greedy)
+from .ops import (DeviceRows, PackedRows, SampleOut, VerifyOut, draft_propose, draft_walk, emitted, pack_rows,
+                  sample_batch, sample_rows, topk_batch, verify_greedy)
 from .state import DeviceSamplers
 from ._lib import LIB_PATH, VsError
 
 __all__ = ["Sampling", "Sampler", "Budget", "sample_rows_for", "sample_batch", "sample_rows", "pack_rows",
-           "PackedRows", "DeviceRows", "SampleOut", "VerifyOut", "verify_greedy", "emitted", "DeviceSamplers", "LIB_PATH", "VsError"]
+           "PackedRows", "DeviceRows", "SampleOut", "VerifyOut", "verify_greedy", "emitted", "DeviceSamplers", "topk_batch", "draft_walk", "draft_propose",
+           "LIB_PATH", "VsError"]

@@ -310,3 +310,87 @@ class PreparedVerify:
         if rc:
             check(rc, "vs_verify_greedy")
         return self.out
+
+
+def topk_batch(logits: torch.Tensor, k: int):
+    """(ids int32 [B, k], vals float32 [B, k]): the k largest logits of each row, value descending, ties to the lower
+    id; rows with fewer than k finite logits pad with -1 / -inf (spec/dflash.py:232-236)."""
+    _require_cuda(logits, "logits")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit stride along V")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    B, V = logits.shape
+    dev = logits.device
+    ids = torch.empty(B, k, dtype=torch.int32, device=dev)
+    vals = torch.empty(B, k, dtype=torch.float32, device=dev)
+    L = _lib.load()
+    ws = workspace(dev, L.vs_sample_workspace_bytes(B, V))
+    check(L.vs_topk_batch(logits.data_ptr(), _DTYPES[logits.dtype], B, V, logits.stride(0), int(k), ids.data_ptr(),
+                          vals.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(dev)), "vs_topk_batch")
+    return ids, vals
+
+
+def _codebooks(A: torch.Tensor, B: torch.Tensor):
+    for t, nm in ((A, "A"), (B, "B")):
+        _require_cuda(t, nm)
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"codebook {nm} must be a contiguous bf16 [vocab, rank] tensor")
+    if A.shape != B.shape:
+        raise ValueError("codebooks A and B differ in shape")
+    return A.shape
+
+
+def draft_walk(uval: torch.Tensor, cid: torch.Tensor, hp: torch.Tensor, A: torch.Tensor, B: torch.Tensor,
+               anchor: torch.Tensor) -> torch.Tensor:
+    """The drafter's greedy walk (spec/dflash.py:50-60) for n blocks: uval float32 [n, S, K] / cid int32 [n, S, K]
+    (value descending), hp float32 [n, S, R], bf16 codebooks [vocab, R], anchor int32 [n] -> drafts int32 [n, S]."""
+    vocab, R = _codebooks(A, B)
+    if uval.dim() == 2:
+        uval, cid, hp, anchor = uval[None], cid[None], hp[None], anchor.reshape(1)
+    n, S, K = uval.shape
+    for t, nm in ((uval, "uval"), (cid, "cid"), (hp, "hp"), (anchor, "anchor")):
+        _require_cuda(t, nm)
+    uval = uval.to(torch.float32).contiguous()
+    cid = cid.to(torch.int32).contiguous()
+    hp = hp.to(torch.float32).contiguous()
+    anchor = anchor.reshape(n).to(torch.int32).contiguous()
+    if tuple(cid.shape) != (n, S, K) or tuple(hp.shape) != (n, S, R):
+        raise ValueError("uval, cid and hp disagree on shape")
+    dev = uval.device
+    out = torch.empty(n, S, dtype=torch.int32, device=dev)
+    check(_lib.load().vs_draft_walk(uval.data_ptr(), cid.data_ptr(), K, hp.data_ptr(), A.data_ptr(), B.data_ptr(),
+                                    vocab, R, anchor.data_ptr(), n, S, K, out.data_ptr(), _stream_handle(dev)),
+          "vs_draft_walk")
+    return out
+
+
+def draft_propose(logits: torch.Tensor, hp: torch.Tensor, A: torch.Tensor, B: torch.Tensor, anchor: torch.Tensor,
+                  vocab_valid: Optional[int] = None) -> torch.Tensor:
+    """DFlash2Drafter.propose after the head (spec/dflash.py:228-240) for n blocks: logits [n, S, V] (or [S, V]) of
+    the block rows 1..S, hp float32 [n, S, R], bf16 codebooks, anchor int32 [n] -> drafts int32 [n, S]. Only the
+    first vocab_valid logits of a row are candidates."""
+    vocab, R = _codebooks(A, B)
+    _require_cuda(logits, "logits")
+    if logits.dim() == 2:
+        logits, hp, anchor = logits[None], hp[None], anchor.reshape(1)
+    if logits.dim() != 3 or logits.stride(2) != 1 or logits.stride(0) != logits.shape[1] * logits.stride(1):
+        raise ValueError("logits must be [n, S, V] with rows evenly strided")
+    if logits.dtype not in _DTYPES:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    n, S, V = logits.shape
+    vv = V if vocab_valid is None else int(vocab_valid)
+    _require_cuda(hp, "hp")
+    _require_cuda(anchor, "anchor")
+    hp = hp.to(torch.float32).contiguous()
+    anchor = anchor.reshape(n).to(torch.int32).contiguous()
+    if tuple(hp.shape) != (n, S, R):
+        raise ValueError("hp must be [n, S, rank]")
+    dev = logits.device
+    out = torch.empty(n, S, dtype=torch.int32, device=dev)
+    L = _lib.load()
+    ws = workspace(dev, L.vs_draft_workspace_bytes(n, S, vv), "draft")
+    check(L.vs_draft_propose(logits.data_ptr(), _DTYPES[logits.dtype], n, S, vv, logits.stride(1), hp.data_ptr(),
+                             A.data_ptr(), B.data_ptr(), vocab, R, anchor.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                             ws.numel(), _stream_handle(dev)), "vs_draft_propose")
+    return out
