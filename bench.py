@@ -11,7 +11,8 @@ Infinity Cache. Printed (one JSON line on stdout):
               launch stream; rocprofv3's average kernel duration agrees within a few percent) vs 8 TB/s
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
-is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts).
+is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts);
+"draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary.
 """
 import argparse
 import json
@@ -125,6 +126,30 @@ def bench_verify(torch, dev, d, steps, warmup, nslots):
     return cold, warm, algo_bytes_verify(d), int(acc.sum() + len(acc))
 
 
+DRAFT_V, DRAFT_VV, DRAFT_S, DRAFT_R = 248320, 248077, 7, 256
+
+
+def bench_draft(torch, dev, steps, warmup, nslots):
+    """DFlash2 propose after the head (spec/dflash.py:228-240): top-16 of the 7 block rows' bf16 logits
+    [7, 248320] over the 248077 valid ids, then the 7-slot walk over rank-256 bf16 codebooks [248320, 256]."""
+    from volundr_amd import ops
+
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = (torch.randn(1, DRAFT_S, DRAFT_V, generator=g, device=dev) * 4).to(torch.bfloat16)
+    slots = [x] + [x.clone() for _ in range(nslots - 1)]
+    A = (torch.randn(DRAFT_V, DRAFT_R, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    B = (torch.randn(DRAFT_V, DRAFT_R, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    hp = torch.randn(1, DRAFT_S, DRAFT_R, generator=g, device=dev)
+    anchor = torch.tensor([1234], dtype=torch.int32, device=dev)
+    call = ops.PreparedPropose(slots, hp, A, B, anchor, vocab_valid=DRAFT_VV)
+    cold = time_calls(torch, call, nslots, steps, warmup)
+    warm = time_calls(torch, call, 1, steps, warmup)
+    # logits once, the predecessor rows (anchor + 6 x 16 candidates) and successor rows (7 x 16), hp, drafts
+    algo = DRAFT_S * DRAFT_VV * 2 + (1 + (DRAFT_S - 1) * 16 + DRAFT_S * 16) * DRAFT_R * 2 + DRAFT_S * DRAFT_R * 4 \
+        + DRAFT_S * 4
+    return cold, warm, algo
+
+
 def cpu_baseline(d, budget_s=10.0):
     """The oracle (NumPy restatement of sampler.py) row by row, single-threaded, for about budget_s seconds."""
     from oracle import sampler_ref as S
@@ -219,6 +244,10 @@ def main():
             dd = synth.CONFIGS[name](seed=0)
             (oe, ok), (we, wk), ab, nt = bench_verify(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, nt)
+        (oe, ok), (we, wk), ab = bench_draft(torch, dev, a.steps, a.warmup, a.slots)
+        others["draft_propose"] = entry(oe, ok, we, ab, DRAFT_S)
+        others["draft_propose"]["workload"] = ("DFlash2 propose: top-16 of bf16 logits [7, 248320] (248077 valid) + "
+                                               "7-slot walk, rank-256 codebooks; 2 kernels per step")
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
     # One kernel per step, launched back to back: the per-step time is the kernel's average launch duration plus
     # the inter-dispatch gap (rocprofv3 --kernel-trace agrees within a few percent); per-launch event pairs add

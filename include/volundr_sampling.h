@@ -144,7 +144,7 @@ int vs_topk_batch(const void* logits, int dtype, int B, int V, int64_t ld, int k
  *   pred = anchor[b]; for e < S: s[c] = uval[b,e,c] + sum_r B[cid[b,e,c]][r] * float32(A[pred][r] * hp[b,e,r]);
  *   pred = cid[b,e, first argmax of s]; out[b,e] = pred.
  *   uval, cid : float32 / int32 [n, S, ldk] (ldk >= K);  hp : float32 [n, S, R];  anchor : int32 [n] (device)
- *   A, B      : bf16 [vocab, R] codebooks, R a multiple of 16 in [16, 256], A 4-byte aligned
+ *   A, B      : bf16 [vocab, R] codebooks, R a multiple of 16 in [16, 256]
  * Candidates with ids outside [0, vocab) never win; a slot with no valid candidate, and every slot after it,
  * outputs -1 (as does every slot of a block whose anchor is outside [0, vocab)). Sums are fp32 in a fixed order
  * of this build (the reference's matmul order is its own): picks agree except between scores within rounding.

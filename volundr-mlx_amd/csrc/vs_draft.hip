@@ -8,10 +8,11 @@
 //
 // One 256-thread workgroup per block: thread t owns candidate c = t / 16 and the contiguous part p = t % 16 of the
 // rank axis (R / 16 entries). Everything the walk can touch is independent of the path it takes, so it is fetched
-// before the first slot: the successor rows B[cid[e][c]] and hp[e] go to VGPRs (thread's part, every slot), the
-// predecessor rows A[anchor] and A[cid[e][c]] (any of them can become `pred`) go to LDS. The 7 slots then run from
-// registers and LDS only: products, a 16-lane sum, one LDS exchange of the 16 scores per slot and a barrier. The
-// walk is latency-bound: two dependent global loads (anchor, then its row) and ~7 LDS round trips.
+// before the first slot: the successor rows B[cid[e][c]] stay in VGPRs as packed bf16 (thread's part, every slot);
+// the predecessor rows A[anchor] and A[cid[e][c]] (any of them can become `pred`) go to LDS, each multiplied by the
+// hp of the one slot that can use it. Every global load is issued before the first is consumed, so the fetch costs
+// two memory latencies (ids, then the rows they name). The slots then run from registers and LDS only: 16 products,
+// a 16-lane sum, one LDS exchange of the 16 scores and a barrier, and a 16-lane first-max reduction.
 #include "vs_common.h"
 #include "vs_host.h"
 
@@ -25,7 +26,8 @@ constexpr int DPARTS = DNT / DK;  // threads per candidate
 constexpr int DSMAX = 8;        // slots per block (dflash.py BLOCK - 1 = 7)
 constexpr int DRMAX = 256;      // rank (dflash.py RANK)
 constexpr int DM = DRMAX / DPARTS;  // rank entries per thread at most
-constexpr int DROWS = 1 + (DSMAX - 1) * DK;  // predecessor rows: the anchor and every non-final slot's candidates
+constexpr int DROWS = 1 + (DSMAX - 1) * DK;  // predecessor rows: the anchor and every non-final slot's 16 positions
+static_assert((DROWS + DSMAX) * DRMAX * 4 <= 160 * 1024 - 1024, "predecessor rows and hp fit the LDS");
 
 struct WalkArgs {
   const float* uval;     // [n, S, ldk] candidate logits, value descending
@@ -37,101 +39,159 @@ struct WalkArgs {
   const int32_t* anchor; // [n]
   int32_t* out;          // [n, S]
   int n, S, K, R, vocab;
+  unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
+// Raw bf16 part of a row (thread part p: M entries from p*M on), packed two per 32-bit word. M == 0: run-time m
+// (any R % 16 == 0), element loads; M = 8 or 16: 16-byte loads.
+template <int M>
+struct Part16 {
+  uint32_t w[DM / 2];
+};
+
+template <int M>
+__device__ __forceinline__ void load_part(const uint16_t* row, int m, Part16<M>& d) {
+  if constexpr (M == 0) {
+#pragma unroll
+    for (int i = 0; i < DM / 2; ++i) {
+      const uint32_t lo = 2 * i < m ? row[2 * i] : 0u, hi = 2 * i + 1 < m ? row[2 * i + 1] : 0u;
+      d.w[i] = lo | (hi << 16);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < M / 8; ++q) {
+      const uint4 r = ((const uint4*)row)[q];
+      d.w[4 * q] = r.x;
+      d.w[4 * q + 1] = r.y;
+      d.w[4 * q + 2] = r.z;
+      d.w[4 * q + 3] = r.w;
+    }
+#pragma unroll
+    for (int i = M / 2; i < DM / 2; ++i) d.w[i] = 0u;
+  }
+}
+
+template <int M>
+__device__ __forceinline__ float part_get(const Part16<M>& d, int i) {
+  const uint32_t w = d.w[i >> 1];
+  return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+
+template <int M>
 __global__ __launch_bounds__(DNT) void vs_draft_walk_kernel(WalkArgs W) {
-  __shared__ uint16_t sA[DROWS * DRMAX];
-  __shared__ float sS[2][DK];
+  // sA row 0 = A[anchor] * hp[0]; row 1 + e*DK + c = A[cid[e][c]] * hp[e + 1]: a predecessor row is only ever
+  // used by the slot after its own, so it is stored already multiplied by that slot's hp (rounded to fp32 as in
+  // a = float32(A[pred]) * hp[e]).
+  __shared__ float sA[DROWS][DRMAX];
+  __shared__ float sH[DSMAX][DRMAX];  // hp of the block
+  __shared__ float sS[2][DK];         // the current slot's scores (double-buffered across slots)
+  __shared__ int sId[DSMAX][DK];      // candidate ids, -1 where invalid
   const int blk = blockIdx.x, t = threadIdx.x;
   const int c = t / DPARTS, p = t % DPARTS;
-  const int S = W.S, K = W.K, R = W.R, m = R / DPARTS;
+  const int S = W.S, K = W.K, R = W.R, m = M ? M : R / DPARTS;
   const float* uv = W.uval + (size_t)blk * S * W.ldk;
   const int32_t* cd = W.cid + (size_t)blk * S * W.ldk;
   const float* hpb = W.hp + (size_t)blk * S * R;
+  VS_TR_DECL(W);
+  VS_TR(W, 0);
 
-  // ---- path-independent operands: this thread's candidate id, logit, successor part and hp part of every slot
+  // ---- path-independent operands. Every load is unconditional (indices clamped into the arrays, results masked
+  // afterwards) and issued before any is consumed, so the fetch costs two memory latencies: the candidate ids and
+  // the anchor, then the rows they name.
+  const int a0 = W.anchor[blk];
+  const int cc0 = c < K ? c : K - 1;
   int id[DSMAX];
   float u[DSMAX];
-  float hv[DSMAX][DM];
-  float bv[DSMAX][DM];
 #pragma unroll
   for (int e = 0; e < DSMAX; ++e) {
-    id[e] = -1;
-    u[e] = 0.0f;
-    if (e < S && c < K) {
-      const int x = cd[e * W.ldk + c];
-      id[e] = (x >= 0 && x < W.vocab) ? x : -1;
-      u[e] = uv[e * W.ldk + c];
-    }
+    const int ee = e < S ? e : S - 1;
+    id[e] = cd[ee * W.ldk + cc0];
+    u[e] = uv[ee * W.ldk + cc0];
   }
+  constexpr int HPT = DSMAX * DRMAX / DNT;  // hp elements per thread (S * R <= DSMAX * DRMAX)
+  float hq[HPT];
 #pragma unroll
-  for (int e = 0; e < DSMAX; ++e) {
-    const uint16_t* brow = W.Bc + (size_t)(id[e] < 0 ? 0 : id[e]) * R + p * m;
-    const float* hrow = hpb + (size_t)(e < S ? e : 0) * R + p * m;
-#pragma unroll
-    for (int i = 0; i < DM; ++i) {
-      bv[e][i] = (i < m) ? bf16_to_f32(brow[i]) : 0.0f;
-      hv[e][i] = (i < m) ? hrow[i] : 0.0f;
-    }
+  for (int j = 0; j < HPT; ++j) {
+    const int i = j * DNT + t;
+    hq[j] = hpb[i < S * R ? i : 0];
   }
-  // ---- predecessor rows to LDS: slot 0 = the anchor, slot 1 + e*K + c = cid[e][c] (e < S - 1)
-  const int a0 = W.anchor[blk];
+  // keep the scheduler from interleaving each load with its use (it would wait on every load in turn)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int e = 0; e < DSMAX; ++e) id[e] = (e < S && c < K && id[e] >= 0 && id[e] < W.vocab) ? id[e] : -1;
   const bool anchor_ok = a0 >= 0 && a0 < W.vocab;
-  const int nrows = 1 + (S - 1) * K;
-  const int wpr = R / 2;  // 32-bit words per row (R is even)
-  for (int i = t; i < nrows * wpr; i += DNT) {
-    const int rr = i / wpr, wd = i - rr * wpr;
-    int src = -1;
-    if (rr == 0) {
-      src = anchor_ok ? a0 : -1;
-    } else {
-      const int e = (rr - 1) / K, cc = (rr - 1) - e * K;
-      const int x = cd[e * W.ldk + cc];
-      src = (x >= 0 && x < W.vocab) ? x : -1;
-    }
-    const uint32_t v = src >= 0 ? ((const uint32_t*)(W.A + (size_t)src * R))[wd] : 0u;
-    ((uint32_t*)(sA + rr * DRMAX))[wd] = v;
+  Part16<M> bq[DSMAX], aq[DSMAX];  // successor rows of every slot; predecessor rows (slots 0..S-2, then the anchor)
+#pragma unroll
+  for (int e = 0; e < DSMAX; ++e) load_part<M>(W.Bc + (size_t)(id[e] < 0 ? 0 : id[e]) * R + p * m, m, bq[e]);
+#pragma unroll
+  for (int e = 0; e < DSMAX - 1; ++e) load_part<M>(W.A + (size_t)(id[e] < 0 ? 0 : id[e]) * R + p * m, m, aq[e]);
+  load_part<M>(W.A + (size_t)(anchor_ok ? a0 : 0) * R + p * m, m, aq[DSMAX - 1]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < HPT; ++j) {
+    const int i = j * DNT + t;
+    if (i < S * R) sH[i / R][i % R] = hq[j];
+  }
+  if (p == 0) {
+#pragma unroll
+    for (int e = 0; e < DSMAX; ++e) sId[e][c] = id[e];
   }
   __syncthreads();
+#pragma unroll
+  for (int e = 0; e < DSMAX - 1; ++e) {
+    if (e + 1 < S) {
+#pragma unroll
+      for (int i = 0; i < DM; ++i)
+        if (i < m) sA[1 + e * DK + c][p * m + i] = part_get(aq[e], i) * sH[e + 1][p * m + i];
+    }
+  }
+  if (c == 0) {
+#pragma unroll
+    for (int i = 0; i < DM; ++i)
+      if (i < m) sA[0][p * m + i] = part_get(aq[DSMAX - 1], i) * sH[0][p * m + i];
+  }
+  __syncthreads();
+  VS_TR(W, 1);
 
-  // ---- the walk
-  int slot = anchor_ok ? 0 : -1;  // LDS row of pred; -1 once no valid predecessor remains
+  // ---- the walk: registers and LDS only
+  const int lc = lane_id() & (DK - 1);  // the candidate this lane reads back for the first-max reduction
+  int slot = anchor_ok ? 0 : -1;       // LDS row of pred; -1 once no valid predecessor remains
 #pragma unroll
   for (int e = 0; e < DSMAX; ++e) {
     if (e < S) {
       float acc = 0.0f;
-      const uint16_t* arow = sA + (slot < 0 ? 0 : slot) * DRMAX + p * m;
+      const float* arow = &sA[slot < 0 ? 0 : slot][p * m];
 #pragma unroll
-      for (int i = 0; i < DM; ++i) {
-        if (i < m) {
-          const float a = bf16_to_f32(arow[i]) * hv[e][i];  // A[pred] * hp[e], rounded to fp32
-          acc = acc + bv[e][i] * a;
-        }
-      }
+      for (int i = 0; i < DM; ++i)
+        if (i < m) acc = acc + part_get(bq[e], i) * arow[i];
       acc = acc + lane_xor<1>(acc);
       acc = acc + lane_xor<2>(acc);
       acc = acc + lane_xor<4>(acc);
       acc = acc + lane_xor<8>(acc);
-      if (p == 0 && c < K) sS[e & 1][c] = id[e] >= 0 ? u[e] + acc : -__builtin_inff();
+      if (p == 0) sS[e & 1][c] = u[e] + acc;
       __syncthreads();
-      // every thread resolves the same first maximum over the valid candidates
-      int best = -1;
-      float bs = 0.0f;
-      for (int cc = 0; cc < K; ++cc) {
-        const int x = cd[e * W.ldk + cc];
-        if (x < 0 || x >= W.vocab) continue;
-        const float s = sS[e & 1][cc];
-        if (best < 0 || s > bs) {
-          best = cc;
-          bs = s;
-        }
-      }
-      if (slot < 0) best = -1;
-      const int tok = best < 0 ? -1 : cd[e * W.ldk + best];
+      // first maximum over the valid candidates, in every 16-lane group: key = score order, then the lower
+      // position; 0 = no valid candidate (a valid key is never 0: ord32 of a non-NaN float is non-zero)
+      const float sc = sS[e & 1][lc];
+      const int cid_l = sId[e][lc];
+      const float scn = sc != sc ? -__builtin_inff() : sc;  // a NaN score ranks as -inf
+      u64 key = (cid_l >= 0 && lc < K) ? ((u64)ord32(scn) << 32) | (u64)(DK - 1 - lc) : (u64)0;
+      u64 o = lane_xor<1>(key);
+      key = o > key ? o : key;
+      o = lane_xor<2>(key);
+      key = o > key ? o : key;
+      o = lane_xor<4>(key);
+      key = o > key ? o : key;
+      o = lane_xor<8>(key);
+      key = o > key ? o : key;
+      const int best = (key == 0 || slot < 0) ? -1 : DK - 1 - (int)(key & (DK - 1));
+      const int tok = best < 0 ? -1 : sId[e][best];
       if (t == 0) W.out[(size_t)blk * S + e] = tok;
-      slot = best < 0 ? -1 : 1 + e * K + best;
+      slot = best < 0 ? -1 : 1 + e * DK + best;
+      VS_TR(W, 2 + e);
     }
   }
+  VS_TR_FLUSH(W);
 }
 
 }  // namespace vs
@@ -150,9 +210,15 @@ extern "C" int vs_draft_walk(const float* uval, const int32_t* cid, int ldk, con
   if (R < DPARTS || R > DRMAX || R % DPARTS != 0)
     return fail(VS_EINVAL, "vs_draft_walk: rank must be a multiple of 16 in [16, 256]");
   if (vocab < 1) return fail(VS_EINVAL, "vs_draft_walk: vocab < 1");
-  if ((uintptr_t)A % 4 != 0) return fail(VS_EINVAL, "vs_draft_walk: predecessor codebook not 4-byte aligned");
-  WalkArgs w{uval, cid, ldk, hp, (const uint16_t*)A, (const uint16_t*)B, anchor, out, n, S, K, R, vocab};
-  hipLaunchKernelGGL(vs_draft_walk_kernel, dim3(n), dim3(DNT), 0, (hipStream_t)stream, w);
+  WalkArgs w{uval, cid, ldk, hp, (const uint16_t*)A, (const uint16_t*)B, anchor, out, n, S, K, R, vocab, g_trace};
+  // 16-byte loads where every part is 16-byte aligned: rank 128 or 256 with aligned codebooks
+  const bool vec = ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0);
+  if (vec && R == 256)
+    hipLaunchKernelGGL(vs_draft_walk_kernel<16>, dim3(n), dim3(DNT), 0, (hipStream_t)stream, w);
+  else if (vec && R == 128)
+    hipLaunchKernelGGL(vs_draft_walk_kernel<8>, dim3(n), dim3(DNT), 0, (hipStream_t)stream, w);
+  else
+    hipLaunchKernelGGL(vs_draft_walk_kernel<0>, dim3(n), dim3(DNT), 0, (hipStream_t)stream, w);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "vs_draft_walk: launch");
   return VS_OK;

@@ -394,3 +394,37 @@ def draft_propose(logits: torch.Tensor, hp: torch.Tensor, A: torch.Tensor, B: to
                              A.data_ptr(), B.data_ptr(), vocab, R, anchor.data_ptr(), out.data_ptr(), ws.data_ptr(),
                              ws.numel(), _stream_handle(dev)), "vs_draft_propose")
     return out
+
+
+class PreparedPropose:
+    """vs_draft_propose with every argument bound once (see PreparedSample): __call__(i) runs the top-16 and the
+    walk on logits slot i ([n, S, V] each) into self.out."""
+
+    def __init__(self, logits_slots: Sequence[torch.Tensor], hp: torch.Tensor, A: torch.Tensor, B: torch.Tensor,
+                 anchor: torch.Tensor, vocab_valid: Optional[int] = None):
+        vocab, R = _codebooks(A, B)
+        x0 = logits_slots[0]
+        _require_cuda(x0, "logits")
+        if x0.dim() != 3 or x0.stride(2) != 1 or x0.stride(0) != x0.shape[1] * x0.stride(1):
+            raise ValueError("logits must be [n, S, V] with rows evenly strided")
+        n, S, V = x0.shape
+        vv = V if vocab_valid is None else int(vocab_valid)
+        hp = hp.to(torch.float32).contiguous()
+        anchor = anchor.reshape(n).to(torch.int32).contiguous()
+        if tuple(hp.shape) != (n, S, R):
+            raise ValueError("hp must be [n, S, rank]")
+        self.dev = x0.device
+        self.out = torch.empty(n, S, dtype=torch.int32, device=self.dev)
+        L = _lib.load()
+        self._fn = L.vs_draft_propose
+        ws = workspace(self.dev, L.vs_draft_workspace_bytes(n, S, vv), "draft")
+        self._slots = [x.data_ptr() for x in logits_slots]
+        self._keep = (list(logits_slots), hp, A, B, anchor, ws)
+        self._rest = (_DTYPES[x0.dtype], n, S, vv, x0.stride(1), hp.data_ptr(), A.data_ptr(), B.data_ptr(), vocab,
+                      R, anchor.data_ptr(), self.out.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
+
+    def __call__(self, slot: int = 0) -> torch.Tensor:
+        rc = self._fn(self._slots[slot], *self._rest)
+        if rc:
+            check(rc, "vs_draft_propose")
+        return self.out
