@@ -12,7 +12,9 @@ Infinity Cache. Printed (one JSON line on stdout):
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
 is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts);
-"draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary.
+"draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary;
+"lmhead_verify_*" is the bf16 lm_head with greedy verify fused in (vs_lmhead_verify_greedy), beside the unfused
+torch matmul + vs_verify_greedy.
 """
 import argparse
 import json
@@ -150,6 +152,36 @@ def bench_draft(torch, dev, steps, warmup, nslots):
     return cold, warm, algo
 
 
+LMH_N, LMH_VV, LMH_K = 248320, 248077, 5120
+
+
+def bench_lmhead(torch, dev, steps, warmup, B=1, T=17):
+    """lm_head + greedy verify at the model's head (volundr.py:958-968: hidden 5120 -> vocab 248320, bf16) for B
+    requests of T positions: the fused kernel (vs_lmhead_verify_greedy) and, for comparison, torch's bf16 matmul
+    (hipBLASLt) writing the logits followed by vs_verify_greedy reading them."""
+    from volundr_amd import ops
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    h = torch.randn(B, T, LMH_K, generator=g, device=dev).to(torch.bfloat16)
+    W = (torch.randn(LMH_N, LMH_K, generator=g, device=dev) / 16).to(torch.bfloat16)
+    drafts = torch.randint(0, LMH_VV, (B, T - 1), generator=g, device=dev, dtype=torch.int32)
+    out = ops.VerifyOut(torch.empty(B, T, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int32, device=dev),
+                        torch.empty(B, T, dtype=torch.float32, device=dev))
+    fused = lambda i: ops.lmhead_verify_greedy(h, W, drafts, vocab_valid=LMH_VV, out=out)  # noqa: E731
+    lg = torch.empty(B * T, LMH_N, dtype=torch.bfloat16, device=dev)
+    h2 = h.reshape(B * T, LMH_K)
+
+    def unfused(i):
+        torch.matmul(h2, W.T, out=lg)
+        ops.verify_greedy(lg.view(B, T, LMH_N), drafts, LMH_VV)
+
+    st = max(steps // 10, 10)
+    f = time_calls(torch, fused, 1, st, max(warmup // 10, 3))
+    u = time_calls(torch, unfused, 1, st, max(warmup // 10, 3))
+    algo = LMH_N * LMH_K * 2 + B * T * LMH_K * 2 + B * T * 8 + B * 4
+    return f, u, algo
+
+
 def cpu_baseline(d, budget_s=10.0):
     """The oracle (NumPy restatement of sampler.py) row by row, single-threaded, for about budget_s seconds."""
     from oracle import sampler_ref as S
@@ -246,6 +278,14 @@ def main():
             others[name] = entry(oe, ok, we, ab, nt)
         (oe, ok), (we, wk), ab = bench_draft(torch, dev, a.steps, a.warmup, a.slots)
         others["draft_propose"] = entry(oe, ok, we, ab, DRAFT_S)
+        for (bb, tt) in ((1, 17), (4, 17)):
+            (fe, fk), (ue, uk), ab = bench_lmhead(torch, dev, a.steps, a.warmup, bb, tt)
+            key = f"lmhead_verify_b{bb}t{tt}"
+            others[key] = entry(fe, fk, fe, ab, bb * tt)
+            others[key]["workload"] = (f"bf16 lm_head 5120 -> 248320 + greedy verify, B={bb} T={tt}: fused kernel; "
+                                       "'unfused_us_per_step' = torch bf16 matmul (logits to HBM) + vs_verify_greedy")
+            others[key]["unfused_us_per_step"] = round(ue, 2)
+            others[key]["frac_of_8tbs"] = round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)
         others["draft_propose"]["workload"] = ("DFlash2 propose: top-16 of bf16 logits [7, 248320] (248077 valid) + "
                                                "7-slot walk, rank-256 codebooks; 2 kernels per step")
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)

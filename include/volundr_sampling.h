@@ -131,6 +131,23 @@ int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t
 
 size_t vs_verify_workspace_bytes(int B, int T, int V);
 
+/* The bf16 lm_head GEMM with greedy verify fused into its epilogue: logits = bf16(h @ W^T) (one rounding, nearest
+ * even, of a float32 sum of products) are reduced in registers and never written unless out_logits is given.
+ *   h          : bf16 [B*T, ldh] final hidden states (row b*T + t), 16-byte aligned, ldh % 8 == 0
+ *   W          : bf16 [N, ldw] lm_head weight (vocab_size rows of K = hidden), 16-byte aligned, ldw % 8 == 0
+ *   K          : hidden size, a multiple of 256;  B*T <= 80
+ *   drafts, out_argmax, out_accept, out_logprob : as vs_verify_greedy (first-max argmax over [0, vocab_valid))
+ *   out_logits : bf16 [B*T, ldo] or NULL (testing / callers that need the rows; costs the logits write)
+ *   ws         : device workspace of at least vs_lmhead_workspace_bytes(B, T) bytes, zeroed once beforehand
+ * Replaces: volundr-mlx/volundr.py:958-968 (lm_head, bf16) with spec/verify.py:223 feeding spec/specdec.py:326-327
+ * (argmax + accept), in one launch. */
+int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K, int vocab_valid,
+                            int B, int T, const int32_t* drafts, int32_t* out_argmax, int32_t* out_accept,
+                            float* out_logprob, void* out_logits, int64_t ldo, void* ws, size_t ws_bytes,
+                            vs_stream_t stream);
+
+size_t vs_lmhead_workspace_bytes(int B, int T);
+
 /* The k largest logits of each of B rows, value descending, ties to the lower id (rows with fewer than k finite
  * logits pad with id -1 and value -inf). 1 <= k <= 256 (less when V needs many workgroups per row; the call fails
  * with VS_EINVAL above the shape's limit). Values are the logits widened to float32.
@@ -169,7 +186,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 3. */
+/* Library ABI version (increments on any signature or struct change): 4. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -48,7 +48,7 @@ extern "C" {
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 3; }
+int vs_version(void) { return 4; }
 
 #ifdef VS_TRACE
 void vs_debug_set_trace(void* p) { vs::g_trace = (unsigned long long*)p; }

@@ -1,0 +1,482 @@
+// vs_lmhead.hip - the bf16 lm_head GEMM with the greedy-verify epilogue fused in, for gfx950: logits are never
+// written to HBM; each workgroup reduces its slice of the vocabulary to per-position (first-max key, max, sum-exp)
+// partials and a second small launch merges them into argmax, accept length and logprob.
+//
+// Reference: logits = lm_head(h) in bf16 (volundr-mlx/volundr.py:958-968, bf16 weight [vocab_size, hidden]; spec
+// verify's head call, spec/verify.py:223), then tok = argmax(logits[:, :vv]) and nacc = sum(cumprod(inp[1:] ==
+// tok[:-1])) (spec/specdec.py:326-327, scheduler.py:462-463). The logits here are bf16(fp32 sum of products), as a
+// bf16 matmul produces them; the epilogue is the verify kernel's (first-max argmax over the bf16 values, logprob =
+// x[tok] - logsumexp(x[:vv])).
+//
+// Shape of the work: R = B*T positions (<= 80) x N vocabulary rows x K hidden, R tiny. The weight (N*K*2 bytes,
+// 2.54 GB at 248320 x 5120) is read exactly once and dominates: the kernel is HBM-bound. Design:
+//  * one 512-thread workgroup per CU (persistent over a contiguous range of 16-row vocabulary tiles);
+//  * v_mfma_f32_16x16x32_bf16 with the weight as the A operand, loaded straight from HBM into registers: lane
+//    (m = l%16, g = l/16) holds W[row m][k + 8g .. 8g + 7]; the loads are arranged so that each instruction reads
+//    whole 128-byte runs of 8 rows, and the operands are rebuilt with one DPP lane rotation; one two-step group of
+//    loads per tile is in flight per wave;
+//  * the hidden rows (B operand) are staged through LDS in 256-wide k-chunks, double-buffered, shared by the 8 waves
+//    (each workgroup reads h once: 256 x R x K x 2 bytes of L2 traffic in all);
+//  * accumulators stay in VGPRs for the whole K loop; the epilogue rounds each to bf16 and folds it into running
+//    per-lane partials.
+#include "vs_common.h"
+#include "vs_host.h"
+
+#pragma clang fp contract(off)
+
+namespace vs {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+#ifndef LH_NT
+#define LH_NT 512
+#endif
+constexpr int LNT = LH_NT;          // threads per workgroup
+constexpr int LNW = LNT / WAVE;     // waves per workgroup
+#ifndef LH_KC
+#define LH_KC 512
+#endif
+#ifndef LH_NTW12
+#define LH_NTW12 4
+#endif
+#ifndef LH_WPC
+#define LH_WPC 1
+#endif
+constexpr int KS = 32;              // k per MFMA
+constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
+constexpr int LPMAX = 2048;         // workgroups per launch
+static_assert(LH_KC % (2 * KS) == 0, "a chunk holds whole two-step groups");
+
+struct LPart {
+  u64 amkey;
+  float mf;
+  uint32_t pad;
+  double se;
+  u64 pad2;
+};
+static_assert(sizeof(LPart) == 32, "LPart layout");
+
+struct LHArgs {
+  const uint16_t* h;  // [R, ldh] bf16
+  int64_t ldh;
+  const uint16_t* W;  // [N, ldw] bf16
+  int64_t ldw;
+  int N, vv, K, B, T, R, ntiles;
+  const int32_t* drafts;  // [B, T-1]
+  int32_t* out_argmax;    // [R]
+  int32_t* out_accept;    // [B]
+  float* out_lp;          // [R] or null
+  uint16_t* out_logits;   // [R, ldo] bf16 or null
+  int64_t ldo;
+  char* ws;  // LPart [P][R]: the workgroup partials
+  unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
+};
+
+// float32 -> bf16, round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// (m, s) pairs: s = sum exp(x - m) over finite x, accumulated in float64; the rescale factor exp(m - mm) <= 1 is a
+// float32 expf (relative error ~1e-7, far inside the logprob tolerance; a float64 exp per merge step made the
+// cross-lane and cross-workgroup merges cost tens of microseconds)
+__device__ __forceinline__ void lse_merge(float& m, double& s, float m2, double s2) {
+  const float mm = m2 > m ? m2 : m;
+  double r = 0.0;
+  if (s > 0.0 && is_finite(mm)) r += s * (double)expf(m - mm);
+  if (s2 > 0.0 && is_finite(mm)) r += s2 * (double)expf(m2 - mm);
+  m = mm;
+  s = r;
+}
+
+template <int NTT, int NTW>
+__global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 * LH_WPC))) void vs_lmhead_verify_kernel(
+    LHArgs A) {
+  constexpr int RP = 16 * NTT;  // positions padded to whole MFMA tiles
+  constexpr int KC = NTT <= 2 ? LH_KC : 256;  // k per LDS chunk (two chunks of RP rows fit the LDS)
+  constexpr int SPC = KC / KS;
+  constexpr int HSTR = KC + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t hs[2][RP][HSTR];
+  __shared__ u64 rk[LNW][RP];
+  __shared__ float rm[LNW][RP];
+  __shared__ double rs[LNW][RP];
+  const int t = threadIdx.x, wv = t / WAVE, ln = lane_id();
+  const int m16 = ln & 15, kg = ln >> 4;
+  const int P = gridDim.x, wg = blockIdx.x;
+  const int R = A.R, K = A.K;
+  const int nchunks = K / KC;
+  const int t0 = (int)((long long)wg * A.ntiles / P), t1 = (int)((long long)(wg + 1) * A.ntiles / P);
+  const int rounds = (t1 - t0 + LNW * NTW - 1) / (LNW * NTW);
+  LPart* parts = (LPart*)A.ws;
+  VS_TR_DECL(A);
+  VS_TR(A, 0);
+  // accept lengths start at T-1 (every draft accepted); the merge kernel lowers them to the first mismatch
+  if (wg == 0 && t < A.B) A.out_accept[t] = A.T - 1;
+
+  // padded positions R..RP-1 read as zeros in both buffers
+  {
+    const int per = (RP - R) * (KC / 8);
+    for (int i = t; i < 2 * per; i += LNT) {
+      const int b = i / per, rem = i - b * per;
+      *(uint4*)&hs[b][R + rem / (KC / 8)][(rem % (KC / 8)) * 8] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  // per-lane running partials of its positions tt*16 + m16
+  u64 pk[NTT];
+  float pm[NTT];
+  double ps[NTT];
+#pragma unroll
+  for (int tt = 0; tt < NTT; ++tt) {
+    pk[tt] = 0;
+    pm[tt] = -__builtin_inff();
+    ps[tt] = 0.0;
+  }
+  const int hpieces = R * (KC / 8);  // 16-byte pieces of one hidden chunk
+  constexpr int HPT = RP * (KC / 8) / LNT;  // pieces per thread (R <= RP rows)
+  static_assert(HPT * LNT == RP * (KC / 8), "the threads cover a padded chunk exactly");
+  // this thread's pieces: (row, column) in the chunk, clamped into range (the clamped ones are not stored)
+  int hrow[HPT], hcol[HPT];
+  bool hin[HPT];
+#pragma unroll
+  for (int q = 0; q < HPT; ++q) {
+    const int i0 = q * LNT + t;
+    hin[q] = i0 < hpieces;
+    const int i = hin[q] ? i0 : hpieces - 1;
+    hrow[q] = i / (KC / 8);
+    hcol[q] = (i % (KC / 8)) * 8;
+  }
+  for (int r = 0; r < rounds; ++r) {
+    // Weight fetch, two MFMA steps (64 k = 128 bytes of a row) at a time, so that every load instruction reads whole
+    // 128-byte runs of 8 rows (an instruction reading 64 bytes from each of 16 rows streams at ~60% of the rate):
+    // half 0 reads rows 0-7 of the tile, half 1 rows 8-15; lane (m, g) reads, of row m & 7 (+ 8 in half 1), the
+    // 16-byte piece g if it is its own row's half (m < 8 for half 0), else piece 4 + g, which belongs to its
+    // partner lane m ^ 8 in the second step. Step 0 takes the own-half register; step 1 takes the other register
+    // from the partner lane (DPP row rotate by 8 inside each 16-lane row).
+    // Addresses: a 64-bit base per round (the round's first tile, uniform) plus 32-bit byte offsets per lane and
+    // tile (a round spans < 4 GB: LNW*NTW tiles of 16 rows of at most ldw*2 bytes, checked on the host).
+    const bool lo8 = m16 < 8;
+    int tile[NTW];
+    const int tb = t0 + r * LNW * NTW;
+    const char* wbase = (const char*)(A.W + (int64_t)tb * 16 * A.ldw);
+    uint32_t wo0[NTW], wo1[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      tile[j] = tb + j * LNW + wv;
+      // a tile past the range reads the range's last tile (its lines are being fetched for another wave anyway)
+      const int tl = tile[j] < t1 ? tile[j] : t1 - 1;
+      int r0 = tl * 16 + (m16 & 7), r1 = r0 + 8;
+      r0 = (r0 < A.N ? r0 : A.N - 1) - tb * 16;
+      r1 = (r1 < A.N ? r1 : A.N - 1) - tb * 16;
+      wo0[j] = (uint32_t)((int64_t)r0 * A.ldw * 2) + (uint32_t)((lo8 ? kg : 4 + kg) * 16);
+      wo1[j] = (uint32_t)((int64_t)r1 * A.ldw * 2) + (uint32_t)((lo8 ? 4 + kg : kg) * 16);
+    }
+    f32x4_t acc[NTW][NTT];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+      for (int tt = 0; tt < NTT; ++tt) acc[j][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // the staged pieces live in named registers (an array of them was kept in scratch memory)
+    uint4 hr0, hr1, hr2, hr3, hr4;
+    static_assert(HPT <= 5, "at most five staged pieces per thread");
+    {
+      const uint16_t* hbase = A.h + (int64_t)(0) * KC;
+      hr0 = *(const uint4*)(hbase + (int64_t)hrow[0] * A.ldh + hcol[0]);
+      if constexpr (HPT > 1) hr1 = *(const uint4*)(hbase + (int64_t)hrow[1] * A.ldh + hcol[1]);
+      if constexpr (HPT > 2) hr2 = *(const uint4*)(hbase + (int64_t)hrow[2] * A.ldh + hcol[2]);
+      if constexpr (HPT > 3) hr3 = *(const uint4*)(hbase + (int64_t)hrow[3] * A.ldh + hcol[3]);
+      if constexpr (HPT > 4) hr4 = *(const uint4*)(hbase + (int64_t)hrow[4] * A.ldh + hcol[4]);
+    }
+    const int ngroups = K / (2 * KS);
+    uint4 wb[NTW][2];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      wb[j][0] = *(const uint4*)(wbase + wo0[j]);
+      wb[j][1] = *(const uint4*)(wbase + wo1[j]);
+    }
+    __syncthreads();  // the previous round's reads of buffer 0 are done
+    {
+      if (hin[0]) *(uint4*)&hs[0][hrow[0]][hcol[0]] = hr0;
+      if constexpr (HPT > 1) if (hin[1]) *(uint4*)&hs[0][hrow[1]][hcol[1]] = hr1;
+      if constexpr (HPT > 2) if (hin[2]) *(uint4*)&hs[0][hrow[2]][hcol[2]] = hr2;
+      if constexpr (HPT > 3) if (hin[3]) *(uint4*)&hs[0][hrow[3]][hcol[3]] = hr3;
+      if constexpr (HPT > 4) if (hin[4]) *(uint4*)&hs[0][hrow[4]][hcol[4]] = hr4;
+    }
+    __syncthreads();
+    VS_TR(A, 1 + 3 * r);
+    for (int c = 0; c < nchunks; ++c) {
+      const int b = c & 1;
+      // the next chunk's hidden rows are fetched now and stored after this chunk's steps (on the last chunk the
+      // same chunk is fetched again and stored into the idle buffer, which nothing reads before the next round
+      // rewrites it behind a barrier)
+      const int cn = c + 1 < nchunks ? c + 1 : c;
+      {
+      const uint16_t* hbase = A.h + (int64_t)(cn) * KC;
+      hr0 = *(const uint4*)(hbase + (int64_t)hrow[0] * A.ldh + hcol[0]);
+      if constexpr (HPT > 1) hr1 = *(const uint4*)(hbase + (int64_t)hrow[1] * A.ldh + hcol[1]);
+      if constexpr (HPT > 2) hr2 = *(const uint4*)(hbase + (int64_t)hrow[2] * A.ldh + hcol[2]);
+      if constexpr (HPT > 3) hr3 = *(const uint4*)(hbase + (int64_t)hrow[3] * A.ldh + hcol[3]);
+      if constexpr (HPT > 4) hr4 = *(const uint4*)(hbase + (int64_t)hrow[4] * A.ldh + hcol[4]);
+    }
+#pragma unroll
+      for (int gq = 0; gq < SPC / 2; ++gq) {
+        bf16x8_t hb0[NTT], hb1[NTT];
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+          hb0[tt] = *(const bf16x8_t*)&hs[b][tt * 16 + m16][(2 * gq) * KS + kg * 8];
+          hb1[tt] = *(const bf16x8_t*)&hs[b][tt * 16 + m16][(2 * gq + 1) * KS + kg * 8];
+        }
+        int gn = c * (SPC / 2) + gq + 1;  // the group fetched now (clamped: one spare fetch at the end)
+        gn = gn < ngroups ? gn : ngroups - 1;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const uint4 a0 = wb[j][0], a1 = wb[j][1];
+          const uint4 s0 = lo8 ? a0 : a1;
+          const uint4 o = lo8 ? a1 : a0;
+          uint4 s1;
+          s1.x = dpp32<0x128>(o.x, o.x);  // row_ror:8 -> the value of lane m ^ 8
+          s1.y = dpp32<0x128>(o.y, o.y);
+          s1.z = dpp32<0x128>(o.z, o.z);
+          s1.w = dpp32<0x128>(o.w, o.w);
+          wb[j][0] = *(const uint4*)(wbase + (wo0[j] + (uint32_t)gn * 4 * KS));
+          wb[j][1] = *(const uint4*)(wbase + (wo1[j] + (uint32_t)gn * 4 * KS));
+#ifndef LH_NO_PIN
+          __builtin_amdgcn_sched_barrier(0);  // keep the next group's loads here, one group ahead of their use
+#endif
+#ifdef LH_DIAG_ONE_TT
+          for (int tt = 0; tt < 1; ++tt) {
+#else
+#pragma unroll
+          for (int tt = 0; tt < NTT; ++tt) {
+#endif
+            acc[j][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, s0), hb0[tt],
+                                                                 acc[j][tt], 0, 0, 0);
+            acc[j][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, s1), hb1[tt],
+                                                                 acc[j][tt], 0, 0, 0);
+          }
+        }
+      }
+      {
+      if (hin[0]) *(uint4*)&hs[b ^ 1][hrow[0]][hcol[0]] = hr0;
+      if constexpr (HPT > 1) if (hin[1]) *(uint4*)&hs[b ^ 1][hrow[1]][hcol[1]] = hr1;
+      if constexpr (HPT > 2) if (hin[2]) *(uint4*)&hs[b ^ 1][hrow[2]][hcol[2]] = hr2;
+      if constexpr (HPT > 3) if (hin[3]) *(uint4*)&hs[b ^ 1][hrow[3]][hcol[3]] = hr3;
+      if constexpr (HPT > 4) if (hin[4]) *(uint4*)&hs[b ^ 1][hrow[4]][hcol[4]] = hr4;
+    }
+      __syncthreads();
+    }
+    VS_TR(A, 2 + 3 * r);
+    // epilogue of the round: lane holds vocabulary rows tile*16 + 4*kg + q of positions tt*16 + m16
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) {
+      const int pos = tt * 16 + m16;
+      float vm = -__builtin_inff();
+      float xs[NTW][4];
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int v = tile[j] * 16 + kg * 4 + q;
+          const uint16_t xb = f32_to_bf16_rne(acc[j][tt][q]);
+          const float x = bf16_to_f32(xb);
+          const bool in = tile[j] < t1 && v < A.vv;
+          if (A.out_logits && tile[j] < t1 && v < A.N && pos < R) A.out_logits[(int64_t)pos * A.ldo + v] = xb;
+          xs[j][q] = in ? x : -__builtin_inff();
+          if (in) {
+            const u64 k = amkey64(x, (uint32_t)v);
+            pk[tt] = k > pk[tt] ? k : pk[tt];
+          }
+          if (in && is_finite(x)) vm = x > vm ? x : vm;
+        }
+      }
+      if (vm > pm[tt]) {
+        if (ps[tt] > 0.0) ps[tt] *= (double)expf(pm[tt] - vm);
+        pm[tt] = vm;
+      }
+      if (is_finite(pm[tt])) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (is_finite(xs[j][q])) sacc += expf(xs[j][q] - pm[tt]);
+        ps[tt] += (double)sacc;
+      }
+    }
+  }
+
+  // lanes of one position (same m16): xor 16, 32; then the waves through LDS; then the workgroup partial
+#pragma unroll
+  for (int tt = 0; tt < NTT; ++tt) {
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh *= 2) {
+      const u64 ok = sh == 16 ? lane_xor<16>(pk[tt]) : lane_xor<32>(pk[tt]);
+      const float om = sh == 16 ? lane_xor<16>(pm[tt]) : lane_xor<32>(pm[tt]);
+      const double os = sh == 16 ? lane_xor<16>(ps[tt]) : lane_xor<32>(ps[tt]);
+      pk[tt] = ok > pk[tt] ? ok : pk[tt];
+      lse_merge(pm[tt], ps[tt], om, os);
+    }
+    if (kg == 0) {
+      rk[wv][tt * 16 + m16] = pk[tt];
+      rm[wv][tt * 16 + m16] = pm[tt];
+      rs[wv][tt * 16 + m16] = ps[tt];
+    }
+  }
+  __syncthreads();
+  if (t < R) {
+    u64 k = rk[0][t];
+    float m = rm[0][t];
+    double s = rs[0][t];
+#pragma unroll
+    for (int w = 1; w < LNW; ++w) {
+      k = rk[w][t] > k ? rk[w][t] : k;
+      lse_merge(m, s, rm[w][t], rs[w][t]);
+    }
+    LPart* pp = parts + (size_t)wg * R + t;
+    st_dev(&pp->amkey, k);
+    st_dev(&pp->mf, m);
+    st_dev(&pp->se, s);
+  }
+  VS_TR(A, 20);
+  VS_TR_FLUSH(A);
+}
+
+// Merge of the P workgroup partials of each position (one 256-thread workgroup per position; a separate launch so
+// the positions merge in parallel on as many CUs): first-max argmax, logprob, and the accept length as the lowest
+// mismatching draft position (specdec.py:327: nacc = leading matches), by atomicMin into out_accept.
+constexpr int MNT = 256;
+constexpr int MPT = LPMAX / MNT;  // partials per thread at most
+__global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
+  __shared__ u64 rk[MNT / WAVE];
+  __shared__ float rm[MNT / WAVE];
+  __shared__ double rs[MNT / WAVE];
+  const int pos = blockIdx.x, t = threadIdx.x, wv = t / WAVE, ln = lane_id();
+  const LPart* parts = (const LPart*)A.ws;
+  u64 kk[MPT];
+  float mm[MPT];
+  double ss[MPT];
+#pragma unroll
+  for (int u = 0; u < MPT; ++u) {  // every load issued before the first is used
+    const int i0 = u * MNT + t;
+    const int i = i0 < P ? i0 : P - 1;
+    const LPart* pp = parts + (size_t)i * A.R + pos;
+    kk[u] = ld_dev(&pp->amkey);  // device-coherent reads of the other workgroups' partials
+    mm[u] = ld_dev(&pp->mf);
+    ss[u] = ld_dev(&pp->se);
+  }
+  u64 k = 0;
+  float m = -__builtin_inff();
+  double s = 0.0;
+#pragma unroll
+  for (int u = 0; u < MPT; ++u) {
+    if (u * MNT + t < P) {
+      k = kk[u] > k ? kk[u] : k;
+      lse_merge(m, s, mm[u], ss[u]);
+    }
+  }
+  k = wave_max(k);
+#pragma unroll
+  for (int sh = 1; sh < WAVE; sh *= 2) {
+    const float om = lane_xor_rt(m, sh);
+    const double os = lane_xor_rt(s, sh);
+    lse_merge(m, s, om, os);
+  }
+  if (ln == 0) {
+    rk[wv] = k;
+    rm[wv] = m;
+    rs[wv] = s;
+  }
+  __syncthreads();
+  if (t == 0) {
+#pragma unroll
+    for (int w = 1; w < MNT / WAVE; ++w) {
+      k = rk[w] > k ? rk[w] : k;
+      lse_merge(m, s, rm[w], rs[w]);
+    }
+    const float xj = am_is_nan(k) ? __builtin_nanf("") : key_value(k);
+    const int32_t tok = (int32_t)key_index(k);
+    A.out_argmax[pos] = tok;
+    if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && s > 0.0) ? (float)((double)xj - ((double)m + log(s))) : 0.0f;
+    const int b = pos / A.T, tp = pos % A.T;
+    if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
+  }
+}
+
+template <int NTT, int NTW>
+static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
+  hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW>), dim3(P), dim3(LNT), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "vs_lmhead_verify_greedy: launch");
+  hipLaunchKernelGGL(vs_lmhead_merge_kernel, dim3(a.R), dim3(MNT), 0, stream, a, P);
+  e = hipGetLastError();
+  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_verify_greedy: launch");
+}
+
+}  // namespace vs
+
+using namespace vs;
+
+extern "C" size_t vs_lmhead_workspace_bytes(int B, int T) {
+  const size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
+  return sizeof(LPart) * (size_t)LPMAX * R;
+}
+
+extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K,
+                                       int vocab_valid, int B, int T, const int32_t* drafts, int32_t* out_argmax,
+                                       int32_t* out_accept, float* out_logprob, void* out_logits, int64_t ldo,
+                                       void* ws, size_t ws_bytes, vs_stream_t stream) {
+  if (B < 0 || T < 1) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: B < 0 or T < 1");
+  if (B == 0) return VS_OK;
+  const long long R = (long long)B * T;
+  if (R > LRMAX) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: B*T above 80 positions");
+  if (N < 1 || vocab_valid < 1 || vocab_valid > N)
+    return fail(VS_EINVAL, "vs_lmhead_verify_greedy: need 1 <= vocab_valid <= N");
+  const int kc = R <= 32 ? LH_KC : 256;
+  if (K < kc || K % kc != 0) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: K must be a positive multiple of the k chunk");
+  if (ldh < K || ldw < K || ldh % 8 != 0 || ldw % 8 != 0)
+    return fail(VS_EINVAL, "vs_lmhead_verify_greedy: row strides must be >= K and multiples of 8");
+  if (!h || !W || !out_argmax || !out_accept || !ws || (T > 1 && !drafts))
+    return fail(VS_EINVAL, "vs_lmhead_verify_greedy: null pointer argument");
+  if ((uintptr_t)h % 16 != 0 || (uintptr_t)W % 16 != 0)
+    return fail(VS_EINVAL, "vs_lmhead_verify_greedy: h and W must be 16-byte aligned");
+  if ((int64_t)LNW * 8 * 16 * ldw * 2 >= ((int64_t)1 << 32))
+    return fail(VS_EINVAL, "vs_lmhead_verify_greedy: weight rows too long (ldw)");
+  if (out_logits && ldo < N) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: ldo < N");
+  if (ws_bytes < vs_lmhead_workspace_bytes(B, T))
+    return fail(VS_EWORKSPACE, "vs_lmhead_verify_greedy: workspace too small");
+  const DevInfo* dv = dev_info();
+  if (!dv) return fail(VS_EHIP, "vs_lmhead_verify_greedy: no HIP device");
+  LHArgs a;
+  a.h = (const uint16_t*)h;
+  a.ldh = ldh;
+  a.W = (const uint16_t*)W;
+  a.ldw = ldw;
+  a.N = N;
+  a.vv = vocab_valid;
+  a.K = K;
+  a.B = B;
+  a.T = T;
+  a.R = (int)R;
+  a.ntiles = (N + 15) / 16;
+  a.drafts = drafts;
+  a.out_argmax = out_argmax;
+  a.out_accept = out_accept;
+  a.out_lp = out_logprob;
+  a.out_logits = (uint16_t*)out_logits;
+  a.ldo = ldo;
+  a.ws = (char*)ws;
+  a.trace = g_trace;
+  int P = dv->cus * LH_WPC;  // LH_WPC workgroups per CU, each over a contiguous range of vocabulary tiles
+  if (P > a.ntiles) P = a.ntiles;
+  if (P > LPMAX) P = LPMAX;
+  const int ntt = (int)((R + 15) / 16);
+  switch (ntt) {
+    case 1: return lmhead_launch<1, LH_NTW12>(a, P, (hipStream_t)stream);
+    case 2: return lmhead_launch<2, LH_NTW12>(a, P, (hipStream_t)stream);
+    case 3: return lmhead_launch<3, 4>(a, P, (hipStream_t)stream);
+    case 4: return lmhead_launch<4, 2>(a, P, (hipStream_t)stream);
+    default: return lmhead_launch<5, 2>(a, P, (hipStream_t)stream);
+  }
+}

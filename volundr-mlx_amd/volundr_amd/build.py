@@ -16,7 +16,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / "csrc"
 LIB = PKG / "libvolundr_sampling.so"
 OBJ = PKG.parent / "_build"
-SOURCES = ["vs_api.hip", "vs_sample.hip", "vs_verify.hip", "vs_draft.hip"]
+SOURCES = ["vs_api.hip", "vs_sample.hip", "vs_verify.hip", "vs_draft.hip", "vs_lmhead.hip"]
 ARCH = os.environ.get("VS_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

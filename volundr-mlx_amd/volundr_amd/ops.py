@@ -428,3 +428,41 @@ class PreparedPropose:
         if rc:
             check(rc, "vs_draft_propose")
         return self.out
+
+
+def lmhead_verify_greedy(h: torch.Tensor, W: torch.Tensor, drafts: Optional[torch.Tensor],
+                         vocab_valid: Optional[int] = None, return_logits: bool = False, out: Optional[VerifyOut] = None):
+    """lm_head (bf16) + greedy verify in one launch (volundr.py:958-968 -> spec/specdec.py:326-327): h bf16 [B, T, K]
+    (or [T, K]) final hidden states, W bf16 [N, K] -> VerifyOut (argmax [B, T], accept [B], logprobs [B, T]); with
+    return_logits also the bf16 logits [B, T, N]."""
+    _require_cuda(h, "h")
+    _require_cuda(W, "W")
+    if h.dtype != torch.bfloat16 or W.dtype != torch.bfloat16:
+        raise ValueError("h and W must be bf16")
+    if h.dim() == 2:
+        h = h.unsqueeze(0)
+    if h.dim() != 3 or W.dim() != 2 or h.shape[2] != W.shape[1]:
+        raise ValueError("h must be [B, T, K] and W [N, K]")
+    B, T_, K = h.shape
+    N = W.shape[0]
+    h2 = h.reshape(B * T_, K)
+    if h2.stride(1) != 1 or W.stride(1) != 1:
+        raise ValueError("h and W need unit stride along K")
+    vv = N if vocab_valid is None else int(vocab_valid)
+    dev = h.device
+    if T_ > 1:
+        if drafts is None:
+            raise ValueError("drafts [B, T-1] are required when T > 1")
+        _require_cuda(drafts, "drafts")
+        drafts = drafts.reshape(B, T_ - 1).to(torch.int32).contiguous()
+    if out is None:
+        out = VerifyOut(torch.empty(B, T_, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int32, device=dev),
+                        torch.empty(B, T_, dtype=torch.float32, device=dev))
+    logits = torch.empty(B, T_, N, dtype=torch.bfloat16, device=dev) if return_logits else None
+    L = _lib.load()
+    ws = workspace(dev, L.vs_lmhead_workspace_bytes(B, T_), "lmhead")
+    check(L.vs_lmhead_verify_greedy(h2.data_ptr(), h2.stride(0), W.data_ptr(), W.stride(0), N, K, vv, B, T_,
+                                    drafts.data_ptr() if T_ > 1 else 0, out.argmax.data_ptr(), out.accept.data_ptr(),
+                                    out.logprobs.data_ptr(), logits.data_ptr() if logits is not None else 0, N,
+                                    ws.data_ptr(), ws.numel(), _stream_handle(dev)), "vs_lmhead_verify_greedy")
+    return (out, logits) if return_logits else out
