@@ -223,6 +223,7 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-others", action="store_true")
+    ap.add_argument("--others", default="", help="comma-separated subset of other_configs to run (default: all)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB --steps times (rocprof counter calibration)")
     a = ap.parse_args()
@@ -260,34 +261,40 @@ def main():
                 "kernel_us_event_pairs": round(ev_, 2), "algo_bytes": ab_,
                 "hbm_gbps": round(ab_ / (e2e_ * 1e-6) / 1e9, 1), "tokens_per_s": round(ntok_ / (e2e_ * 1e-6), 1)}
 
+    want = set(x for x in a.others.split(",") if x)
+    sel = lambda name: not want or name in want  # noqa: E731
     if not a.no_others:
         for name in ("c1", "c3", "c5"):
-            if name == a.config:
+            if name == a.config or not sel(name):
                 continue
             dd = synth.CONFIGS[name](seed=0)
             (oe, ok), (we, wk), ab = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
-        dd = synth.CONFIGS["c3"](seed=0)
-        (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)
-        others["c3_state"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
+        if sel("c3_state"):
+            dd = synth.CONFIGS["c3"](seed=0)
+            (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others["c3_state"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         for name in ("c2", "c4"):
-            if name == a.config:
+            if name == a.config or not sel(name):
                 continue
             dd = synth.CONFIGS[name](seed=0)
             (oe, ok), (we, wk), ab, nt = bench_verify(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, nt)
-        (oe, ok), (we, wk), ab = bench_draft(torch, dev, a.steps, a.warmup, a.slots)
-        others["draft_propose"] = entry(oe, ok, we, ab, DRAFT_S)
+        if sel("draft_propose"):
+            (oe, ok), (we, wk), ab = bench_draft(torch, dev, a.steps, a.warmup, a.slots)
+            others["draft_propose"] = entry(oe, ok, we, ab, DRAFT_S)
+            others["draft_propose"]["workload"] = ("DFlash2 propose: top-16 of bf16 logits [7, 248320] (248077 valid) "
+                                                   "+ 7-slot walk, rank-256 codebooks; 2 kernels per step")
         for (bb, tt) in ((1, 17), (4, 17)):
-            (fe, fk), (ue, uk), ab = bench_lmhead(torch, dev, a.steps, a.warmup, bb, tt)
             key = f"lmhead_verify_b{bb}t{tt}"
+            if not sel(key):
+                continue
+            (fe, fk), (ue, uk), ab = bench_lmhead(torch, dev, a.steps, a.warmup, bb, tt)
             others[key] = entry(fe, fk, fe, ab, bb * tt)
             others[key]["workload"] = (f"bf16 lm_head 5120 -> 248320 + greedy verify, B={bb} T={tt}: fused kernel; "
                                        "'unfused_us_per_step' = torch bf16 matmul (logits to HBM) + vs_verify_greedy")
             others[key]["unfused_us_per_step"] = round(ue, 2)
             others[key]["frac_of_8tbs"] = round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)
-        others["draft_propose"]["workload"] = ("DFlash2 propose: top-16 of bf16 logits [7, 248320] (248077 valid) + "
-                                               "7-slot walk, rank-256 codebooks; 2 kernels per step")
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
     # One kernel per step, launched back to back: the per-step time is the kernel's average launch duration plus
     # the inter-dispatch gap (rocprofv3 --kernel-trace agrees within a few percent); per-launch event pairs add

@@ -148,78 +148,88 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
     hrow[q] = i / (KC / 8);
     hcol[q] = (i % (KC / 8)) * 8;
   }
-  for (int r = 0; r < rounds; ++r) {
-    // Weight fetch, two MFMA steps (64 k = 128 bytes of a row) at a time, so that every load instruction reads whole
-    // 128-byte runs of 8 rows (an instruction reading 64 bytes from each of 16 rows streams at ~60% of the rate):
-    // half 0 reads rows 0-7 of the tile, half 1 rows 8-15; lane (m, g) reads, of row m & 7 (+ 8 in half 1), the
-    // 16-byte piece g if it is its own row's half (m < 8 for half 0), else piece 4 + g, which belongs to its
-    // partner lane m ^ 8 in the second step. Step 0 takes the own-half register; step 1 takes the other register
-    // from the partner lane (DPP row rotate by 8 inside each 16-lane row).
-    // Addresses: a 64-bit base per round (the round's first tile, uniform) plus 32-bit byte offsets per lane and
-    // tile (a round spans < 4 GB: LNW*NTW tiles of 16 rows of at most ldw*2 bytes, checked on the host).
-    const bool lo8 = m16 < 8;
-    int tile[NTW];
-    const int tb = t0 + r * LNW * NTW;
-    const char* wbase = (const char*)(A.W + (int64_t)tb * 16 * A.ldw);
-    uint32_t wo0[NTW], wo1[NTW];
+  // Weight fetch, two MFMA steps (64 k = 128 bytes of a row) at a time, so that every load instruction reads whole
+  // 128-byte runs of 8 rows (an instruction reading 64 bytes from each of 16 rows streams at ~60% of the rate):
+  // half 0 reads rows 0-7 of the tile, half 1 rows 8-15; lane (m, g) reads, of row m & 7 (+ 8 in half 1), the
+  // 16-byte piece g if it is its own row's half (m < 8 for half 0), else piece 4 + g, which belongs to its partner
+  // lane m ^ 8 in the second step. Step 0 takes the own-half register; step 1 takes the other register from the
+  // partner lane (DPP row rotate by 8 inside each 16-lane row).
+  // Addresses: a 64-bit base per round (the round's first tile, uniform) plus 32-bit byte offsets per lane and tile
+  // (a round spans < 4 GB: LNW*NTW tiles of 16 rows of at most ldw*2 bytes, checked on the host).
+  // The stream never stops between rounds: the last group of a round fetches the next round's first group, and the
+  // last chunk stages the next round's first hidden chunk, so a round's epilogue overlaps those loads.
+  const bool lo8 = m16 < 8;
+  auto round_offsets = [&](int rr, const char*& base, uint32_t (&o0)[NTW], uint32_t (&o1)[NTW]) {
+    const int tb = t0 + rr * LNW * NTW;
+    base = (const char*)(A.W + (int64_t)tb * 16 * A.ldw);
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      tile[j] = tb + j * LNW + wv;
+      int tl = tb + j * LNW + wv;
       // a tile past the range reads the range's last tile (its lines are being fetched for another wave anyway)
-      const int tl = tile[j] < t1 ? tile[j] : t1 - 1;
+      tl = tl < t1 ? tl : t1 - 1;
       int r0 = tl * 16 + (m16 & 7), r1 = r0 + 8;
       r0 = (r0 < A.N ? r0 : A.N - 1) - tb * 16;
       r1 = (r1 < A.N ? r1 : A.N - 1) - tb * 16;
-      wo0[j] = (uint32_t)((int64_t)r0 * A.ldw * 2) + (uint32_t)((lo8 ? kg : 4 + kg) * 16);
-      wo1[j] = (uint32_t)((int64_t)r1 * A.ldw * 2) + (uint32_t)((lo8 ? 4 + kg : kg) * 16);
+      o0[j] = (uint32_t)((int64_t)r0 * A.ldw * 2) + (uint32_t)((lo8 ? kg : 4 + kg) * 16);
+      o1[j] = (uint32_t)((int64_t)r1 * A.ldw * 2) + (uint32_t)((lo8 ? 4 + kg : kg) * 16);
     }
+  };
+  const int ngroups = K / (2 * KS);
+  const char* wbase;
+  uint32_t wo0[NTW], wo1[NTW];
+  round_offsets(0, wbase, wo0, wo1);
+  // the staged pieces live in named registers (an array of them was kept in scratch memory)
+  uint4 hr0, hr1, hr2, hr3, hr4;
+  static_assert(HPT <= 5, "at most five staged pieces per thread");
+#define LH_HLOAD(cc)                                                                                          \
+  {                                                                                                           \
+    const uint16_t* hbase = A.h + (int64_t)(cc) * KC;                                                         \
+    hr0 = *(const uint4*)(hbase + (int64_t)hrow[0] * A.ldh + hcol[0]);                                        \
+    if constexpr (HPT > 1) hr1 = *(const uint4*)(hbase + (int64_t)hrow[HPT > 1 ? 1 : 0] * A.ldh + hcol[HPT > 1 ? 1 : 0]); \
+    if constexpr (HPT > 2) hr2 = *(const uint4*)(hbase + (int64_t)hrow[HPT > 2 ? 2 : 0] * A.ldh + hcol[HPT > 2 ? 2 : 0]); \
+    if constexpr (HPT > 3) hr3 = *(const uint4*)(hbase + (int64_t)hrow[HPT > 3 ? 3 : 0] * A.ldh + hcol[HPT > 3 ? 3 : 0]); \
+    if constexpr (HPT > 4) hr4 = *(const uint4*)(hbase + (int64_t)hrow[HPT > 4 ? 4 : 0] * A.ldh + hcol[HPT > 4 ? 4 : 0]); \
+  }
+#define LH_HSTORE(bb)                                                                                          \
+  {                                                                                                            \
+    if (hin[0]) *(uint4*)&hs[bb][hrow[0]][hcol[0]] = hr0;                                                      \
+    if constexpr (HPT > 1) if (hin[HPT > 1 ? 1 : 0]) *(uint4*)&hs[bb][hrow[HPT > 1 ? 1 : 0]][hcol[HPT > 1 ? 1 : 0]] = hr1; \
+    if constexpr (HPT > 2) if (hin[HPT > 2 ? 2 : 0]) *(uint4*)&hs[bb][hrow[HPT > 2 ? 2 : 0]][hcol[HPT > 2 ? 2 : 0]] = hr2; \
+    if constexpr (HPT > 3) if (hin[HPT > 3 ? 3 : 0]) *(uint4*)&hs[bb][hrow[HPT > 3 ? 3 : 0]][hcol[HPT > 3 ? 3 : 0]] = hr3; \
+    if constexpr (HPT > 4) if (hin[HPT > 4 ? 4 : 0]) *(uint4*)&hs[bb][hrow[HPT > 4 ? 4 : 0]][hcol[HPT > 4 ? 4 : 0]] = hr4; \
+  }
+  LH_HLOAD(0)
+  uint4 wb[NTW][2];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    wb[j][0] = *(const uint4*)(wbase + wo0[j]);
+    wb[j][1] = *(const uint4*)(wbase + wo1[j]);
+  }
+  __syncthreads();  // the padded rows are zeroed
+  LH_HSTORE(0)
+  __syncthreads();
+  int cg = 0;  // chunks processed so far (all rounds): the LDS buffer of the current chunk is cg & 1
+  for (int r = 0; r < rounds; ++r) {
+    int tile[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) tile[j] = t0 + r * LNW * NTW + j * LNW + wv;
+    // the next round's addresses (this round's again on the last round: its final prefetch is a spare)
+    const char* nbase;
+    uint32_t no0[NTW], no1[NTW];
+    round_offsets(r + 1 < rounds ? r + 1 : r, nbase, no0, no1);
     f32x4_t acc[NTW][NTT];
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
 #pragma unroll
       for (int tt = 0; tt < NTT; ++tt) acc[j][tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    // the staged pieces live in named registers (an array of them was kept in scratch memory)
-    uint4 hr0, hr1, hr2, hr3, hr4;
-    static_assert(HPT <= 5, "at most five staged pieces per thread");
-    {
-      const uint16_t* hbase = A.h + (int64_t)(0) * KC;
-      hr0 = *(const uint4*)(hbase + (int64_t)hrow[0] * A.ldh + hcol[0]);
-      if constexpr (HPT > 1) hr1 = *(const uint4*)(hbase + (int64_t)hrow[1] * A.ldh + hcol[1]);
-      if constexpr (HPT > 2) hr2 = *(const uint4*)(hbase + (int64_t)hrow[2] * A.ldh + hcol[2]);
-      if constexpr (HPT > 3) hr3 = *(const uint4*)(hbase + (int64_t)hrow[3] * A.ldh + hcol[3]);
-      if constexpr (HPT > 4) hr4 = *(const uint4*)(hbase + (int64_t)hrow[4] * A.ldh + hcol[4]);
-    }
-    const int ngroups = K / (2 * KS);
-    uint4 wb[NTW][2];
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      wb[j][0] = *(const uint4*)(wbase + wo0[j]);
-      wb[j][1] = *(const uint4*)(wbase + wo1[j]);
-    }
-    __syncthreads();  // the previous round's reads of buffer 0 are done
-    {
-      if (hin[0]) *(uint4*)&hs[0][hrow[0]][hcol[0]] = hr0;
-      if constexpr (HPT > 1) if (hin[1]) *(uint4*)&hs[0][hrow[1]][hcol[1]] = hr1;
-      if constexpr (HPT > 2) if (hin[2]) *(uint4*)&hs[0][hrow[2]][hcol[2]] = hr2;
-      if constexpr (HPT > 3) if (hin[3]) *(uint4*)&hs[0][hrow[3]][hcol[3]] = hr3;
-      if constexpr (HPT > 4) if (hin[4]) *(uint4*)&hs[0][hrow[4]][hcol[4]] = hr4;
-    }
-    __syncthreads();
     VS_TR(A, 1 + 3 * r);
-    for (int c = 0; c < nchunks; ++c) {
-      const int b = c & 1;
-      // the next chunk's hidden rows are fetched now and stored after this chunk's steps (on the last chunk the
-      // same chunk is fetched again and stored into the idle buffer, which nothing reads before the next round
-      // rewrites it behind a barrier)
-      const int cn = c + 1 < nchunks ? c + 1 : c;
-      {
-      const uint16_t* hbase = A.h + (int64_t)(cn) * KC;
-      hr0 = *(const uint4*)(hbase + (int64_t)hrow[0] * A.ldh + hcol[0]);
-      if constexpr (HPT > 1) hr1 = *(const uint4*)(hbase + (int64_t)hrow[1] * A.ldh + hcol[1]);
-      if constexpr (HPT > 2) hr2 = *(const uint4*)(hbase + (int64_t)hrow[2] * A.ldh + hcol[2]);
-      if constexpr (HPT > 3) hr3 = *(const uint4*)(hbase + (int64_t)hrow[3] * A.ldh + hcol[3]);
-      if constexpr (HPT > 4) hr4 = *(const uint4*)(hbase + (int64_t)hrow[4] * A.ldh + hcol[4]);
-    }
+    for (int c = 0; c < nchunks; ++c, ++cg) {
+      const int b = cg & 1;
+      // the next chunk's hidden rows (chunk 0 again after the last: the next round's first) are fetched now and
+      // stored into the idle buffer after this chunk's steps
+      const int cn = c + 1 < nchunks ? c + 1 : 0;
+      LH_HLOAD(cn)
+      const bool last_chunk = c + 1 == nchunks;
 #pragma unroll
       for (int gq = 0; gq < SPC / 2; ++gq) {
         bf16x8_t hb0[NTT], hb1[NTT];
@@ -228,8 +238,10 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
           hb0[tt] = *(const bf16x8_t*)&hs[b][tt * 16 + m16][(2 * gq) * KS + kg * 8];
           hb1[tt] = *(const bf16x8_t*)&hs[b][tt * 16 + m16][(2 * gq + 1) * KS + kg * 8];
         }
-        int gn = c * (SPC / 2) + gq + 1;  // the group fetched now (clamped: one spare fetch at the end)
-        gn = gn < ngroups ? gn : ngroups - 1;
+        // the group fetched now: the next one of this round, or the next round's first
+        const bool wrap = last_chunk && gq == SPC / 2 - 1;
+        const int gn = wrap ? 0 : c * (SPC / 2) + gq + 1;
+        const char* fb = wrap ? nbase : wbase;
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
           const uint4 a0 = wb[j][0], a1 = wb[j][1];
@@ -240,17 +252,14 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
           s1.y = dpp32<0x128>(o.y, o.y);
           s1.z = dpp32<0x128>(o.z, o.z);
           s1.w = dpp32<0x128>(o.w, o.w);
-          wb[j][0] = *(const uint4*)(wbase + (wo0[j] + (uint32_t)gn * 4 * KS));
-          wb[j][1] = *(const uint4*)(wbase + (wo1[j] + (uint32_t)gn * 4 * KS));
+          const uint32_t f0 = wrap ? no0[j] : wo0[j], f1 = wrap ? no1[j] : wo1[j];
+          wb[j][0] = *(const uint4*)(fb + (f0 + (uint32_t)gn * 4 * KS));
+          wb[j][1] = *(const uint4*)(fb + (f1 + (uint32_t)gn * 4 * KS));
 #ifndef LH_NO_PIN
           __builtin_amdgcn_sched_barrier(0);  // keep the next group's loads here, one group ahead of their use
 #endif
-#ifdef LH_DIAG_ONE_TT
-          for (int tt = 0; tt < 1; ++tt) {
-#else
 #pragma unroll
           for (int tt = 0; tt < NTT; ++tt) {
-#endif
             acc[j][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, s0), hb0[tt],
                                                                  acc[j][tt], 0, 0, 0);
             acc[j][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, s1), hb1[tt],
@@ -258,14 +267,14 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
           }
         }
       }
-      {
-      if (hin[0]) *(uint4*)&hs[b ^ 1][hrow[0]][hcol[0]] = hr0;
-      if constexpr (HPT > 1) if (hin[1]) *(uint4*)&hs[b ^ 1][hrow[1]][hcol[1]] = hr1;
-      if constexpr (HPT > 2) if (hin[2]) *(uint4*)&hs[b ^ 1][hrow[2]][hcol[2]] = hr2;
-      if constexpr (HPT > 3) if (hin[3]) *(uint4*)&hs[b ^ 1][hrow[3]][hcol[3]] = hr3;
-      if constexpr (HPT > 4) if (hin[4]) *(uint4*)&hs[b ^ 1][hrow[4]][hcol[4]] = hr4;
-    }
+      LH_HSTORE(b ^ 1)
       __syncthreads();
+    }
+    wbase = nbase;
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      wo0[j] = no0[j];
+      wo1[j] = no1[j];
     }
     VS_TR(A, 2 + 3 * r);
     // epilogue of the round: lane holds vocabulary rows tile*16 + 4*kg + q of positions tt*16 + m16
@@ -306,6 +315,8 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
       }
     }
   }
+#undef LH_HLOAD
+#undef LH_HSTORE
 
   // lanes of one position (same m16): xor 16, 32; then the waves through LDS; then the workgroup partial
 #pragma unroll
