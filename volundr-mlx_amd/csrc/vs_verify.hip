@@ -19,6 +19,7 @@ namespace vs {
 constexpr int VNT = 256;
 constexpr int VNW = VNT / WAVE;
 constexpr int VNV_MAX = 64;  // 16-byte loads per lane (streamed, not held)
+constexpr int VNF = 8;       // 16-byte loads per lane held in VGPRs by the fast path
 constexpr int VGMAX = 64;
 constexpr int VRMAX = 8192;  // rows (B*T) per call: the counters live at fixed offsets so any call finds them zero
 
@@ -49,19 +50,51 @@ struct VTraits;
 template <>
 struct VTraits<VS_F32> {
   static constexpr int VEC = 4;
+  __device__ static uint4 gather(const void* p, int base, int hi) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = base + q < hi ? ((const uint32_t*)p)[base + q] : 0xFF800000u;
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
   __device__ static float get(const uint4& r, int q) { return ((const float*)&r)[q]; }
   __device__ static float one(const void* p, int64_t i) { return ((const float*)p)[i]; }
 };
 template <>
 struct VTraits<VS_BF16> {
   static constexpr int VEC = 8;
-  __device__ static float get(const uint4& r, int q) { return bf16_to_f32(((const uint16_t*)&r)[q]); }
+  __device__ static uint4 gather(const void* p, int base, int hi) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = base + 2 * q < hi ? ((const uint16_t*)p)[base + 2 * q] : 0xFF80u;
+      const uint32_t b = base + 2 * q + 1 < hi ? ((const uint16_t*)p)[base + 2 * q + 1] : 0xFF80u;
+      w[q] = a | (b << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  __device__ static float get(const uint4& r, int q) {
+    const uint32_t w = q < 2 ? r.x : q < 4 ? r.y : q < 6 ? r.z : r.w;  // q is a constant after unrolling
+    return __uint_as_float((q & 1) ? (w & 0xFFFF0000u) : (w << 16));
+  }
   __device__ static float one(const void* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
 };
 template <>
 struct VTraits<VS_F16> {
   static constexpr int VEC = 8;
-  __device__ static float get(const uint4& r, int q) { return f16_to_f32(((const uint16_t*)&r)[q]); }
+  __device__ static uint4 gather(const void* p, int base, int hi) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = base + 2 * q < hi ? ((const uint16_t*)p)[base + 2 * q] : 0xFC00u;
+      const uint32_t b = base + 2 * q + 1 < hi ? ((const uint16_t*)p)[base + 2 * q + 1] : 0xFC00u;
+      w[q] = a | (b << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  __device__ static float get(const uint4& r, int q) {
+    const uint32_t w = q < 2 ? r.x : q < 4 ? r.y : q < 6 ? r.z : r.w;  // q is a constant after unrolling
+    return f16_to_f32((uint16_t)((q & 1) ? (w >> 16) : (w & 0xFFFFu)));
+  }
   __device__ static float one(const void* p, int64_t i) { return f16_to_f32(((const uint16_t*)p)[i]); }
 };
 
@@ -89,11 +122,81 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   VS_TR_DECL(A);
   VS_TR(A, 0);
 
-  // One streaming pass: first-max key (np.argmax order, NaN first), running finite maximum m and
-  // s = sum(exp(x - m)) rescaled whenever m grows (float32 exp per element, float64 accumulation).
   u64 am = 0;
   float m = -__builtin_inff();
   double se = 0.0;
+  if (A.NV <= VNF) {
+    // Fast path: the whole chunk fits in VGPRs (<= VNF 16-byte loads per lane, all issued at once). Pass 1: the
+    // lane's first maximum (strict > in increasing index order), its finite maximum and its first NaN; pass 2:
+    // sum(exp(x - m)) from the registers as exp2((x - m) * log2(e)) (one v_exp_f32 per element). Keys are built
+    // once per lane: np.argmax's order (NaN first, then the value, then the lower index) is kept.
+    uint4 rv[VNF];
+#pragma unroll
+    for (int u = 0; u < VNF; ++u) {
+      int base = lo + (u * VNT + t) * VEC;
+      base = (u < A.NV && base < hi) ? base : lo;  // clamped into the row: the values are masked below
+      rv[u] = A.vec_ok ? *(const uint4*)(rowp + (int64_t)base * (DT == VS_F32 ? 4 : 2)) : make_uint4(0, 0, 0, 0);
+    }
+    // a vector that is not whole inside the chunk (the row's last, or any when unaligned) is assembled element by
+    // element, -inf past the end, so both passes below read registers only
+#pragma unroll
+    for (int u = 0; u < VNF; ++u) {
+      const int base = lo + (u * VNT + t) * VEC;
+      if (u < A.NV && base < hi && !(A.vec_ok && base + VEC <= hi)) rv[u] = TR::gather(rowp, base, hi);
+    }
+    // A lane's elements inside the chunk are a prefix of its (u, q) order: nin of them.
+    const int base0 = lo + t * VEC;
+    int nin = 0;
+#pragma unroll
+    for (int u = 0; u < VNF; ++u) {
+      const int rem = hi - (base0 + u * VNT * VEC);
+      nin += (u < A.NV && rem > 0) ? (rem < VEC ? rem : VEC) : 0;
+    }
+    float best = -__builtin_inff();
+    int bi = -1, nani = -1;
+#pragma unroll
+    for (int u = 0; u < VNF; ++u) {
+      if (u >= A.NV) break;  // uniform: the work scales with the chunk, not with the register budget
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        const bool in = u * VEC + q < nin;
+        const float x = TR::get(rv[u], q);
+        const int idx = base0 + u * VNT * VEC + q;
+        if (in && (x > best || (bi < 0 && x == x))) {
+          best = x;
+          bi = idx;
+        }
+        if (in && x != x && nani < 0) nani = idx;
+        if (in && is_finite(x)) m = x > m ? x : m;
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one vector at a time (hoisting every widening costs VGPRs)
+    }
+    if (nani >= 0)
+      am = amkey64(__builtin_nanf(""), (uint32_t)nani);
+    else if (bi >= 0)
+      am = amkey64(best, (uint32_t)bi);
+    // the raw registers are declared changed here, so the compiler re-widens them in pass 2 instead of keeping
+    // every widened value of pass 1 live (VGPRs, hence occupancy)
+#pragma unroll
+    for (int u = 0; u < VNF; ++u) asm volatile("" : "+v"(rv[u].x), "+v"(rv[u].y), "+v"(rv[u].z), "+v"(rv[u].w));
+    if (is_finite(m)) {
+      const float L2E = 1.44269504088896340736f;
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < VNF; ++u) {
+        if (u >= A.NV) break;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float x = TR::get(rv[u], q);
+          if (u * VEC + q < nin && is_finite(x)) acc += __builtin_amdgcn_exp2f((x - m) * L2E);
+          if (q == VEC - 1) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      se = (double)acc;
+    }
+  } else {
+  // General path (chunks longer than the register budget): one streaming pass with the first-max key, a running
+  // finite maximum m and s = sum(exp(x - m)) rescaled whenever m grows (float32 exp per element, float64 sums).
   auto load = [&](uint4* r, int j0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -139,6 +242,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+  }
   }
   VS_TR(A, 1);
   // workgroup merge of (m, se) pairs and the key
@@ -235,9 +339,23 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   const int chmax = VNV_MAX * unit;
   int gmin = (vocab_valid + chmax - 1) / chmax;
   if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
-  int G = (2 * dv->cus + R - 1) / R;  // aim at >= 2 workgroups per CU in flight
-  const int g4 = (vocab_valid + 4 * unit - 1) / (4 * unit);  // and at most 4 loads per lane
-  if (G < g4) G = g4;
+  // About VS_VERIFY_NVT 16-byte loads per lane (measured best on MI355X: fewer lanes' worth of work per workgroup
+  // adds merge and arrival overhead, more lengthens each workgroup's chain), but never more workgroups than are
+  // resident at once (a second wave would start only after the first finished).
+#ifndef VS_VERIFY_NVT
+#define VS_VERIFY_NVT 4
+#endif
+  const void* kfn = dtype == VS_F32 ? (const void*)vs_verify_kernel<VS_F32>
+                    : dtype == VS_BF16 ? (const void*)vs_verify_kernel<VS_BF16>
+                                       : (const void*)vs_verify_kernel<VS_F16>;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, VNT, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  int G = (vocab_valid + VS_VERIFY_NVT * unit - 1) / (VS_VERIFY_NVT * unit);
+  const int gres = (per_cu * dv->cus) / R;
+  if (G > gres) G = gres;
+  const int gf = (vocab_valid + VNF * unit - 1) / (VNF * unit);  // the fewest workgroups the fast path allows
+  if (G < gf) G = gf;
+  if (G < 1) G = 1;
   if (G > VGMAX) G = VGMAX;
   if (G < gmin) G = gmin;
   int CH = (vocab_valid + G - 1) / G;
