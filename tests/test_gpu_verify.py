@@ -62,3 +62,19 @@ def test_nonfinite(dev):
     x[0, 2, 10] = np.inf
     o = verify_greedy(torch.from_numpy(x).to(dev), torch.tensor([[5, 0]], dtype=torch.int32, device=dev), 300)
     assert o.argmax.cpu().tolist() == [[5, 0, 9]] and o.accept.item() == 2
+
+
+@pytest.mark.parametrize("T", [2, 32, 33, 34, 40])
+def test_accept_lengths_around_the_packed_limit(dev, T):
+    """Blocks of up to 33 positions carry the accept information in one packed word, longer ones take the
+    counter-and-reload path: every accept length 0..T-1 on both sides of the limit."""
+    rng = np.random.default_rng(T)
+    B, V = T, 3000  # request b gets its first mismatch at position b (b = T-1: all drafts accepted)
+    x = rng.standard_normal((B, T, V)).astype(np.float32)
+    tok = np.argmax(x, -1)
+    drafts = tok[:, :-1].astype(np.int32).copy()
+    for b in range(B):
+        if b < T - 1:
+            drafts[b, b] = (drafts[b, b] + 1) % V
+    o = check(dev, x, drafts, V, torch.float32, f"T={T}")
+    assert o.accept.cpu().tolist() == list(range(T))

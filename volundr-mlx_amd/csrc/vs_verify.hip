@@ -50,6 +50,7 @@ struct VTraits;
 template <>
 struct VTraits<VS_F32> {
   static constexpr int VEC = 4;
+  static constexpr uint32_t NEG_INF_WORD = 0xFF800000u;
   __device__ static uint4 gather(const void* p, int base, int hi) {
     uint32_t w[4];
 #pragma unroll
@@ -62,6 +63,7 @@ struct VTraits<VS_F32> {
 template <>
 struct VTraits<VS_BF16> {
   static constexpr int VEC = 8;
+  static constexpr uint32_t NEG_INF_WORD = 0xFF80FF80u;
   __device__ static uint4 gather(const void* p, int base, int hi) {
     uint32_t w[4];
 #pragma unroll
@@ -81,6 +83,7 @@ struct VTraits<VS_BF16> {
 template <>
 struct VTraits<VS_F16> {
   static constexpr int VEC = 8;
+  static constexpr uint32_t NEG_INF_WORD = 0xFC00FC00u;
   __device__ static uint4 gather(const void* p, int base, int hi) {
     uint32_t w[4];
 #pragma unroll
@@ -114,7 +117,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   const int row = l / G, g = l % G;
   uint32_t* rowdone = (uint32_t*)A.ws;
   uint32_t* reqdone = rowdone + VRMAX;
-  VPart* parts = (VPart*)(A.ws + 8 * VRMAX);
+  u64* reqword = (u64*)(A.ws + 8 * VRMAX);  // T <= 33: arrivals << 32 | mismatch bit per draft position
+  VPart* parts = (VPart*)(A.ws + 16 * VRMAX);
 
   const int lo = g * A.CH;
   const int hi = min(A.vv, lo + A.CH);
@@ -143,37 +147,60 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     for (int u = 0; u < VNF; ++u) {
       const int base = lo + (u * VNT + t) * VEC;
       if (u < A.NV && base < hi && !(A.vec_ok && base + VEC <= hi)) rv[u] = TR::gather(rowp, base, hi);
+      // a vector wholly past the chunk reads as -inf (a select, not a branch)
+      const bool past = base >= hi;
+      rv[u].x = past ? TR::NEG_INF_WORD : rv[u].x;
+      rv[u].y = past ? TR::NEG_INF_WORD : rv[u].y;
+      rv[u].z = past ? TR::NEG_INF_WORD : rv[u].z;
+      rv[u].w = past ? TR::NEG_INF_WORD : rv[u].w;
     }
-    // A lane's elements inside the chunk are a prefix of its (u, q) order: nin of them.
+#ifdef VS_TRACE
+    __builtin_amdgcn_s_waitcnt(0);
+    VS_TR(A, 5);
+#endif
+    // Every element past the chunk now reads -inf, and a lane's elements inside the chunk come first in its (u, q)
+    // order, so no element needs a range test: -inf after a taken element is never taken (strict >), adds nothing
+    // to the sums and is not finite. A lane with no element inside the chunk contributes no key.
     const int base0 = lo + t * VEC;
-    int nin = 0;
-#pragma unroll
-    for (int u = 0; u < VNF; ++u) {
-      const int rem = hi - (base0 + u * VNT * VEC);
-      nin += (u < A.NV && rem > 0) ? (rem < VEC ? rem : VEC) : 0;
-    }
+    const bool any_in = base0 < hi;
+    // Branch-free (selects; & and | on bools: && and || compile to branches). NaN compares as -inf for the first
+    // maximum and only raises a flag; the (rare) first NaN index is found by a second scan. With every element
+    // -inf or NaN the first maximum is the lane's first element, as np.argmax has it.
     float best = -__builtin_inff();
-    int bi = -1, nani = -1;
+    int bi = base0;
+    bool anynan = false;
 #pragma unroll
     for (int u = 0; u < VNF; ++u) {
       if (u >= A.NV) break;  // uniform: the work scales with the chunk, not with the register budget
 #pragma unroll
       for (int q = 0; q < VEC; ++q) {
-        const bool in = u * VEC + q < nin;
         const float x = TR::get(rv[u], q);
-        const int idx = base0 + u * VNT * VEC + q;
-        if (in && (x > best || (bi < 0 && x == x))) {
-          best = x;
-          bi = idx;
-        }
-        if (in && x != x && nani < 0) nani = idx;
-        if (in && is_finite(x)) m = x > m ? x : m;
+        const bool isnan = x != x;
+        const float xc = isnan ? -__builtin_inff() : x;
+        const bool take = xc > best;
+        best = take ? xc : best;
+        bi = take ? base0 + u * VNT * VEC + q : bi;
+        anynan = anynan | isnan;
+        m = __builtin_fmaxf(m, is_finite(x) ? x : -__builtin_inff());
       }
       __builtin_amdgcn_sched_barrier(0);  // one vector at a time (hoisting every widening costs VGPRs)
     }
-    if (nani >= 0)
+    VS_TR(A, 6);
+    int nani = -1;
+    if (anynan) {
+#pragma unroll
+      for (int u = 0; u < VNF; ++u) {
+        if (u >= A.NV) break;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float x = TR::get(rv[u], q);
+          nani = ((x != x) & (nani < 0)) ? base0 + u * VNT * VEC + q : nani;
+        }
+      }
+    }
+    if (any_in && nani >= 0)
       am = amkey64(__builtin_nanf(""), (uint32_t)nani);
-    else if (bi >= 0)
+    else if (any_in)
       am = amkey64(best, (uint32_t)bi);
     // the raw registers are declared changed here, so the compiler re-widens them in pass 2 instead of keeping
     // every widened value of pass 1 live (VGPRs, hence occupancy)
@@ -188,7 +215,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
 #pragma unroll
         for (int q = 0; q < VEC; ++q) {
           const float x = TR::get(rv[u], q);
-          if (u * VEC + q < nin && is_finite(x)) acc += __builtin_amdgcn_exp2f((x - m) * L2E);
+          const float d = is_finite(x) ? (x - m) * L2E : -__builtin_inff();
+          acc += __builtin_amdgcn_exp2f(d);  // exp2(-inf) = 0: masked terms add nothing, without a branch
           if (q == VEC - 1) __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -245,16 +273,36 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   }
   }
   VS_TR(A, 1);
-  // workgroup merge of (m, se) pairs and the key
-  am = block_max<VNT>(am, red64);
-  const float mb = block_max<VNT>(m, redf);
-  const double sc = (se > 0.0 && is_finite(mb)) ? se * exp((double)m - (double)mb) : 0.0;
-  const double sb = block_sum<VNT>(sc, redd);
-  if (t == 0) {
-    VPart* pp = parts + (size_t)row * G + g;
-    st_dev(&pp->amkey, am);
-    st_dev(&pp->mf, mb);
-    st_dev(&pp->se, sb);
+  // workgroup merge of the key and the (m, se) pairs: each wave reduces its lanes (max, then the sum rescaled to
+  // the wave's max), one LDS exchange and one barrier, then thread 0 merges the VNW waves
+  {
+    const int wv = t / WAVE;
+    const u64 kw = wave_max(am);
+    const float mw = wave_max(m);
+    const double sw = wave_sum((se > 0.0 && is_finite(mw)) ? se * (double)expf(m - mw) : 0.0);
+    if (lane_id() == 0) {
+      red64[wv] = kw;
+      redf[wv] = mw;
+      redd[wv] = sw;
+    }
+    __syncthreads();
+    if (t == 0) {
+      u64 kb = red64[0];
+      float mb = redf[0];
+#pragma unroll
+      for (int w = 1; w < VNW; ++w) {
+        kb = red64[w] > kb ? red64[w] : kb;
+        mb = redf[w] > mb ? redf[w] : mb;
+      }
+      double sb = 0.0;
+#pragma unroll
+      for (int w = 0; w < VNW; ++w)
+        sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)expf(redf[w] - mb) : 0.0;
+      VPart* pp = parts + (size_t)row * G + g;
+      st_dev(&pp->amkey, kb);
+      st_dev(&pp->mf, mb);
+      st_dev(&pp->se, sb);
+    }
   }
   VS_TR(A, 2);
   if (block_arrive(&rowdone[row], &flag) != (uint32_t)(G - 1)) {
@@ -280,11 +328,27 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     uint32_t last = 0;
     if (t == 0) {
       const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
-      st_dev(&A.out_argmax[row], (int32_t)key_index(bam));
+      const int32_t tok = (int32_t)key_index(bam);
       if (A.out_lp) A.out_lp[row] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
       st_dev(&rowdone[row], 0u);
-      publish_wait();
-      last = ctr_add(&reqdone[req], 1u) == (uint32_t)(A.T - 1);
+      if (A.T <= 33) {
+        // one atomic carries the arrival and this position's mismatch bit (each row adds its own bit, so the sum is
+        // the union); the request's last row reads every mismatch from the returned word (specdec.py:327)
+        const int tp = row - req * A.T;
+        const bool mis = tp < A.T - 1 && A.drafts[(size_t)req * (A.T - 1) + tp] != tok;
+        const u64 add = (1ull << 32) | (mis ? (1ull << tp) : 0ull);
+        A.out_argmax[row] = tok;
+        const u64 old = __hip_atomic_fetch_add(&reqword[req], add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(old >> 32) == (uint32_t)(A.T - 1)) {
+          const uint32_t mask = (uint32_t)((old + add) & 0xFFFFFFFFull) | (A.T - 1 < 32 ? (1u << (A.T - 1)) : 0u);
+          A.out_accept[req] = mask ? __builtin_ctz(mask) : 32;
+          st_dev(&reqword[req], 0ull);
+        }
+      } else {
+        st_dev(&A.out_argmax[row], tok);
+        publish_wait();
+        last = ctr_add(&reqdone[req], 1u) == (uint32_t)(A.T - 1);
+      }
     }
     // last row of the request: accept prefix (specdec.py:327), 64 positions per ballot
     if (lane_bcast(last, 0)) {
@@ -316,7 +380,7 @@ using namespace vs;
 extern "C" size_t vs_verify_workspace_bytes(int B, int T, int V) {
   (void)V;
   size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
-  return 8 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
+  return 16 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
 }
 
 extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t ld, int vocab_valid,
