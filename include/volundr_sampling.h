@@ -135,7 +135,7 @@ size_t vs_verify_workspace_bytes(int B, int T, int V);
  * even, of a float32 sum of products) are reduced in registers and never written unless out_logits is given.
  *   h          : bf16 [B*T, ldh] final hidden states (row b*T + t), 16-byte aligned, ldh % 8 == 0
  *   W          : bf16 [N, ldw] lm_head weight (vocab_size rows of K = hidden), 16-byte aligned, ldw % 8 == 0
- *   K          : hidden size, a multiple of 256;  B*T <= 80
+ *   K          : hidden size, any multiple of 256;  B*T <= 80
  *   drafts, out_argmax, out_accept, out_logprob : as vs_verify_greedy (first-max argmax over [0, vocab_valid))
  *   out_logits : bf16 [B*T, ldo] or NULL (testing / callers that need the rows; costs the logits write)
  *   ws         : device workspace of at least vs_lmhead_workspace_bytes(B, T) bytes, zeroed once beforehand

@@ -127,3 +127,12 @@ def test_lmhead_full_size_against_torch(dev):
     np.testing.assert_array_equal(o.accept.cpu().numpy(), acc)
     np.testing.assert_allclose(o.logprobs.cpu().numpy(), lp, rtol=1e-5, atol=1e-6)
     assert int(o.accept[0]) <= 9
+
+
+@pytest.mark.parametrize("B,T,K", [(1, 17, 768), (1, 1, 1280), (2, 16, 256), (4, 17, 768)])
+def test_lmhead_hidden_sizes(dev, B, T, K):
+    """Any hidden size that is a multiple of 256 (the 512-wide k chunks are used only where K allows them)."""
+    N = 3001
+    h, w, drafts = _case(K + B * T, B, T, K, N, scale=4.0)
+    o, got = _run(dev, h, w, drafts, B, T, N)
+    _check(o, got, h, w, drafts, B, T, N)

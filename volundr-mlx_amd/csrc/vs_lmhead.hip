@@ -34,9 +34,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #endif
 constexpr int LNT = LH_NT;          // threads per workgroup
 constexpr int LNW = LNT / WAVE;     // waves per workgroup
-#ifndef LH_KC
-#define LH_KC 512
-#endif
 #ifndef LH_NTW12
 #define LH_NTW12 4
 #endif
@@ -46,7 +43,6 @@ constexpr int LNW = LNT / WAVE;     // waves per workgroup
 constexpr int KS = 32;              // k per MFMA
 constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
 constexpr int LPMAX = 2048;         // workgroups per launch
-static_assert(LH_KC % (2 * KS) == 0, "a chunk holds whole two-step groups");
 
 struct LPart {
   u64 amkey;
@@ -92,11 +88,11 @@ __device__ __forceinline__ void lse_merge(float& m, double& s, float m2, double 
   s = r;
 }
 
-template <int NTT, int NTW>
+// KC: k per LDS chunk (512 where K allows and two chunks of RP rows fit the LDS: fewer barriers; else 256)
+template <int NTT, int NTW, int KC>
 __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 * LH_WPC))) void vs_lmhead_verify_kernel(
     LHArgs A) {
   constexpr int RP = 16 * NTT;  // positions padded to whole MFMA tiles
-  constexpr int KC = NTT <= 2 ? LH_KC : 256;  // k per LDS chunk (two chunks of RP rows fit the LDS)
   constexpr int SPC = KC / KS;
   constexpr int HSTR = KC + 8;
   __shared__ __attribute__((aligned(16))) uint16_t hs[2][RP][HSTR];
@@ -415,9 +411,9 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
   }
 }
 
-template <int NTT, int NTW>
+template <int NTT, int NTW, int KC>
 static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
-  hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW>), dim3(P), dim3(LNT), 0, stream, a);
+  hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW, KC>), dim3(P), dim3(LNT), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "vs_lmhead_verify_greedy: launch");
   hipLaunchKernelGGL(vs_lmhead_merge_kernel, dim3(a.R), dim3(MNT), 0, stream, a, P);
@@ -444,8 +440,8 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   if (R > LRMAX) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: B*T above 80 positions");
   if (N < 1 || vocab_valid < 1 || vocab_valid > N)
     return fail(VS_EINVAL, "vs_lmhead_verify_greedy: need 1 <= vocab_valid <= N");
-  const int kc = R <= 32 ? LH_KC : 256;
-  if (K < kc || K % kc != 0) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: K must be a positive multiple of the k chunk");
+  if (K < 256 || K % 256 != 0) return fail(VS_EINVAL, "vs_lmhead_verify_greedy: K must be a positive multiple of 256");
+  const bool kc512 = R <= 32 && K % 512 == 0;
   if (ldh < K || ldw < K || ldh % 8 != 0 || ldw % 8 != 0)
     return fail(VS_EINVAL, "vs_lmhead_verify_greedy: row strides must be >= K and multiples of 8");
   if (!h || !W || !out_argmax || !out_accept || !ws || (T > 1 && !drafts))
@@ -484,10 +480,12 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   if (P > LPMAX) P = LPMAX;
   const int ntt = (int)((R + 15) / 16);
   switch (ntt) {
-    case 1: return lmhead_launch<1, LH_NTW12>(a, P, (hipStream_t)stream);
-    case 2: return lmhead_launch<2, LH_NTW12>(a, P, (hipStream_t)stream);
-    case 3: return lmhead_launch<3, 4>(a, P, (hipStream_t)stream);
-    case 4: return lmhead_launch<4, 2>(a, P, (hipStream_t)stream);
-    default: return lmhead_launch<5, 2>(a, P, (hipStream_t)stream);
+    case 1: return kc512 ? lmhead_launch<1, LH_NTW12, 512>(a, P, (hipStream_t)stream)
+                         : lmhead_launch<1, LH_NTW12, 256>(a, P, (hipStream_t)stream);
+    case 2: return kc512 ? lmhead_launch<2, LH_NTW12, 512>(a, P, (hipStream_t)stream)
+                         : lmhead_launch<2, LH_NTW12, 256>(a, P, (hipStream_t)stream);
+    case 3: return lmhead_launch<3, 4, 256>(a, P, (hipStream_t)stream);
+    case 4: return lmhead_launch<4, 2, 256>(a, P, (hipStream_t)stream);
+    default: return lmhead_launch<5, 2, 256>(a, P, (hipStream_t)stream);
   }
 }
