@@ -403,11 +403,11 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   const int chmax = VNV_MAX * unit;
   int gmin = (vocab_valid + chmax - 1) / chmax;
   if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
-  // About VS_VERIFY_NVT 16-byte loads per lane (measured best on MI355X: fewer lanes' worth of work per workgroup
+  // About VS_VERIFY_NVT 16-byte loads per lane (measured best on MI355X: less work per workgroup
   // adds merge and arrival overhead, more lengthens each workgroup's chain), but never more workgroups than are
   // resident at once (a second wave would start only after the first finished).
 #ifndef VS_VERIFY_NVT
-#define VS_VERIFY_NVT 4
+#define VS_VERIFY_NVT 6
 #endif
   const void* kfn = dtype == VS_F32 ? (const void*)vs_verify_kernel<VS_F32>
                     : dtype == VS_BF16 ? (const void*)vs_verify_kernel<VS_BF16>
