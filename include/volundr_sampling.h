@@ -180,13 +180,19 @@ int vs_draft_propose(const void* logits, int dtype, int n, int S, int V, int64_t
 
 size_t vs_draft_workspace_bytes(int n, int S, int V);
 
+/* Polls an inter-workgroup wait of vs_sample_batch / vs_sample_batch_state makes before it gives up and flags its
+ * row VS_OUT_TIMEOUT (0 restores the default, ~2M polls). A testing hook: a tiny limit forces the timeout path, whose
+ * rows report VS_OUT_TIMEOUT, commit no request state and leave the workspace zeroed. Applies to later calls of the
+ * process. No counterpart in the reference (its sampler is single-threaded host code). */
+int vs_set_spin_limit(unsigned polls);
+
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 4. */
+/* Library ABI version (increments on any signature or struct change): 5. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -1,0 +1,88 @@
+"""The timeout path of the sampling kernel, forced from the host with a tiny spin limit (vs_set_spin_limit), so
+that every kernel still exits normally: FULL-class rows, whose workgroups meet at row barriers, report
+VS_OUT_TIMEOUT instead of hanging; rows that finished are correct; no request state is committed for a flagged row;
+and the workspace is left zeroed, so the next ordinary call is exact without a reset."""
+import numpy as np
+import pytest
+import torch
+
+from volundr_amd import DeviceSamplers, Sampler, VsError, _lib, ops, synth
+from volundr_amd._lib import OUT_TIMEOUT
+from volundr_amd.session import Sampling
+
+pytestmark = pytest.mark.gpu
+
+
+def _flags(out):
+    return [int(f) & 0xFFFFFFFF for f in out.flags.cpu().tolist()]
+
+
+def _forced(fn):
+    L = _lib.load()
+    L.vs_set_spin_limit(1)
+    try:
+        r = fn()
+        torch.cuda.synchronize()
+    finally:
+        L.vs_set_spin_limit(0)
+    return r
+
+
+def test_timeouts_flagged_and_workspace_left_clean(dev):
+    d = synth.CONFIGS["c3"](seed=1)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    V = x.shape[1]
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
+    clean = ops.sample_rows(x, rows)
+    ids0, lp0, fl0 = clean.ids.cpu().tolist(), clean.logprobs.cpu().tolist(), _flags(clean)
+    assert not any(f & OUT_TIMEOUT for f in fl0)
+    print("[timeout] forced run, c3 seed 1", flush=True)
+    t = _forced(lambda: ops.sample_rows(x, rows))
+    fl = _flags(t)
+    timed = [bool(f & OUT_TIMEOUT) for f in fl]
+    assert any(timed)
+    ids = t.ids.cpu().tolist()
+    for r in range(len(fl)):
+        if not timed[r]:
+            assert ids[r] == ids0[r], r
+    again = ops.sample_rows(x, rows)  # no reset: the timed-out rows left the workspace zeroed
+    assert again.ids.cpu().tolist() == ids0
+    assert again.logprobs.cpu().tolist() == lp0
+    assert _flags(again) == fl0
+
+
+def test_sampler_raises_on_timeout_and_recovers(dev):
+    sp = Sampling(temperature=0.8, top_p=0.9)  # FULL class on a full-vocabulary row: row barriers
+    s = Sampler(sp, vocab_valid=163840, request_id=3)
+    x = torch.randn(163840, generator=torch.Generator().manual_seed(2)).to(dev)
+    rng0, n0 = s.rng, len(s.history)
+    with pytest.raises(VsError):
+        _forced(lambda: s.sample(x))
+    tok = s.sample(x)  # works again (the draw of the failed call was consumed by Sampler.uniform, as on the host)
+    assert 0 <= tok < 163840
+    assert s.rng != rng0 and len(s.history) == n0  # sample() does not accept
+
+
+def test_device_state_not_committed_for_timed_out_rows(dev):
+    d = synth.CONFIGS["c3"](seed=2)
+    B, V = d["logits"].shape
+    samplers = []
+    for r, sp in enumerate(d["params"]):
+        s = Sampler(sp, vocab_valid=V, request_id=r)
+        s.rng = 0x1234567 ^ r
+        samplers.append(s)
+    ds = DeviceSamplers(samplers, V, hist_cap=64, device=dev)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    st0 = ds.host_state().copy()
+    out = _forced(lambda: ds.step(x))
+    fl = _flags(out)
+    st1 = ds.host_state()
+    assert any(f & OUT_TIMEOUT for f in fl)
+    for r in range(B):
+        if fl[r] & OUT_TIMEOUT:
+            assert st1[r]["produced"] == st0[r]["produced"] and st1[r]["rng"] == st0[r]["rng"], r
+            assert st1[r]["hist_len"] == st0[r]["hist_len"], r
+        else:
+            assert st1[r]["produced"] == st0[r]["produced"] + 1, r
+    out2 = ds.step(x)  # the next step runs normally
+    assert not any(f & OUT_TIMEOUT for f in _flags(out2))

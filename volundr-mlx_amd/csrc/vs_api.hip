@@ -11,6 +11,7 @@ namespace vs {
 
 static thread_local std::string g_err;
 unsigned long long* g_trace = nullptr;
+unsigned g_spin_limit = 0;
 
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(int code, const std::string& msg) {
@@ -48,7 +49,12 @@ extern "C" {
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 4; }
+int vs_version(void) { return 5; }
+
+int vs_set_spin_limit(unsigned polls) {
+  vs::g_spin_limit = polls;
+  return VS_OK;
+}
 
 #ifdef VS_TRACE
 void vs_debug_set_trace(void* p) { vs::g_trace = (unsigned long long*)p; }

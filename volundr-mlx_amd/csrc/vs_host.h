@@ -19,6 +19,9 @@ struct DevInfo {
 // Properties of the current device (cached per device).
 const DevInfo* dev_info();
 
+// Polls of an inter-workgroup wait before it gives up (0: the default). Set by vs_set_spin_limit.
+extern unsigned g_spin_limit;
+
 // Phase-timestamp buffer of development builds (VS_TRACE); always null in the shipped library.
 extern unsigned long long* g_trace;
 

@@ -2331,7 +2331,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.lds_ch = lds_ch;
   a.kcap = kcap;
   a.kmax = kmax;
-  a.spin_limit = 1u << 21;
+  a.spin_limit = g_spin_limit ? g_spin_limit : 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.params = list_k > 0 ? nullptr : params;
   a.list_k = list_k;

@@ -39,10 +39,10 @@ STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4")
                         ("produced", "<i4"), ("min_new_tokens", "<i4")])
 assert STATE_DTYPE.itemsize == 32
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
-           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_workspace_init", "vs_last_error", "vs_version")
+           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version")
 
 _lib = None
 
@@ -69,6 +69,8 @@ def load():
     L.vs_lmhead_verify_greedy.restype = i32
     L.vs_lmhead_workspace_bytes.argtypes = [i32, i32]
     L.vs_lmhead_workspace_bytes.restype = sz
+    L.vs_set_spin_limit.argtypes = [ctypes.c_uint]
+    L.vs_set_spin_limit.restype = i32
     L.vs_topk_batch.argtypes = [vp, i32, i32, i32, i64, i32, vp, vp, vp, sz, vp]
     L.vs_topk_batch.restype = i32
     L.vs_draft_walk.argtypes = [vp, vp, i32, vp, vp, vp, i32, i32, vp, i32, i32, i32, vp, vp]
