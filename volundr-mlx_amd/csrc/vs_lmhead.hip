@@ -29,17 +29,8 @@ namespace vs {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-#ifndef LH_NT
-#define LH_NT 512
-#endif
-constexpr int LNT = LH_NT;          // threads per workgroup
+constexpr int LNT = 512;            // threads per workgroup
 constexpr int LNW = LNT / WAVE;     // waves per workgroup
-#ifndef LH_NTW12
-#define LH_NTW12 4
-#endif
-#ifndef LH_WPC
-#define LH_WPC 1
-#endif
 constexpr int KS = 32;              // k per MFMA
 constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
 constexpr int LPMAX = 2048;         // workgroups per launch
@@ -90,7 +81,7 @@ __device__ __forceinline__ void lse_merge(float& m, double& s, float m2, double 
 
 // KC: k per LDS chunk (512 where K allows and two chunks of RP rows fit the LDS: fewer barriers; else 256)
 template <int NTT, int NTW, int KC>
-__global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 * LH_WPC))) void vs_lmhead_verify_kernel(
+__global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))) void vs_lmhead_verify_kernel(
     LHArgs A) {
   constexpr int RP = 16 * NTT;  // positions padded to whole MFMA tiles
   constexpr int SPC = KC / KS;
@@ -251,9 +242,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256 *
           const uint32_t f0 = wrap ? no0[j] : wo0[j], f1 = wrap ? no1[j] : wo1[j];
           wb[j][0] = *(const uint4*)(fb + (f0 + (uint32_t)gn * 4 * KS));
           wb[j][1] = *(const uint4*)(fb + (f1 + (uint32_t)gn * 4 * KS));
-#ifndef LH_NO_PIN
           __builtin_amdgcn_sched_barrier(0);  // keep the next group's loads here, one group ahead of their use
-#endif
 #pragma unroll
           for (int tt = 0; tt < NTT; ++tt) {
             acc[j][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, s0), hb0[tt],
@@ -475,15 +464,15 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   a.ldo = ldo;
   a.ws = (char*)ws;
   a.trace = g_trace;
-  int P = dv->cus * LH_WPC;  // LH_WPC workgroups per CU, each over a contiguous range of vocabulary tiles
+  int P = dv->cus;  // one workgroup per CU, each over a contiguous range of vocabulary tiles
   if (P > a.ntiles) P = a.ntiles;
   if (P > LPMAX) P = LPMAX;
   const int ntt = (int)((R + 15) / 16);
   switch (ntt) {
-    case 1: return kc512 ? lmhead_launch<1, LH_NTW12, 512>(a, P, (hipStream_t)stream)
-                         : lmhead_launch<1, LH_NTW12, 256>(a, P, (hipStream_t)stream);
-    case 2: return kc512 ? lmhead_launch<2, LH_NTW12, 512>(a, P, (hipStream_t)stream)
-                         : lmhead_launch<2, LH_NTW12, 256>(a, P, (hipStream_t)stream);
+    case 1: return kc512 ? lmhead_launch<1, 4, 512>(a, P, (hipStream_t)stream)
+                         : lmhead_launch<1, 4, 256>(a, P, (hipStream_t)stream);
+    case 2: return kc512 ? lmhead_launch<2, 4, 512>(a, P, (hipStream_t)stream)
+                         : lmhead_launch<2, 4, 256>(a, P, (hipStream_t)stream);
     case 3: return lmhead_launch<3, 4, 256>(a, P, (hipStream_t)stream);
     case 4: return lmhead_launch<4, 2, 256>(a, P, (hipStream_t)stream);
     default: return lmhead_launch<5, 2, 256>(a, P, (hipStream_t)stream);

@@ -403,18 +403,16 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   const int chmax = VNV_MAX * unit;
   int gmin = (vocab_valid + chmax - 1) / chmax;
   if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
-  // About VS_VERIFY_NVT 16-byte loads per lane (measured best on MI355X: less work per workgroup
+  // About NVT 16-byte loads per lane (measured best on MI355X: less work per workgroup
   // adds merge and arrival overhead, more lengthens each workgroup's chain), but never more workgroups than are
   // resident at once (a second wave would start only after the first finished).
-#ifndef VS_VERIFY_NVT
-#define VS_VERIFY_NVT 6
-#endif
+  constexpr int NVT = 6;
   const void* kfn = dtype == VS_F32 ? (const void*)vs_verify_kernel<VS_F32>
                     : dtype == VS_BF16 ? (const void*)vs_verify_kernel<VS_BF16>
                                        : (const void*)vs_verify_kernel<VS_F16>;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, VNT, 0) != hipSuccess || per_cu < 1) per_cu = 1;
-  int G = (vocab_valid + VS_VERIFY_NVT * unit - 1) / (VS_VERIFY_NVT * unit);
+  int G = (vocab_valid + NVT * unit - 1) / (NVT * unit);
   const int gres = (per_cu * dv->cus) / R;
   if (G > gres) G = gres;
   const int gf = (vocab_valid + VNF * unit - 1) / (VNF * unit);  // the fewest workgroups the fast path allows
