@@ -113,6 +113,16 @@ def test_bf16_rows(dev):
     run(dev, x, ps, rng.random(B), dtype=torch.bfloat16, label="bf16")  # many exact ties after rounding
 
 
+@pytest.mark.parametrize("V", [30000, 163840])
+def test_f16_rows(dev, V):
+    rng = np.random.default_rng(8)
+    B = 6
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    hists = [rng.integers(0, V, size=int(rng.integers(0, 500))) for _ in range(B)]
+    run(dev, x, ps, rng.random(B), hists, dtype=torch.float16, label=f"f16 V{V}")
+
+
 def test_coop_path_near_flat(dev):
     rng = np.random.default_rng(11)
     B, V = 4, 50000
