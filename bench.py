@@ -285,13 +285,14 @@ def main():
             others["draft_propose"] = entry(oe, ok, we, ab, DRAFT_S)
             others["draft_propose"]["workload"] = ("DFlash2 propose: top-16 of bf16 logits [7, 248320] (248077 valid) "
                                                    "+ 7-slot walk, rank-256 codebooks; 2 kernels per step")
-        for (bb, tt) in ((1, 17), (4, 17)):
+        for (bb, tt) in ((1, 17), (4, 17), (16, 1)):
             key = f"lmhead_verify_b{bb}t{tt}"
             if not sel(key):
                 continue
             (fe, fk), (ue, uk), ab = bench_lmhead(torch, dev, a.steps, a.warmup, bb, tt)
             others[key] = entry(fe, fk, fe, ab, bb * tt)
-            others[key]["workload"] = (f"bf16 lm_head 5120 -> 248320 + greedy verify, B={bb} T={tt}: fused kernel; "
+            what = "greedy decode (argmax + logprob)" if tt == 1 else "greedy verify"
+            others[key]["workload"] = (f"bf16 lm_head 5120 -> 248320 + {what}, B={bb} T={tt}: fused kernel; "
                                        "'unfused_us_per_step' = torch bf16 matmul (logits to HBM) + vs_verify_greedy")
             others[key]["unfused_us_per_step"] = round(ue, 2)
             others[key]["frac_of_8tbs"] = round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)
