@@ -35,12 +35,16 @@ def _check_walk(got, uval, cid, hp, A, B, anchors):
     return checked
 
 
-@pytest.mark.parametrize("V,k,dt", [(163840, 16, torch.float32), (151936, 16, torch.bfloat16),
-                                    (5003, 1, torch.float32), (40000, 50, torch.float16),
-                                    (163840, 256, torch.bfloat16)])
-def test_topk_batch_exact(dev, V, k, dt):
-    g = torch.Generator().manual_seed(V + k)
-    x = (torch.randn(14, V, generator=g) * 3).to(dt)
+# 14 rows: 18 workgroups per row (lists merged by heads); 16, 20 and 64 rows: 16, 12 and 4 (merged by rank)
+@pytest.mark.parametrize("V,k,dt,B", [(163840, 16, torch.float32, 14), (151936, 16, torch.bfloat16, 14),
+                                      (5003, 1, torch.float32, 14), (40000, 50, torch.float16, 14),
+                                      (163840, 256, torch.bfloat16, 14), (163840, 50, torch.float32, 16),
+                                      (151936, 16, torch.bfloat16, 20), (5003, 1, torch.float32, 16),
+                                      (40000, 256, torch.float16, 20), (163840, 20, torch.bfloat16, 64),
+                                      (70000, 3, torch.float32, 64)])
+def test_topk_batch_exact(dev, V, k, dt, B):
+    g = torch.Generator().manual_seed(V + k + B)
+    x = (torch.randn(B, V, generator=g) * 3).to(dt)
     ids, vals = topk_batch(x.to(dev), k)
     xf = x.float().numpy()
     for r in range(x.shape[0]):
@@ -49,16 +53,20 @@ def test_topk_batch_exact(dev, V, k, dt):
         np.testing.assert_array_equal(vals[r].cpu().numpy(), wv)
 
 
-def test_topk_batch_ties_and_short_rows(dev):
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("B", [6, 16, 40])
+def test_topk_batch_ties_and_short_rows(dev, B):
+    rng = np.random.default_rng(5 + B)
     V = 9000
-    x = rng.integers(-3, 4, size=(6, V)).astype(np.float32)  # heavy ties: the lower id wins
+    x = rng.integers(-3, 4, size=(B, V)).astype(np.float32)  # heavy ties: the lower id wins
     x[1, :] = -np.inf
     x[1, [7, 4000, 8999]] = [1.0, 1.0, -2.0]  # three finite logits: 13 of 16 padded
     x[2, :] = -np.inf  # no finite logit at all
     x[3, 100:200] = np.nan  # NaN never enters the list
+    x[4, :] = -np.inf
+    x[4, 8990:] = rng.standard_normal(10)  # every finite logit in the last workgroup's chunk: one list is full
+    x[5, ::700] = np.inf  # +inf is not finite: never listed
     ids, vals = topk_batch(torch.from_numpy(x).to(dev), 16)
-    for r in range(6):
+    for r in range(B):
         wi, wv = D.topk_sorted(x[r], 16)
         assert ids[r].cpu().numpy().tolist() == wi.tolist(), r
         np.testing.assert_array_equal(vals[r].cpu().numpy(), wv)

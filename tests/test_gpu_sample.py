@@ -37,15 +37,16 @@ def rand_params(rng, n, V):
     return ps
 
 
+# 12 rows: 21 workgroups per row (top-k lists merged by heads); 24 rows: 10 (merged by rank)
 @pytest.mark.parametrize("V", [1000, 5003, 40000])
 @pytest.mark.parametrize("seed", [0, 1])
-def test_random_mix(dev, V, seed):
-    rng = np.random.default_rng(100 + seed)
-    B = 12
+@pytest.mark.parametrize("B", [12, 24])
+def test_random_mix(dev, V, seed, B):
+    rng = np.random.default_rng(100 + seed + B)
     x = (rng.standard_normal((B, V)) * rng.choice([0.2, 1.0, 3.0], size=(B, 1))).astype(np.float32)
     ps = rand_params(rng, B, V)
     hists = [rng.integers(0, V, size=int(rng.integers(0, 300))) for _ in range(B)]
-    run(dev, x, ps, rng.random(B), hists, label=f"mix V{V} s{seed}")
+    run(dev, x, ps, rng.random(B), hists, label=f"mix V{V} s{seed} B{B}")
 
 
 @pytest.mark.parametrize("k", [50, 256])

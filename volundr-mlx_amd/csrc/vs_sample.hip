@@ -1214,6 +1214,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     const int k = top_k;
     if (t == 0) {
       s.misc[4] = 0;
+      s.misc[9] = 0;
       s.misc[14] = 0;
     }
     float fmx = -__builtin_inff();
@@ -1335,54 +1336,97 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     VS_TR(A, 3);
     if (arrive_done()) {
       VS_TR(A, 4);
-      // ---- merge (last workgroup of the row). Each list holds its workgroup's sorted local top-kc. With r =
-      // ceil(k / G) heads per list, M = the keff-th largest head bounds the global keff-th key from below; the
-      // survivors >= M (at most keff + G * r) contain the global top-keff. ----
-      const int lkr = __builtin_ctz((unsigned)kr);
-      const int tot = G * kr;  // <= G * kcap <= KEYS_CAP
-      const int r = (k + G - 1) / G;
-      const int nh = G * r;
-      u64* heads = s.keys;           // nh <= k + G <= 320
-      u64* hs = s.keys + 512;        // keff largest heads
-      u64* sel = (u64*)s.xv;         // survivors (the chunk is no longer needed)
-      u64 r8[KEYS_CAP / SNT];        // all lists, loaded in one round trip
+      int n, keff;
+      u64 bam;
+      // ---- merge (last workgroup of the row). Each list holds its workgroup's sorted local top-kc (zero padded to
+      // kr). A lower bound M of the row's keff-th key leaves few survivors >= M, which are ranked; the bound:
+      //  * nh = G * r <= 64 (r = ceil(k / G) heads per list): when >= keff heads are non-zero, M = the lowest key
+      //    of the keff-th largest head value (>= keff heads, all keys of the row, are >= M, so its keff-th key is
+      //    >= M), else 0;
+      //  * otherwise: the smallest r-th key of the lists that hold >= r keys, valid when those lists number
+      //    >= keff / r (they alone hold >= keff keys >= it), else 0.
+      // Every wave loads the heads and list summaries and derives M itself (ballots over the heads, one per lane),
+      // so the survivors go straight from the registers to one LDS array: a single barrier before the rank. ----
+      {
+        const int lkr = __builtin_ctz((unsigned)kr);
+        const int tot = G * kr;  // <= G * kcap <= KEYS_CAP
+        const int r = (k + G - 1) / G;
+        const int nh = G * r;
+        u64* sel = s.keys;  // survivors (<= tot)
+        u64 r8[KEYS_CAP / SNT];  // all lists, loaded in one round trip
 #pragma unroll
-      for (int u = 0; u < KEYS_CAP / SNT; ++u) {
-        const int idx = t + u * SNT;
-        r8[u] = idx < tot ? ld_dev(&cand[(idx >> lkr) * A.kcap + (idx & (kr - 1))]) : (u64)0;
-      }
-      int nf2 = 0, nz2 = 0;
-      u64 k2 = 0;
-      if (t < G) {
-        nf2 = (int)ld_dev(&parts[t].nfin);
-        k2 = ld_dev(&parts[t].amkey);
-        const int kcg = (int)ld_dev(&parts[t].kc);
-        nz2 = kcg < r ? kcg : r;
-      }
-#pragma unroll
-      for (int u = 0; u < KEYS_CAP / SNT; ++u) {
-        const int idx = t + u * SNT;
-        const int j = idx & (kr - 1);
-        if (idx < tot && j < r) heads[(idx >> lkr) * r + j] = r8[u];
-      }
-      if (t < WAVE) {
-        const int nn = wave_sum(nf2);
-        const int nz = wave_sum(nz2);
-        const u64 bam2 = wave_max(k2);
-        if (t == 0) {
-          s.misc[7] = nn;
-          s.misc[12] = nz;
-          s.red64[0] = bam2;
-          s.misc[9] = 0;
+        for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+          const int idx = t + u * SNT;
+          r8[u] = idx < tot ? ld_dev(&cand[(idx >> lkr) * A.kcap + (idx & (kr - 1))]) : (u64)0;
         }
+        const int ln = lane_id();
+        int nf2 = 0, full = 0;
+        u64 k2 = 0, h2 = ~(u64)0, hd = 0;
+        if (ln < G) {
+          nf2 = (int)ld_dev(&parts[ln].nfin);
+          k2 = ld_dev(&parts[ln].amkey);
+          full = (int)ld_dev(&parts[ln].kc) >= r;
+          const u64 h = ld_dev(&cand[ln * A.kcap + r - 1]);
+          h2 = full ? h : h2;
+        }
+        if (nh <= WAVE && ln < nh) hd = ld_dev(&cand[(ln / r) * A.kcap + ln % r]);
+        n = wave_sum(nf2);
+        bam = wave_max(k2);
+        keff = k < n ? k : n;  // sampler.py:133-134
+        if (keff < 1) keff = 1;
+        u64 M;
+        if (nh <= WAVE) {
+          // th = the largest value with >= keff heads of value >= th: a most-significant-bit-first bisection with
+          // ballots on the heads' value bits (the key's upper word); M = th's lowest key
+          const uint32_t hh = (uint32_t)(hd >> 32);
+          const int nzh = __popcll(__ballot(hh != 0));
+          uint32_t th = 0;
+#pragma unroll
+          for (int b = 31; b >= 0; --b) {
+            const uint32_t c = th | (1u << b);
+            th = __popcll(__ballot(hh >= c)) >= keff ? c : th;
+          }
+          M = nzh >= keff ? (u64)th << 32 : (u64)0;
+        } else {
+          const int nfull = wave_sum(full);
+          const u64 mb = wave_min(h2);
+          M = nfull * r >= keff ? mb : (u64)0;
+        }
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+          const u64 x = r8[u];
+          cnt += ((x != 0) & (x >= M) & (((t + u * SNT) & (kr - 1)) < keff)) ? 1 : 0;
+        }
+        int p = wave_alloc(cnt, &s.misc[9]);
+        if (cnt) {
+#pragma unroll
+          for (int u = 0; u < KEYS_CAP / SNT; ++u) {
+            const u64 x = r8[u];
+            if ((x != 0) & (x >= M) & (((t + u * SNT) & (kr - 1)) < keff)) sel[p++] = x;
+          }
+        }
+        __syncthreads();
+        const int Sv = s.misc[9];
+        VS_TR(A, 14);
+        if (n > 0) {
+          if (Sv <= RANK_MAX) {
+            rank_sort(sel, Sv, s.tk, keff);  // sampler.py:140 on the survivors
+          } else {
+            // many survivors (no useful bound): radix-select the keff-th key, then rank the keff keys above it
+            if (t == 0) s.misc[10] = 0;
+            __syncthreads();
+            const u64 T = block_kth(s, sel, Sv, keff);
+            u64* sel2 = (u64*)s.xv;
+#pragma unroll
+            for (int u = 0; u < KEYS_CAP / SNT; ++u)
+              if (r8[u] != 0 && r8[u] >= T) sel2[atomicAdd(&s.misc[10], 1)] = r8[u];
+            __syncthreads();
+            rank_sort(sel2, keff, s.tk, keff);
+          }
+        }
+        VS_TR(A, 6);
       }
-      __syncthreads();
-      VS_TR(A, 14);
-      const int n = s.misc[7];
-      const int nzh = s.misc[12];  // non-zero heads
-      const u64 bam = s.red64[0];
-      int keff = k < n ? k : n;  // sampler.py:133-134
-      if (keff < 1) keff = 1;
       // top-list mode (vs_topk_batch): the sorted list, id -1 and value -inf past the row's finite logits
       auto write_list = [&](int have) {
         const int r = A.row0 + row;
@@ -1402,57 +1446,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           f.keep = 0;
           write_out(A, row, f, st, rng_next);
         }
+      } else if (A.list_k > 0) {
+        write_list(keff);
       } else {
-        u64 M = 0;  // 0: fewer than keff heads, no bound
-        if (nzh >= keff) {
-          rank_sort(heads, nh, hs, keff);
-          M = hs[keff - 1];
-        }
-        VS_TR(A, 17);
-        {  // survivors, straight from the registers
-          int cnt = 0;
-#pragma unroll
-          for (int u = 0; u < KEYS_CAP / SNT; ++u) cnt += (r8[u] != 0 && r8[u] >= M) ? 1 : 0;
-          int p = wave_alloc(cnt, &s.misc[9]);
-          if (cnt) {
-#pragma unroll
-            for (int u = 0; u < KEYS_CAP / SNT; ++u)
-              if (r8[u] != 0 && r8[u] >= M) {
-                if (p < RANK_MAX) sel[p] = r8[u];
-                ++p;
-              }
-          }
-        }
-        __syncthreads();
-        const int Cm = s.misc[9];
-        VS_TR(A, 5);
-        if (Cm <= RANK_MAX) {
-          rank_sort(sel, Cm, s.tk, keff);  // sampler.py:140 on the survivors
-        } else {
-          // many survivors (a few lists hold most of the top keys): radix-select the keff-th key of all lists
-#pragma unroll
-          for (int u = 0; u < KEYS_CAP / SNT; ++u)
-            if (t + u * SNT < tot) s.keys[t + u * SNT] = r8[u];
-          if (t == 0) s.misc[10] = 0;
-          __syncthreads();
-          const u64 T = block_kth(s, s.keys, tot, keff);
-#pragma unroll
-          for (int u = 0; u < KEYS_CAP / SNT; ++u)
-            if (r8[u] != 0 && r8[u] >= T) {
-              const int p = atomicAdd(&s.misc[10], 1);
-              if (p < RANK_MAX) sel[p] = r8[u];
-            }
-          __syncthreads();
-          rank_sort(sel, keff, s.tk, keff);
-        }
-        VS_TR(A, 6);
-        if (A.list_k > 0) {
-          write_list(keff);
-        } else {
-          const Final f = wave_sample(s, s.tk, keff, P);
-          VS_TR(A, 7);
-          write_out(A, row, f, st, rng_next);
-        }
+        const Final f = wave_sample(s, s.tk, keff, P);
+        VS_TR(A, 7);
+        write_out(A, row, f, st, rng_next);
       }
       cleanup(0);
     }
