@@ -1644,6 +1644,39 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (t == 0) s.misc[15] = 0;
         // every position's fine-bin id (0xFFFF = not kept), so that the later passes test a u16 per position
         uint16_t* fid = (uint16_t*)(s.keys + FID_OFF);
+        // Visit the chunk positions whose fine-bin id satisfies PRED (a test on `id` alone, false for 0xFFFF): the
+        // ids are read eight at a time (16-byte LDS reads, four in flight per lane) and tested without branches;
+        // BODY runs for the (few) positions that pass, with i = the position in the chunk. The id array is
+        // initialised to 0xFFFF over the whole chunk area, so the last group's tail never passes.
+#define FOR_FID(PRED, BODY)                                                        \
+  {                                                                                \
+    const int n8_ = (hi - lo + 7) / 8;                                             \
+    const uint4* f4_ = (const uint4*)fid;                                          \
+    for (int w0_ = t; w0_ < n8_; w0_ += 4 * SNT) {                                 \
+      uint4 q_[4];                                                                 \
+      _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                           \
+        const int w_ = w0_ + u_ * SNT;                                             \
+        q_[u_] = f4_[w_ < n8_ ? w_ : 0];                                           \
+      }                                                                            \
+      _Pragma("unroll") for (int u_ = 0; u_ < 4; ++u_) {                           \
+        const int w_ = w0_ + u_ * SNT;                                             \
+        const uint32_t wd_[4] = {q_[u_].x, q_[u_].y, q_[u_].z, q_[u_].w};          \
+        uint32_t hm_ = 0;                                                          \
+        _Pragma("unroll") for (int h_ = 0; h_ < 8; ++h_) {                         \
+          const uint32_t id = (wd_[h_ >> 1] >> (16 * (h_ & 1))) & 0xFFFFu;         \
+          hm_ |= (PRED) ? (1u << h_) : 0u;                                         \
+        }                                                                          \
+        hm_ = w_ < n8_ ? hm_ : 0u;                                                 \
+        while (hm_) {                                                              \
+          const int h_ = __builtin_ctz(hm_);                                       \
+          hm_ &= hm_ - 1;                                                          \
+          const int i = 8 * w_ + h_;                                               \
+          const uint32_t id = (wd_[h_ >> 1] >> (16 * (h_ & 1))) & 0xFFFFu;         \
+          BODY                                                                     \
+        }                                                                          \
+      }                                                                            \
+    }                                                                              \
+  }
         for (int v = t; v < A.CH / 8; v += SNT) ((uint4*)fid)[v] = make_uint4(~0u, ~0u, ~0u, ~0u);
         hist_clear(s);
         __syncthreads();
@@ -1802,21 +1835,23 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               __syncthreads();
               VS_TRX(46);
-              for (int i = t; i < hi - lo; i += SNT) {
-                const uint32_t id = fid[i];
-                const int c = (int)(id >> 8);
-                int j = -1;
+              // the selected coarse digits, -1 for unused set slots (a valid id never has digit -1)
+              static_assert(NSET == 4, "the fine-bin test below names four set slots");
+              int sd4[NSET];
 #pragma unroll
-                for (int q = 0; q < NSET; ++q) j = (q < ns && set[q] == c) ? q : j;
-                if (id != 0xFFFFu && j >= 0) {
-                  u64 fx;
-                  const double pr = mass(s.xv[i] / tt, &fx);
-                  const int b2 = j * NBIN + (int)(id & 0xFF);
-                  atomicAdd(&s.fc[b2], 1u);
-                  atomicAdd(&s.ffix[b2], fx);
-                  unsafeAtomicAdd(&s.ff64[b2], pr);
-                }
-              }
+              for (int q = 0; q < NSET; ++q) sd4[q] = q < ns ? set[q] : -1;
+              FOR_FID((id != 0xFFFFu) & (((int)(id >> 8) == sd4[0]) | ((int)(id >> 8) == sd4[1]) |
+                                          ((int)(id >> 8) == sd4[2]) | ((int)(id >> 8) == sd4[3])),
+                      {
+                        const int c = (int)(id >> 8);
+                        const int j = sd4[1] == c ? 1 : (sd4[2] == c ? 2 : (sd4[3] == c ? 3 : 0));
+                        u64 fx;
+                        const double pr = mass(s.xv[i] / tt, &fx);
+                        const int b2 = j * NBIN + (int)(id & 0xFF);
+                        atomicAdd(&s.fc[b2], 1u);
+                        atomicAdd(&s.ffix[b2], fx);
+                        unsafeAtomicAdd(&s.ff64[b2], pr);
+                      })
               __syncthreads();
               VS_TR(A, 15);
               HistSlot* h2 = hslots + slot;
@@ -1906,13 +1941,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 } else {
                   if (t == 0) s.misc[16] = 0;
                   __syncthreads();
-                  for (int i = t; i < hi - lo; i += SNT) {
-                    const int id = (int)fid[i];
-                    if (id != 0xFFFF && ((has_tp && id == lp_.id) || (id <= la.id && id >= lb.id))) {
-                      const int p = atomicAdd(&s.misc[16], 1);
-                      if (p < FID_OFF) s.keys[p] = key64(s.xv[i], (uint32_t)(lo + i));
-                    }
-                  }
+                  const int tpid = has_tp ? lp_.id : -1, laid = la.id, lbid = lb.id;
+                  FOR_FID((id != 0xFFFFu) & (((int)id == tpid) | (((int)id <= laid) & ((int)id >= lbid))), {
+                    const int p = atomicAdd(&s.misc[16], 1);
+                    if (p < FID_OFF) s.keys[p] = key64(s.xv[i], (uint32_t)(lo + i));
+                  })
                   __syncthreads();
                   const int nloc = s.misc[16];  // <= gcount <= GCAP2
                   if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
