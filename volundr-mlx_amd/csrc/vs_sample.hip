@@ -1960,6 +1960,76 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   VS_TR(A, 7);
                   // ---- final: exact key order inside the located fine bins ----
                   const int m = (int)ld_relaxed(&ctl->g2count);
+                  if (m <= WAVE) {
+                    // Few gathered keys (the usual case): one wave sorts them (descending key) and answers both
+                    // picks with scans and ballots, no barrier. A fine bin's members are contiguous in key order,
+                    // so the in-bin cumulative masses are masked scans of the sorted keys.
+                    if (t < WAVE) {
+                      u64 e1[1] = {t < m ? ld_dev(&gather[t]) : (u64)0};
+                      wave_sort_desc<1>(e1);
+                      const u64 kk = e1[0];
+                      const float xs = key_value(kk) / tt;
+                      const int fi = kk != 0 ? fine_of(xs) : -1;
+                      u64 fx = 0;
+                      const double pr = kk != 0 ? mass(xs, &fx) : 0.0;
+                      struct WPick {
+                        u64 key, cnt_in, fix_in, fix;
+                        double f64_in, f64;
+                      };
+                      // first member (descending key) of fine bin `id` whose in-bin cumulative mass reaches
+                      // `tgt`, else the bin's last member
+                      auto wpick = [&](int id, double tgt) -> WPick {
+                        const bool mem = fi == id;
+                        const u64 w = mem ? fx : (u64)0;
+                        const double wf = mem ? pr : 0.0;
+                        const u64 inc = wave_scan(w);
+                        const double incf = wave_scan(wf);
+                        const unsigned long long mm = __ballot(mem);
+                        const unsigned long long hb = __ballot(mem & ((double)inc >= tgt));
+                        const int ln = hb ? __ffsll((long long)hb) - 1 : (mm ? 63 - __clzll((long long)mm) : 0);
+                        WPick pk;
+                        pk.key = mm ? lane_bcast(kk, ln) : (u64)0;
+                        pk.fix = mm ? lane_bcast(w, ln) : (u64)0;
+                        pk.fix_in = mm ? lane_bcast(inc - w, ln) : (u64)0;
+                        pk.f64 = mm ? lane_bcast(wf, ln) : 0.0;
+                        pk.f64_in = mm ? lane_bcast(incf - wf, ln) : 0.0;
+                        pk.cnt_in = (u64)__popcll(mm & ((1ull << ln) - 1ull));
+                        return pk;
+                      };
+                      uint32_t flags = VS_OUT_COOP;
+                      int keep = total;
+                      u64 zfix = Sfix;
+                      double zf = Sf;
+                      if (has_tp) {  // sampler.py:145-148
+                        const WPick pp = wpick(lp_.id, tgt_p - (double)lp_.fix_before);
+                        keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
+                        zfix = lp_.fix_before + pp.fix_in + pp.fix;
+                        zf = lp_.f64_before + pp.f64_in + pp.f64;
+                        const double tol = 1e-6 * (double)Sfix;
+                        if (fabs((double)(zfix - pp.fix) - tgt_p) < tol || fabs((double)zfix - tgt_p) < tol)
+                          flags |= VS_OUT_TOPP_BOUNDARY;
+                      }
+                      // sampler.py:153-156
+                      const double tgt_d = P.u * (double)zfix;
+                      const Loc ld = locate(tgt_d);
+                      const WPick pd = wpick(ld.id, tgt_d - (double)ld.fix_before);
+                      const float d = key_value(pd.key) / tt - xs0;
+                      const double before = (double)(ld.fix_before + pd.fix_in);
+                      const double tol = 1e-6 * (double)zfix;
+                      if (fabs(before - tgt_d) < tol || fabs(before + (double)pd.fix - tgt_d) < tol)
+                        flags |= VS_OUT_DRAW_BOUNDARY;
+                      fin.token = (int32_t)key_index(pd.key);
+                      fin.lp = (float)((double)d - log(zf));
+                      fin.keep = keep;
+                      fin.flags = flags;
+                      VS_TR(A, 8);
+                      write_out(A, row, fin, st, rng_next);
+                    }
+                    __syncthreads();
+                    cleanup(slot);
+                    VS_TR_FLUSH(A);
+                    return;
+                  }
                   u64* fk = s.keys;
                   int* fi = (int*)(s.keys + GCAP2);
                   u64* fxs = s.keys + GCAP2 + GCAP2 / 2;
