@@ -110,6 +110,7 @@ struct SampleArgs {
   int kmax;    // largest top_k of the TOPK class for this launch
   uint32_t spin_limit;
   double fix_scale;  // probability -> fixed point
+  double zspan_max;     // ln(fix_scale) - ln(1e6): the kept-value span up to which z comes from fixed point
   const vs_row_params* params;
   vs_row_state* state;  // device-resident request state, or null
   int list_k;           // > 0: top-list mode (vs_topk_batch): every row publishes its list_k largest logits, sorted
@@ -1627,6 +1628,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // c = f >> 8) and 255 - (f & 255) (fine), so that the 256-bin scan walks them in descending-logit order.
         const float span = xs0 - xs_lo;
         const float fscale = span > 0.0f ? 65536.0f / span : 0.0f;
+        // The logprob's normaliser z (the kept mass, sampler.py:153) comes from the exact fixed-point sums when
+        // every kept mass is >= exp(-span) >= 1e6 / scale: each mass then carries a relative rounding error
+        // <= 5e-7, and so does every partial sum of them, far inside the logprob tolerance. Otherwise (masses down
+        // to exp(-40)) the passes also keep float64 sums per bin.
+        const bool zfix_only = (double)span <= A.zspan_max;
+        const double inv_scale = 1.0 / scale;  // a power of two: exact
         auto fine_of = [&](float xs) -> int {  // xs = x / t
           const float u = xs0 - xs;
           int f = (int)(u * fscale);
@@ -1683,26 +1690,31 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // With few qualifying lanes the kept logits are also listed in LDS for the gather below; otherwise the
         // kept count exceeds GSMALL and no gather happens.
         const bool few = nq * 4 <= SNT;
-        int cbr = 0;
-        FOR_KEPT({
-          u64 kk;
-          float xs;
-          if (keep_xs(x, e, kk, xs)) {
-            ++cbr;
-            u64 fx;
-            const double pr = mass(xs, &fx);
-            const int fo = fine_of(xs);
-            fid[e - lo] = (uint16_t)fo;
-            const int c = fo >> 8;
-            atomicAdd(&s.hc[c], 1u);
-            atomicAdd(&s.hfix[c], fx);
-            unsafeAtomicAdd(&s.hf64[c], pr);
-            if (few) {
-              const int p = atomicAdd(&s.misc[15], 1);
-              if (p < FID_OFF) s.keys[p] = kk;
+        // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it
+        auto pass1 = [&](auto with_f64) -> int {
+          int cnt = 0;
+          FOR_KEPT({
+            u64 kk;
+            float xs;
+            if (keep_xs(x, e, kk, xs)) {
+              ++cnt;
+              u64 fx;
+              const double pr = mass(xs, &fx);
+              const int fo = fine_of(xs);
+              fid[e - lo] = (uint16_t)fo;
+              const int c = fo >> 8;
+              atomicAdd(&s.hc[c], 1u);
+              atomicAdd(&s.hfix[c], fx);
+              if constexpr (decltype(with_f64)::value) unsafeAtomicAdd(&s.hf64[c], pr);
+              if (few) {
+                const int p = atomicAdd(&s.misc[15], 1);
+                if (p < FID_OFF) s.keys[p] = kk;
+              }
             }
-          }
-        })
+          })
+          return cnt;
+        };
+        const int cbr = zfix_only ? pass1(std::false_type{}) : pass1(std::true_type{});
         int cb;
         if (few) {
           __syncthreads();
@@ -1736,7 +1748,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (t < NBIN && s.hc[t]) {
           atomicAdd(&h1->cnt[t], s.hc[t]);
           atomicAdd(&h1->fix[t], s.hfix[t]);
-          unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
+          if (!zfix_only) unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
         }
         ++nbar;
         ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
@@ -1787,7 +1799,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             if (t < NBIN) {
               s.hc[t] = ld_relaxed(&h1->cnt[t]);
               s.hfix[t] = ld_relaxed64(&h1->fix[t]);
-              s.hf64[t] = ld_relaxed_f64(&h1->f64[t]);
+              s.hf64[t] = zfix_only ? 0.0 : ld_relaxed_f64(&h1->f64[t]);
             }
             __syncthreads();
             // prefix sums of the coarse histogram (kept in the key area for every later lookup of this row)
@@ -1800,7 +1812,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               return hist_find(s.hc, s.hfix, s.hf64, cpc, cpw, cpf, target);
             };
             const u64 Sfix = cpw[0];
-            const double Sf = cpf[0] + s.hf64[0];
+            const double Sf = zfix_only ? (double)Sfix * inv_scale : cpf[0] + s.hf64[0];
             VS_TRX(44);
             const bool has_tp = P.top_p < 1.0;
             const double tgt_p = P.top_p * (double)Sfix;
@@ -1850,7 +1862,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                         const int b2 = j * NBIN + (int)(id & 0xFF);
                         atomicAdd(&s.fc[b2], 1u);
                         atomicAdd(&s.ffix[b2], fx);
-                        unsafeAtomicAdd(&s.ff64[b2], pr);
+                        if (!zfix_only) unsafeAtomicAdd(&s.ff64[b2], pr);
                       })
               __syncthreads();
               VS_TR(A, 15);
@@ -1862,7 +1874,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   const int b2 = i % NBIN;
                   atomicAdd(&hs->cnt[b2], s.fc[i]);
                   atomicAdd(&hs->fix[b2], s.ffix[i]);
-                  unsafeAtomicAdd(&hs->f64[b2], s.ff64[i]);
+                  if (!zfix_only) unsafeAtomicAdd(&hs->f64[b2], s.ff64[i]);
                 }
               }
               VS_TR(A, 16);
@@ -1875,7 +1887,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   const int b2 = i % NBIN;
                   s.fc[i] = ld_relaxed(&hs->cnt[b2]);
                   s.ffix[i] = ld_relaxed64(&hs->fix[b2]);
-                  s.ff64[i] = ld_relaxed_f64(&hs->f64[b2]);
+                  s.ff64[i] = zfix_only ? 0.0 : ld_relaxed_f64(&hs->f64[b2]);
                 }
                 __syncthreads();
                 // prefix sums of each fine set, one wave per set
@@ -2004,7 +2016,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                         const WPick pp = wpick(lp_.id, tgt_p - (double)lp_.fix_before);
                         keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
                         zfix = lp_.fix_before + pp.fix_in + pp.fix;
-                        zf = lp_.f64_before + pp.f64_in + pp.f64;
+                        zf = zfix_only ? (double)zfix * inv_scale : lp_.f64_before + pp.f64_in + pp.f64;
                         const double tol = 1e-6 * (double)Sfix;
                         if (fabs((double)(zfix - pp.fix) - tgt_p) < tol || fabs((double)zfix - tgt_p) < tol)
                           flags |= VS_OUT_TOPP_BOUNDARY;
@@ -2138,7 +2150,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     const Pick pp = pick(lp_.id, tgt_p - (double)lp_.fix_before);
                     keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
                     zfix = lp_.fix_before + pp.fix_in + pp.fix;
-                    zf = lp_.f64_before + pp.f64_in + pp.f64;
+                    zf = zfix_only ? (double)zfix * inv_scale : lp_.f64_before + pp.f64_in + pp.f64;
                     const double tol = 1e-6 * (double)Sfix;
                     if (fabs((double)(zfix - pp.fix) - tgt_p) < tol || fabs((double)zfix - tgt_p) < tol)
                       flags |= VS_OUT_TOPP_BOUNDARY;
@@ -2435,6 +2447,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.kmax = kmax;
   a.spin_limit = g_spin_limit ? g_spin_limit : 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
+  a.zspan_max = (63 - bits) * 0.6931471805599453 - 13.815510557964274;  // ln(fix_scale) - ln(1e6)
   a.params = list_k > 0 ? nullptr : params;
   a.list_k = list_k;
   a.list_ids = list_ids;
