@@ -1047,8 +1047,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
     __syncthreads();
     VS_TR(A, 24);
-    auto penalise = [&](int i, uint32_t c) {
-      float y = s.xv[i];
+    auto penalised = [&](float y, uint32_t c) -> float {
       if (rep != 1.0f) {
         const float dv = y / rep, ml = y * rep;  // both, then a select: no divergent branch
         y = y > 0.0f ? dv : ml;
@@ -1056,30 +1055,36 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       const float cf = (float)c;
       const float fc = fpen * cf;
       const float sub = fc + ppen;
-      s.xv[i] = y - sub;
+      return y - sub;
     };
-    // Lane L of wave w owns positions w * R + 64 j + L of the counts. It marks its non-zero ones in a bit mask and
-    // visits only those: the loop runs as often as the busiest lane of the wave has distinct tokens, with no
-    // per-position branch (scalar branches and LDS writes dominate a per-position loop).
-    const int R = A.CH / SNW;  // a multiple of WAVE
-    const int w0 = (t / WAVE) * R;
-    const int L = lane_id();
-    constexpr int NJ = EPT_MAX * SNT / SNW / WAVE;  // the largest R / WAVE
+    // Thread t owns positions t + SNT j of the counts (strided, so that a dense run of distinct tokens, as a
+    // Zipf-like history puts at the low ids, spreads over every wave). It marks its non-zero ones in a bit mask and
+    // visits only those, two per loop trip with both reads issued first: the loop runs as often as the busiest
+    // lane of the wave has distinct tokens / 2, with no per-position branch.
+    constexpr int NJ = EPT_MAX * SNT / SNT;  // the largest CH / SNT (CH <= EPT_MAX * SNT)
     static_assert(NJ <= 32, "one mask bit per owned position");
-    // Reads are unconditional (a uniform guard would become a scalar branch per read); past R they land in the
-    // next wave's counts or the unused rest of the key area (7 R + NJ * 64 < 16384 words) and are masked out.
+    // Reads are unconditional (a uniform guard would become a scalar branch per read); past CH they land in the
+    // unused rest of the key area (NJ * SNT < 16384 words) and are masked out.
+    uint32_t cv[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) cv[jj] = s.cnt[jj * SNT + t];
+    __builtin_amdgcn_sched_barrier(0);  // all NJ reads in flight before the first test
     uint32_t mask = 0;
 #pragma unroll
-    for (int jj = 0; jj < NJ; ++jj) {
-      const uint32_t c = s.cnt[w0 + jj * WAVE + L];
-      mask |= (uint32_t)(c != 0 && jj * WAVE < R) << jj;
-    }
+    for (int jj = 0; jj < NJ; ++jj) mask |= (uint32_t)((cv[jj] != 0) & (jj * SNT < A.CH)) << jj;
     VS_TRX(34);
     while (mask) {
-      const int jj = __builtin_ctz(mask);
+      const int ja = __builtin_ctz(mask);
       mask &= mask - 1;
-      const int i = w0 + jj * WAVE + L;
-      penalise(i, s.cnt[i]);
+      const bool two = mask != 0;
+      const int jb = two ? __builtin_ctz(mask) : ja;
+      mask &= mask - 1;
+      const int ia = ja * SNT + t, ib = jb * SNT + t;
+      const float ya = s.xv[ia], yb = s.xv[ib];
+      const uint32_t ca = s.cnt[ia], cb = s.cnt[ib];
+      const float za = penalised(ya, ca), zb = penalised(yb, cb);
+      s.xv[ia] = za;
+      if (two) s.xv[ib] = zb;
     }
     VS_TRX(35);
     __syncthreads();
