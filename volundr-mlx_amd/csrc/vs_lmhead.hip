@@ -161,7 +161,6 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       o1[j] = (uint32_t)((int64_t)r1 * A.ldw * 2) + (uint32_t)((lo8 ? 4 + kg : kg) * 16);
     }
   };
-  const int ngroups = K / (2 * KS);
   const char* wbase;
   uint32_t wo0[NTW], wo1[NTW];
   round_offsets(0, wbase, wo0, wo1);

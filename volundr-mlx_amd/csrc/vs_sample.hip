@@ -709,7 +709,7 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
   if (got > 0) {
     for (int b = 31; b >= 0; --b) {
       const uint32_t c = wb | (1u << b);
-      if (__popcll(__ballot(tmax >= c)) >= got) wb = c;
+      if ((int)__popcll(__ballot(tmax >= c)) >= got) wb = c;
     }
   }
   VS_TRX(37);
@@ -1101,6 +1101,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   _Pragma("unroll 4") for (int i_ = t; i_ < hi - lo; i_ += SNT) { \
     const int e = lo + i_;                                        \
     const float x = s.xv[i_];                                     \
+    (void)e;                                                      \
     BODY                                                          \
   }
   // The chunk in LDS, four positions per lane at a time: the four reads are issued before any of them is used, so
@@ -1390,7 +1391,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #pragma unroll
           for (int b = 31; b >= 0; --b) {
             const uint32_t c = th | (1u << b);
-            th = __popcll(__ballot(hh >= c)) >= keff ? c : th;
+            th = (int)__popcll(__ballot(hh >= c)) >= keff ? c : th;
           }
           M = nzh >= keff ? (u64)th << 32 : (u64)0;
         } else {
@@ -1684,6 +1685,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           hm_ &= hm_ - 1;                                                          \
           const int i = 8 * w_ + h_;                                               \
           const uint32_t id = (wd_[h_ >> 1] >> (16 * (h_ & 1))) & 0xFFFFu;         \
+          (void)id;                                                                \
           BODY                                                                     \
         }                                                                          \
       }                                                                            \
