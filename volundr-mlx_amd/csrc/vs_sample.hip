@@ -26,7 +26,7 @@ namespace vs {
 constexpr int SNT = 512;         // threads per workgroup
 constexpr int SNW = SNT / WAVE;  // waves per workgroup
 constexpr int NRED = 16;         // entries of each LDS reduction/broadcast array (>= SNW and >= 6)
-static_assert(NRED >= SNW, "one reduction slot per wave");
+static_assert(NRED >= 2 * SNW, "one reduction slot per wave, and the TOPK wave heads at 8 ..");
 constexpr int EPT_MAX = 24;      // logits per lane in flight during the load
 constexpr int NBIN = 256;        // radix digit = 8 bits
 constexpr int MAX_ROUNDS = 32;   // histogram slots per row (8 count + 1 coarse + 4 fine + 1 + 7 + 7 radix rounds)
@@ -78,8 +78,9 @@ struct Part {  // one per workgroup, written with device-coherent stores
   float mf;
   uint32_t pad;
   double se;
+  u64 heads[8];  // TOPK lists of the unsorted format: eight of the list's largest keys (0 = none)
 };
-static_assert(sizeof(Part) == 32, "Part layout");
+static_assert(sizeof(Part) == 96, "Part layout");
 
 struct HistSlot {
   uint32_t cnt[NBIN];
@@ -1239,7 +1240,14 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     VS_TR(A, 11);
     const u64 am = lb.nlanes ? (u64)0 : chunk_amkey();
     int kc = 0, C = 0;
-    const int kr = pow2_ceil(k);  // list length read by the merge (<= kcap)
+    const int kr = pow2_ceil(k);  // sorted list length read by the merge (<= kcap)
+    // Two list formats. Sorted: the local top-kc, zero padded to kr. Unsorted (when 8 G >= k, so that the row's
+    // G * 8 heads can bound its k-th key): every candidate, zero padded to CP, and eight heads per workgroup (the
+    // largest candidate of each wave), which spares the local rank sort; a workgroup with more than CP candidates
+    // publishes its sorted top-kc instead (also a valid unsorted list, headed by its first eight keys).
+    const bool ufmt = 8 * G >= k;
+    const int CP = A.kcap < 4 * kr ? A.kcap : 4 * kr;  // a power of two
+    bool listed = false;  // the candidates were published as they are
     if (lb.nlanes > 0) {
       const uint32_t L = lb.L;
       const float Lf = L ? inv_ord32(L) : -__builtin_inff();  // x >= Lf  <=>  ord32(x) >= L for finite x
@@ -1258,6 +1266,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       const int totw = nqw * M;
       u64* segw = s.keys + wv * SEGW;
       int cw = 0;
+      u64 lmx = 0;  // this lane's largest candidate key
       for (int p0 = 0; p0 < totw; p0 += WAVE) {
         const int pp = p0 + Ln;
         int q = (int)((float)pp * invM);  // pp < 2^24: corrected to the exact quotient below
@@ -1270,11 +1279,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         const bool c = pp < totw && i < nel && x >= Lf && is_finite(x);
         const unsigned long long mc = __ballot(c);
         const int pos = cw + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mc, 0u));
-        if (c && pos < SEGW) segw[pos] = key64(x, (uint32_t)(lo + i));
+        const u64 kk = key64(x, (uint32_t)(lo + i));
+        if (c && pos < SEGW) segw[pos] = kk;
+        lmx = (c & (kk > lmx)) ? kk : lmx;
         cw += __popcll(mc);
       }
+      const u64 hwv = wave_max(lmx);  // the wave's head (0: no candidate)
       int* segc = s.misc + M_SEGC;  // [SNW] candidates per wave
-      if (Ln == 0) segc[wv] = cw;
+      if (Ln == 0) {
+        segc[wv] = cw;
+        s.red64[8 + wv] = hwv;
+      }
       __syncthreads();
       C = 0;
 #pragma unroll
@@ -1282,7 +1297,25 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       VS_TR(A, 12);
       VS_TRV(A, 19, C);
       kc = C < k ? C : k;
-      if (C <= RANK_MAX) {
+      if (ufmt && C <= CP) {
+        // the unsorted list: each wave stores its segment at its offset (C <= CP <= kcap <= SEGW: none dropped)
+        int off = 0;
+#pragma unroll
+        for (int v = 0; v < SNW; ++v) off += v < wv ? segc[v] : 0;
+        for (int j = Ln; j < cw; j += WAVE) st_dev(&cand[g * A.kcap + off + j], segw[j]);
+        if (t < SNW) {  // the wave heads in descending order (equal ones, i.e. zeros, by wave): all 8 written
+          const u64 hx = s.red64[8 + t];
+          int rk = 0;
+#pragma unroll
+          for (int v = 0; v < SNW; ++v) {
+            const u64 hy = s.red64[8 + v];
+            rk += ((hy > hx) | ((hy == hx) & (v < t))) ? 1 : 0;
+          }
+          st_dev(&parts[g].heads[rk], hx);
+        }
+        kc = C;
+        listed = true;
+      } else if (C <= RANK_MAX) {
         // the segments, made contiguous in the chunk area (no longer needed on this path), then ranked
         u64* ck = (u64*)s.xv;
         int off = 0;
@@ -1335,8 +1368,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
       VS_TR(A, 13);
     }
-    // the published list: the sorted local top-kc, zero padded to kr
-    for (int i = t; i < kr; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
+    if (listed) {
+      for (int i = C + t; i < CP; i += SNT) st_dev(&cand[g * A.kcap + i], (u64)0);
+    } else {  // the sorted local top-kc, zero padded to kr (sorted format) or CP (unsorted format)
+      const int plen = ufmt ? CP : kr;
+      for (int i = t; i < plen; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
+      if (ufmt && t < 8) st_dev(&parts[g].heads[t], t < kc ? s.tk[t] : (u64)0);
+    }
     // C counts every finite logit when there is no bound, and is >= k otherwise: the row's sum decides
     // min(k, finite count) exactly.
     put_part(am, (uint32_t)C, (uint32_t)kc, 0.0f, 0.0);
@@ -1355,34 +1393,71 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       // Every wave loads the heads and list summaries and derives M itself (ballots over the heads, one per lane),
       // so the survivors go straight from the registers to one LDS array: a single barrier before the rank. ----
       {
-        const int lkr = __builtin_ctz((unsigned)kr);
-        const int tot = G * kr;  // <= G * kcap <= KEYS_CAP
+        const int plen = ufmt ? CP : kr;  // list stride read here (a power of two)
+        const int lpl = __builtin_ctz((unsigned)plen);
+        const int tot = G * plen;  // <= G * kcap <= KEYS_CAP
         const int r = (k + G - 1) / G;
-        const int nh = G * r;
+        const int nh = G * r;  // heads: the first r keys (unsorted format: r <= 8 of its eight heads) of each list
         u64* sel = s.keys;  // survivors (<= tot)
         u64 r8[KEYS_CAP / SNT];  // all lists, loaded in one round trip
 #pragma unroll
         for (int u = 0; u < KEYS_CAP / SNT; ++u) {
           const int idx = t + u * SNT;
-          r8[u] = idx < tot ? ld_dev(&cand[(idx >> lkr) * A.kcap + (idx & (kr - 1))]) : (u64)0;
+          r8[u] = idx < tot ? ld_dev(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
         }
         const int ln = lane_id();
         int nf2 = 0, full = 0;
         u64 k2 = 0, h2 = ~(u64)0, hd = 0;
+        u64 hv[8];  // unsorted format: lane ln holds heads ln + 64 u (workgroup h / r, place h % r)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int hx = ln + WAVE * u;
+          hv[u] = (ufmt && hx < nh) ? ld_dev(&parts[hx / r].heads[hx % r]) : (u64)0;
+        }
         if (ln < G) {
           nf2 = (int)ld_dev(&parts[ln].nfin);
           k2 = ld_dev(&parts[ln].amkey);
-          full = (int)ld_dev(&parts[ln].kc) >= r;
-          const u64 h = ld_dev(&cand[ln * A.kcap + r - 1]);
-          h2 = full ? h : h2;
+          if (!ufmt) {
+            full = (int)ld_dev(&parts[ln].kc) >= r;
+            const u64 h = ld_dev(&cand[ln * A.kcap + r - 1]);
+            h2 = full ? h : h2;
+          }
         }
-        if (nh <= WAVE && ln < nh) hd = ld_dev(&cand[(ln / r) * A.kcap + ln % r]);
+        if (!ufmt && nh <= WAVE && ln < nh) hd = ld_dev(&cand[(ln / r) * A.kcap + ln % r]);
         n = wave_sum(nf2);
         bam = wave_max(k2);
         keff = k < n ? k : n;  // sampler.py:133-134
         if (keff < 1) keff = 1;
         u64 M;
-        if (nh <= WAVE) {
+        if (ufmt) {
+          // th = the largest value with >= keff heads of value >= th (heads are keys of the row, so its keff-th
+          // key is >= th's lowest key); bisection with ballots over the heads' value bits, most significant first
+          const int hu = (nh + WAVE - 1) / WAVE;  // head slots in use per lane (uniform)
+          uint32_t hh[8];
+          int nzh = 0;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            hh[u] = (uint32_t)(hv[u] >> 32);
+            nzh += (int)__popcll(__ballot(hh[u] != 0));
+          }
+          uint32_t th = 0;
+          if (hu == 1) {
+#pragma unroll
+            for (int b = 31; b >= 0; --b) {
+              const uint32_t c = th | (1u << b);
+              th = (int)__popcll(__ballot(hh[0] >= c)) >= keff ? c : th;
+            }
+          } else {
+            for (int b = 31; b >= 0; --b) {
+              const uint32_t c = th | (1u << b);
+              int cnt = 0;
+#pragma unroll
+              for (int u = 0; u < 8; ++u) cnt += (int)__popcll(__ballot(hh[u] >= c));
+              th = cnt >= keff ? c : th;
+            }
+          }
+          M = nzh >= keff ? (u64)th << 32 : (u64)0;
+        } else if (nh <= WAVE) {
           // th = the largest value with >= keff heads of value >= th: a most-significant-bit-first bisection with
           // ballots on the heads' value bits (the key's upper word); M = th's lowest key
           const uint32_t hh = (uint32_t)(hd >> 32);
@@ -1399,18 +1474,19 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           const u64 mb = wave_min(h2);
           M = nfull * r >= keff ? mb : (u64)0;
         }
+        // a survivor is >= M and, in a sorted list, at a position below keff
         int cnt = 0;
 #pragma unroll
         for (int u = 0; u < KEYS_CAP / SNT; ++u) {
           const u64 x = r8[u];
-          cnt += ((x != 0) & (x >= M) & (((t + u * SNT) & (kr - 1)) < keff)) ? 1 : 0;
+          cnt += ((x != 0) & (x >= M) & (ufmt | (((t + u * SNT) & (kr - 1)) < keff))) ? 1 : 0;
         }
         int p = wave_alloc(cnt, &s.misc[9]);
         if (cnt) {
 #pragma unroll
           for (int u = 0; u < KEYS_CAP / SNT; ++u) {
             const u64 x = r8[u];
-            if ((x != 0) & (x >= M) & (((t + u * SNT) & (kr - 1)) < keff)) sel[p++] = x;
+            if ((x != 0) & (x >= M) & (ufmt | (((t + u * SNT) & (kr - 1)) < keff))) sel[p++] = x;
           }
         }
         __syncthreads();
