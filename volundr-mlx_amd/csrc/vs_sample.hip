@@ -1383,15 +1383,16 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       VS_TR(A, 4);
       int n, keff;
       u64 bam;
-      // ---- merge (last workgroup of the row). Each list holds its workgroup's sorted local top-kc (zero padded to
-      // kr). A lower bound M of the row's keff-th key leaves few survivors >= M, which are ranked; the bound:
-      //  * nh = G * r <= 64 (r = ceil(k / G) heads per list): when >= keff heads are non-zero, M = the lowest key
-      //    of the keff-th largest head value (>= keff heads, all keys of the row, are >= M, so its keff-th key is
-      //    >= M), else 0;
-      //  * otherwise: the smallest r-th key of the lists that hold >= r keys, valid when those lists number
-      //    >= keff / r (they alone hold >= keff keys >= it), else 0.
-      // Every wave loads the heads and list summaries and derives M itself (ballots over the heads, one per lane),
-      // so the survivors go straight from the registers to one LDS array: a single barrier before the rank. ----
+      // ---- merge (last workgroup of the row). Each list holds its workgroup's candidates (unsorted format) or
+      // sorted local top-kc, zero padded. A lower bound M of the row's keff-th key leaves few survivors >= M, which
+      // are ranked; the bound, with r = ceil(k / G) heads per list (a sorted list's first r keys, or the first r of
+      // an unsorted list's eight heads):
+      //  * r <= 8: when >= keff heads are non-zero, M = the lowest key of the keff-th largest head value (>= keff
+      //    heads, all keys of the row, are >= M, so its keff-th key is >= M), else 0;
+      //  * otherwise (sorted lists): the smallest r-th key of the lists that hold >= r keys, valid when those
+      //    lists number >= keff / r (they alone hold >= keff keys >= it), else 0.
+      // Every wave loads the heads and list summaries and derives M itself (ballots over the heads), so the
+      // survivors go straight from the registers to one LDS array: a single barrier before the rank. ----
       {
         const int plen = ufmt ? CP : kr;  // list stride read here (a power of two)
         const int lpl = __builtin_ctz((unsigned)plen);
@@ -1406,33 +1407,37 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           r8[u] = idx < tot ? ld_dev(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
         }
         const int ln = lane_id();
+        const bool hb8 = r <= 8;  // heads bound (else, sorted lists only, the smallest r-th key)
         int nf2 = 0, full = 0;
-        u64 k2 = 0, h2 = ~(u64)0, hd = 0;
-        u64 hv[8];  // unsorted format: lane ln holds heads ln + 64 u (workgroup h / r, place h % r)
+        u64 k2 = 0, h2 = ~(u64)0;
+        const int hu = hb8 ? (nh + WAVE - 1) / WAVE : 0;  // head slots in use per lane (uniform)
+        u64 hv[8];  // lane ln holds heads ln + 64 u (list h / r, place h % r)
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const int hx = ln + WAVE * u;
-          hv[u] = (ufmt && hx < nh) ? ld_dev(&parts[hx / r].heads[hx % r]) : (u64)0;
+          hv[u] = 0;
+          if (u < hu) {
+            const int hx = ln + WAVE * u;
+            const int hg = hx / r, hj = hx - hg * r;
+            if (hx < nh) hv[u] = ld_dev(ufmt ? &parts[hg].heads[hj] : &cand[hg * A.kcap + hj]);
+          }
         }
         if (ln < G) {
           nf2 = (int)ld_dev(&parts[ln].nfin);
           k2 = ld_dev(&parts[ln].amkey);
-          if (!ufmt) {
+          if (!hb8) {
             full = (int)ld_dev(&parts[ln].kc) >= r;
             const u64 h = ld_dev(&cand[ln * A.kcap + r - 1]);
             h2 = full ? h : h2;
           }
         }
-        if (!ufmt && nh <= WAVE && ln < nh) hd = ld_dev(&cand[(ln / r) * A.kcap + ln % r]);
         n = wave_sum(nf2);
         bam = wave_max(k2);
         keff = k < n ? k : n;  // sampler.py:133-134
         if (keff < 1) keff = 1;
         u64 M;
-        if (ufmt) {
+        if (hb8) {
           // th = the largest value with >= keff heads of value >= th (heads are keys of the row, so its keff-th
           // key is >= th's lowest key); bisection with ballots over the heads' value bits, most significant first
-          const int hu = (nh + WAVE - 1) / WAVE;  // head slots in use per lane (uniform)
           uint32_t hh[8];
           int nzh = 0;
 #pragma unroll
@@ -1455,18 +1460,6 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               for (int u = 0; u < 8; ++u) cnt += (int)__popcll(__ballot(hh[u] >= c));
               th = cnt >= keff ? c : th;
             }
-          }
-          M = nzh >= keff ? (u64)th << 32 : (u64)0;
-        } else if (nh <= WAVE) {
-          // th = the largest value with >= keff heads of value >= th: a most-significant-bit-first bisection with
-          // ballots on the heads' value bits (the key's upper word); M = th's lowest key
-          const uint32_t hh = (uint32_t)(hd >> 32);
-          const int nzh = __popcll(__ballot(hh != 0));
-          uint32_t th = 0;
-#pragma unroll
-          for (int b = 31; b >= 0; --b) {
-            const uint32_t c = th | (1u << b);
-            th = (int)__popcll(__ballot(hh >= c)) >= keff ? c : th;
           }
           M = nzh >= keff ? (u64)th << 32 : (u64)0;
         } else {
