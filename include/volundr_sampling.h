@@ -39,8 +39,14 @@ enum { VS_F32 = 0, VS_BF16 = 1, VS_F16 = 2 };
 
 /* vs_row_params.flags */
 enum {
-  VS_ROW_GREEDY = 1u /* Sampling.greedy (session.py:466-467): top_k == 1 or temperature < 1e-6 -> np.argmax of the
-                        processed row over the full vocabulary, first maximum (sampler.py:127-128) */
+  VS_ROW_GREEDY = 1u, /* Sampling.greedy (session.py:466-467): top_k == 1 or temperature < 1e-6 -> np.argmax of the
+                         processed row over the full vocabulary, first maximum (sampler.py:127-128) */
+  VS_ROW_ARGMAX_VV = 2u /* with VS_ROW_GREEDY: a request that needs no logits (Sampling.needs_logits is False,
+                           session.py:469-474) takes the first-max argmax over [0, vocab_valid) with no edits
+                           (sampler.py:96, mx.argmax(logits[:vv])). The host sets it only for rows with no bias,
+                           neutral penalties and no suppressed id below vocab_valid; the one condition that can change
+                           per step, an active stop mask (produced < min_new_tokens with stop ids), is decided by the
+                           kernel: a row whose stop range applies takes the ordinary greedy path over the full row */
 };
 
 /* out_flags bits */
@@ -57,7 +63,7 @@ enum {
 };
 
 /* Per-row sampling parameters (the fields of session.py:439-456 that Sampler.sample reads, sampler.py:100-156).
- * 88 bytes, 8-byte aligned. Index ranges are [begin, end) into the shared arrays of vs_sample_batch.
+ * 96 bytes, 8-byte aligned. Index ranges are [begin, end) into the shared arrays of vs_sample_batch.
  * top_p and min_p stay float64 because the reference compares them with float64 sums (sampler.py:146,150). */
 typedef struct vs_row_params {
   float temperature;        /* sampler.py:129 t = float32(temperature) */
@@ -75,6 +81,8 @@ typedef struct vs_row_params {
   int32_t supp_begin, supp_end; /* suppressed ids, sorted: -inf before the penalties (sampler.py:110-112) */
   int32_t stop_begin, stop_end; /* stop ids masked while produced < min_new_tokens, sorted: -inf after the
                                    penalties (sampler.py:123-126); the host passes an empty range otherwise */
+  int32_t vocab_valid;          /* Sampler.vv (sampler.py:59), read only by VS_ROW_ARGMAX_VV rows; 1 <= vv */
+  uint32_t reserved;            /* zero */
 } vs_row_params;
 
 /* Sampler.sample for B rows of logits (row r starts at element r*ld; ld >= V).
@@ -192,7 +200,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 5. */
+/* Library ABI version (increments on any signature or struct change): 6. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -184,3 +184,67 @@ def sample_batch(X, params, u, hists=None, produced=None):
         c = counts_from_history(hists[i]) if hists is not None else {}
         out.append(sample(X[i], params[i], float(u[i]), c, 0 if produced is None else produced[i]))
     return out
+
+
+# ---------------------------------------------------------------- Sampler.choose (sampler.py:83-98)
+def budget_action(prompt, generated, n, soft, start, end):
+    """The reasoning budget's action before output token p = len(generated) (volundr-mlx/sampler.py:18-55, driven
+    by Sampler.choose / accept, sampler.py:77-92), derived from the whole token record instead of a state machine:
+
+      * the span is open from the prompt when the last `start` among the prompt's final 16 tokens has no `end`
+        after it (sampler.py:25-31); its origin is output position 0, and j0 = -1;
+      * otherwise the first generated `start` (at j0) opens it with origin j0 + 1 (sampler.py:34-36);
+      * the span is forced shut at position pf = origin + n (sampler.py:47-50): the forced token is `end`;
+      * it closes by itself if an `end` is generated at some j with j0 < j < min(p, pf) (sampler.py:37-39).
+
+    Returns ("none", None), ("force", end) or ("bias", [(id, value)]) as Budget.act does."""
+    tail = list(prompt)[-16:]
+    j0, origin = None, None
+    if start in tail:
+        last = len(tail) - 1 - tail[::-1].index(start)
+        if end not in tail[last + 1:]:
+            j0, origin = -1, 0
+    if origin is None:
+        if start not in generated:
+            return ("none", None)
+        j0 = list(generated).index(start)
+        origin = j0 + 1
+    p = len(generated)
+    pf = origin + int(n)
+    if end in list(generated)[j0 + 1:min(p, pf)]:
+        return ("none", None)
+    if p > pf:
+        return ("bias", [(start, -np.inf)])
+    if p == pf:
+        return ("force", end)
+    if float(soft) != 0.0 and p - origin >= 0.8 * int(n):
+        return ("bias", [(end, float(soft))])
+    return ("none", None)
+
+
+def needs_logits(sp, vocab_valid: int, produced: int) -> bool:
+    """Sampling.needs_logits (volundr-mlx/session.py:469-474)."""
+    return (not sp.greedy or bool(sp.logit_bias) or sp.repetition_penalty != 1.0
+            or sp.frequency_penalty != 0.0 or sp.presence_penalty != 0.0
+            or (produced < sp.min_new_tokens and bool(sp.stop_token_ids))
+            or any(t < vocab_valid for t in sp.suppress_tokens))
+
+
+def choose(x, sp, vocab_valid: int, u: float, generated, prompt=(), think_ids=(None, None)) -> Result:
+    """Sampler.choose (sampler.py:83-98) for one row x (the full logits row, float32) given the tokens the request
+    has produced so far (`generated`, forced tokens included). `u` is the draw the row would consume. Returns the
+    Result with kind "force" (budget, no draw), "argmax" (mx.argmax(x[:vv]), first maximum, no draw; logprob =
+    x[j] - logsumexp(x[:vv])) or what `sample` returns."""
+    extra = []
+    if sp.reasoning_budget and think_ids[0] is not None and think_ids[1] is not None:      # :85-92
+        kind, v = budget_action(prompt, generated, sp.reasoning_budget, sp.reasoning_budget_soft_bias, *think_ids)
+        if kind == "force":
+            return Result(int(v), 0.0, kind="force")
+        if kind == "bias":
+            extra = v
+    produced = len(generated)
+    if extra or needs_logits(sp, vocab_valid, produced):                                   # :93-94
+        return sample(x, sp, u, counts_from_history(generated), produced, extra)
+    xv = np.asarray(x, dtype=np.float32)[:vocab_valid]                                     # :95-96
+    j = int(np.argmax(xv))
+    return Result(j, _logsoftmax_at(xv, j), kind="argmax")

@@ -1,0 +1,135 @@
+"""GPU parity of the drop-in routes the scheduler takes (volundr-mlx/sampler.py:83-98, called per row by
+scheduler.py:416-425): Sampler.choose, the batched sample_rows_for and the device-resident DeviceSamplers, against
+the oracle driven as Sampler.choose drives Sampler.sample (oracle.sampler_ref.choose). Covers every branch of
+choose: the reasoning budget's force and bias, argmax-only requests (mx.argmax over [:vocab_valid]), greedy
+requests that need the sampler (argmax over the full row), stop masks that move a request between the two, and
+sampled rows. The production vocabulary is used: V = 248320 logits of which vocab_valid = 248077 are real, with the
+row maximum planted in the padding columns."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_ref as S
+from parity import LP_ATOL, LP_RTOL
+from volundr_amd import DeviceSamplers, Sampler
+from volundr_amd.sampler import sample_rows_for
+from volundr_amd.session import Sampling
+
+pytestmark = pytest.mark.gpu
+
+V, VV = 248320, 248077
+THINK, UNTHINK = 1000, 1001
+PAD_HOT = V - 5          # a padding column that holds the row maximum
+
+
+class OracleRequest:
+    """Sampler state for the oracle: rng, the produced tokens (forced ones included), the prompt."""
+
+    def __init__(self, sp, prompt=(), think=(None, None)):
+        self.sp, self.prompt, self.think = sp, list(prompt), think
+        self.rng = S.seed_state(sp.seed)
+        self.gen = []
+
+    def step(self, x):
+        nxt, u = S.xorshift64s_next(self.rng)
+        r = S.choose(x, self.sp, VV, u, self.gen, self.prompt, self.think)
+        return r, nxt
+
+    def accept(self, tok, r, nxt):
+        if r.kind == "sample":
+            self.rng = nxt
+        self.gen.append(int(tok))
+
+
+def _requests():
+    """(Sampling, prompt, think_ids) per request: every branch of Sampler.choose."""
+    return [
+        (Sampling(temperature=0.0, seed=1), (), (None, None)),                                  # argmax-only
+        (Sampling(top_k=1, min_new_tokens=2, stop_token_ids=[PAD_HOT], seed=2), (), (None, None)),  # stop, then argmax
+        (Sampling(temperature=0.0, repetition_penalty=1.2, seed=3), (), (None, None)),          # greedy, full row
+        (Sampling(top_k=20, temperature=0.8, seed=4), (), (None, None)),                        # sampled top-k
+        (Sampling(top_p=0.9, temperature=1.1, presence_penalty=0.4, frequency_penalty=0.1, seed=5), (), (None, None)),
+        (Sampling(temperature=0.0, suppress_tokens=[VV + 2], seed=6), (), (None, None)),        # suppress >= vv
+        (Sampling(temperature=0.0, reasoning_budget=3, seed=7), (5, THINK), (THINK, UNTHINK)),   # budget force
+        (Sampling(top_k=50, reasoning_budget=5, reasoning_budget_soft_bias=30.0, seed=8), (THINK,), (THINK, UNTHINK)),
+    ]
+
+
+def _logits(rng, B):
+    x = np.clip(rng.standard_normal((B, V)) * 2.0, -10.0, 10.0).astype(np.float32)
+    x[:, PAD_HOT] = 14.0           # the largest logit sits in the padding: only [:vv] argmaxes must skip it
+    x[:, 7] = 11.5                 # the largest valid logit
+    return x
+
+
+def _check(label, tok, lp, r):
+    if r.kind == "sample" and (r.draw_boundary or r.topp_boundary) and tok != r.token:
+        return
+    assert tok == r.token, f"{label}: token {tok} != oracle {r.token} ({r.kind})"
+    if r.kind != "force" and lp is not None:
+        assert abs(lp - r.logprob) <= LP_RTOL * abs(r.logprob) + LP_ATOL, f"{label}: logprob {lp} vs {r.logprob}"
+
+
+def test_choose_and_sample_rows_for(dev):
+    rng = np.random.default_rng(2024)
+    reqs = _requests()
+    B = len(reqs)
+    per_row = [Sampler(sp, prompt=pr, think_ids=th, vocab_valid=VV) for sp, pr, th in reqs]
+    batched = [Sampler(sp, prompt=pr, think_ids=th, vocab_valid=VV) for sp, pr, th in reqs]
+    oracle = [OracleRequest(sp, pr, th) for sp, pr, th in reqs]
+    kinds = set()
+    for step in range(8):
+        x = _logits(rng, B)
+        xt = torch.from_numpy(x).to(dev)
+        print(f"[choose] step {step}", flush=True)
+        toks_b = sample_rows_for(xt, batched)
+        torch.cuda.synchronize()
+        for r in range(B):
+            tok_a = per_row[r].choose(xt[r])
+            res, nxt = oracle[r].step(x[r])
+            kinds.add(res.kind)
+            lab = f"step {step} row {r}"
+            _check("choose " + lab, tok_a, per_row[r].last_logprob if res.kind != "force" else None, res)
+            _check("sample_rows_for " + lab, toks_b[r], batched[r].last_logprob if res.kind != "force" else None, res)
+            oracle[r].accept(tok_a, res, nxt)
+            assert tok_b_follow(toks_b[r], tok_a, res)
+    assert kinds == {"argmax", "greedy", "sample", "force"}
+    for r in range(B):
+        for s in (per_row[r], batched[r]):
+            assert s.rng == oracle[r].rng, f"row {r}: rng"
+            assert s.produced == len(oracle[r].gen)
+    # the routes the planted padding maximum separates
+    assert oracle[0].gen == [7] * 8                        # argmax over [:vv]
+    assert oracle[1].gen[:2] == [7, 7] and oracle[1].gen[2:] == [7] * 6   # stop-masked, then [:vv]
+    assert oracle[2].gen[0] == PAD_HOT                     # the sampler's argmax sees the whole row
+    assert oracle[6].gen[3] == UNTHINK                     # forced after 3 thinking tokens
+
+
+def tok_b_follow(tok_b, tok_a, res):
+    """The two host routes agree except on an excused boundary row."""
+    return tok_b == tok_a or (res.kind == "sample" and (res.draw_boundary or res.topp_boundary))
+
+
+def test_device_samplers_vocab_valid(dev):
+    """DeviceSamplers keeps every request's state on the device and must reproduce Sampler.choose, including the
+    argmax over [:vocab_valid] for requests that need no logits and the switch when a stop mask expires."""
+    rng = np.random.default_rng(77)
+    reqs = [q for q in _requests() if q[0].reasoning_budget is None]
+    B = len(reqs)
+    samplers = [Sampler(sp, vocab_valid=VV) for sp, _, _ in reqs]
+    oracle = [OracleRequest(sp) for sp, _, _ in reqs]
+    ds = DeviceSamplers(samplers, V, hist_cap=32, device=dev)
+    for step in range(6):
+        x = _logits(rng, B)
+        print(f"[device vv] step {step}", flush=True)
+        out = ds.step(torch.from_numpy(x).to(dev))
+        ids = out.ids.cpu().numpy()
+        lps = out.logprobs.cpu().numpy().astype(np.float64)
+        for r in range(B):
+            res, nxt = oracle[r].step(x[r])
+            _check(f"state step {step} row {r}", int(ids[r]), float(lps[r]), res)
+            oracle[r].accept(ids[r], res, nxt)
+    st = ds.host_state()
+    for r in range(B):
+        assert int(st[r]["rng"]) == oracle[r].rng and ds.history(r) == oracle[r].gen
+    assert oracle[0].gen == [7] * 6 and oracle[2].gen[0] == PAD_HOT

@@ -25,7 +25,7 @@ def test_header_symbols_exported():
 
 def test_row_struct_size_matches_header():
     hdr = (ROOT / "include" / "volundr_sampling.h").read_text()
-    assert "88 bytes" in hdr and _lib.ROW_DTYPE.itemsize == 88
+    assert "96 bytes" in hdr and _lib.ROW_DTYPE.itemsize == 96
     assert "32 bytes" in hdr and _lib.STATE_DTYPE.itemsize == 32
     assert f"increments on any signature or struct change): {_lib.ABI_VERSION}." in hdr
 

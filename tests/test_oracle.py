@@ -139,7 +139,7 @@ def test_oracle_matches_brute_force(seed):
     counts = S.counts_from_history(rng.integers(0, V, size=int(rng.integers(0, 10))))
     for u in rng.random(5):
         r = S.sample(x, sp, float(u), counts)
-        if r.draw_boundary or r.topp_boundary or r.topk_tie:
+        if r.draw_boundary or r.topp_boundary:
             continue
         assert r.token == brute_sample(x, sp, float(u), counts)
 
@@ -208,3 +208,141 @@ def test_bf16_bits_roundtrip():
     b = synth.f32_to_bf16_bits(x)
     assert np.allclose(synth.bf16_bits_to_f32(b), x, rtol=2**-8)
     assert VR.to_f32(b).tolist() == synth.bf16_bits_to_f32(b).tolist()
+
+
+# ---------------------------------------------------------------- build-defined outputs the GPU tests rely on
+def test_logsoftmax_greedy_closed_form():
+    # greedy row: logprob = x[j] - log(sum exp(x)) over the finite entries
+    x = np.array([1.0, 0.0, -1.0], np.float32)
+    r = S.sample(x, P(top_k=1), 0.5)
+    assert r.kind == "greedy" and r.token == 0
+    assert abs(r.logprob - (1.0 - math.log(math.e + 1.0 + 1.0 / math.e))) < 1e-12
+    # -inf entries carry no mass; a NaN-free row with infinities keeps the finite normaliser
+    x = np.array([-np.inf, 2.0, -np.inf, 2.0, 0.0], np.float32)
+    r = S.sample(x, P(temperature=0.0), 0.5)
+    assert r.token == 1 and abs(r.logprob - (2.0 - math.log(2 * math.exp(2.0) + 1.0))) < 1e-12
+    # a non-finite choice has logprob 0 (no finite logit at all, or +inf winning)
+    assert S.sample(np.full(4, -np.inf, np.float32), P(), 0.5).logprob == 0.0
+    assert S.sample(np.array([0.0, np.inf], np.float32), P(top_k=1), 0.5).logprob == 0.0
+
+
+def _three_way():
+    x = np.log(np.array([0.5, 0.3, 0.2])).astype(np.float32)
+    xs = x - x[0]
+    pr = np.exp(xs.astype(np.float64))
+    return x, np.cumsum(pr / pr.sum())
+
+
+@pytest.mark.parametrize("d,flag", [(1e-7, True), (-1e-7, True), (1e-5, False), (-1e-5, False)])
+def test_draw_boundary_predicate(d, flag):
+    # the draw u*z (z = 1 without top-p) placed next to the first CDF step cs[0]
+    x, cs = _three_way()
+    r = S.sample(x, P(), float(cs[0] + d))
+    assert r.draw_boundary == flag
+    assert r.token == (0 if d < 0 else 1)          # first cumsum >= u*z
+    r = S.sample(x, P(), float(cs[1] + d))         # the second step
+    assert r.draw_boundary == flag and r.token == (1 if d < 0 else 2)
+
+
+@pytest.mark.parametrize("d,flag", [(1e-7, True), (-1e-7, True), (1e-5, False), (-1e-5, False)])
+def test_topp_boundary_predicate(d, flag):
+    x, cs = _three_way()
+    r = S.sample(x, P(top_p=float(cs[1] + d)), 0.1)
+    assert r.topp_boundary == flag
+    assert r.keep == (2 if d < 0 else 3)           # first cumsum >= top_p, plus one
+    assert not r.draw_boundary and r.token == 0
+
+
+# ---------------------------------------------------------------- Sampler.choose and the reasoning budget
+def _budget_replay(prompt, gen, n, soft, start, end):
+    """Actions of the product Budget (a state machine) when driven as Sampler.choose drives it."""
+    from volundr_amd.sampler import Budget
+
+    b = Budget(n, soft, prompt, start, end)
+    acts = []
+    for j, tok in enumerate(gen):
+        acts.append(b.act(j))
+        if acts[-1][0] == "force":
+            tok = end
+        b.accept(j, tok)
+    acts.append(b.act(len(gen)))
+    return acts
+
+
+def test_budget_hand_cases():
+    S_, E_ = 7, 8
+    # open in the prompt tail, n = 4: forced at output 4, then <think> masked for good
+    acts = [S.budget_action([1, 2, S_], [0] * p, 4, 0.0, S_, E_) for p in range(4)]
+    assert [a[0] for a in acts] == ["none"] * 4
+    assert S.budget_action([1, 2, S_], [0, 0, 0, 0], 4, 0.0, S_, E_) == ("force", E_)
+    assert S.budget_action([1, 2, S_], [0, 0, 0, 0, E_], 4, 0.0, S_, E_) == ("bias", [(S_, -np.inf)])
+    # closed inside the prompt tail: idle until a generated <think>; soft bias from 80% of n on
+    assert S.budget_action([S_, E_], [0] * 20, 10, 1.5, S_, E_) == ("none", None)
+    # origin 1 (the token after the generated <think>): k zeros after it are k tokens spent
+    assert S.budget_action([S_, E_], [S_] + [0] * 7, 10, 1.5, S_, E_) == ("none", None)         # 7 < 8
+    assert S.budget_action([S_, E_], [S_] + [0] * 8, 10, 1.5, S_, E_) == ("bias", [(E_, 1.5)])  # 8 >= 0.8 * 10
+
+    # closed by the model before the budget: nothing more, ever
+    assert S.budget_action([S_], [0, E_, 0, 0, 0, 0, 0], 4, 1.0, S_, E_) == ("none", None)
+    # a <think> older than 16 prompt tokens does not count
+    assert S.budget_action([S_] + [0] * 16, [0] * 30, 4, 0.0, S_, E_) == ("none", None)
+
+
+def test_budget_spot_values_of_the_state_machine():
+    from volundr_amd.sampler import Budget
+
+    b = Budget(10, 1.5, [7, 8], 7, 8)
+    assert b.open is None and not b.closed and b.act(20) == ("none", None)
+    b.accept(0, 7)
+    assert b.open == 1 and b.act(5) == ("none", None) and b.act(9) == ("bias", [(8, 1.5)])
+    assert b.act(11) == ("force", 8) and b.forced and b.closed and b.open is None
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_budget_state_machine_matches_record_derivation(seed):
+    """The product's state-machine Budget and the oracle's whole-record derivation agree on every step of random
+    token streams rich in <think>/<\\think> tokens."""
+    rng = np.random.default_rng(seed)
+    S_, E_ = 7, 8
+    prompt = list(rng.choice([0, 1, S_, E_], size=int(rng.integers(0, 24)), p=[0.5, 0.2, 0.2, 0.1]))
+    n = int(rng.integers(1, 12))
+    soft = float(rng.choice([0.0, 2.0]))
+    gen = []
+    acts = []
+    from volundr_amd.sampler import Budget
+
+    b = Budget(n, soft, prompt, S_, E_)
+    for j in range(40):
+        a = b.act(j)
+        want = S.budget_action(prompt, gen, n, soft, S_, E_)
+        assert a == want, f"step {j}: {a} vs {want}"
+        tok = E_ if a[0] == "force" else int(rng.choice([0, 1, S_, E_], p=[0.6, 0.2, 0.1, 0.1]))
+        b.accept(j, tok)
+        gen.append(tok)
+        acts.append(a)
+
+
+def test_choose_routes():
+    V, vv = 12, 10
+    x = np.zeros(V, np.float32)
+    x[11] = 9.0                      # a padding column holds the row maximum
+    x[3] = 2.0
+    # needs no logits: argmax over [:vv] with its logprob over [:vv]
+    r = S.choose(x, P(temperature=0.0), vv, 0.5, [])
+    assert r.kind == "argmax" and r.token == 3
+    assert abs(r.logprob - (2.0 - math.log(math.exp(2.0) + 9))) < 1e-12
+    # greedy with a penalty needs the sampler: argmax over the full row (sampler.py:127-128 has no vv slice)
+    r = S.choose(x, P(temperature=0.0, repetition_penalty=1.1), vv, 0.5, [])
+    assert r.kind == "greedy" and r.token == 11
+    # the stop mask makes an argmax-only request a sampler row while produced < min_new_tokens
+    sp = P(top_k=1, min_new_tokens=2, stop_token_ids=[11])
+    assert S.choose(x, sp, vv, 0.5, [0]).kind == "greedy" and S.choose(x, sp, vv, 0.5, [0]).token == 3
+    assert S.choose(x, sp, vv, 0.5, [0, 0]).kind == "argmax"
+    # budget force and bias
+    sp = P(reasoning_budget=10, reasoning_budget_soft_bias=50.0, temperature=0.0)
+    r = S.choose(x, sp, vv, 0.5, [5] + [0] * 10, prompt=[], think_ids=(5, 6))
+    assert r.kind == "force" and r.token == 6
+    r = S.choose(x, sp, vv, 0.5, [5] + [0] * 7, prompt=[], think_ids=(5, 6))    # 7 spent: no bias yet
+    assert r.kind == "argmax" and r.token == 3
+    r = S.choose(x, sp, vv, 0.5, [5] + [0] * 8, prompt=[], think_ids=(5, 6))    # 8 >= 0.8*10: +50 on <\think>
+    assert r.kind == "greedy" and r.token == 6

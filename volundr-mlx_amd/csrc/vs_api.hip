@@ -49,7 +49,7 @@ extern "C" {
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 5; }
+int vs_version(void) { return 6; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;

@@ -945,7 +945,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   if (A.params) {
     P = A.params[grow];
   } else {  // top-list mode: plain logits, top_k = list_k, no edits
-    P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0};
+    P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0u};
   }
   // state entry point: the draw, the history range and the stop mask come from the request's device state
   vs_row_state st = {0, 0, 0, 0, 0, 0};
@@ -966,8 +966,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   HistSlot* hslots = (HistSlot*)(rws + OFF_HIST);
 
   const int V = A.V;
+  // A request that needs no logits (sampler.py:96) reads only [0, vocab_valid) and takes no edits; with its stop
+  // mask active it is an ordinary greedy row over the whole vocabulary (sampler.py:123-128).
+  const bool argmax_vv = (P.flags & VS_ROW_ARGMAX_VV) && (P.flags & VS_ROW_GREEDY) && P.stop_end == P.stop_begin;
+  const int vlim = argmax_vv ? min(V, P.vocab_valid) : V;
+  if (argmax_vv) P.bias_end = P.bias_begin, P.supp_end = P.supp_begin, P.hist_end = P.hist_begin;
   const int lo = g * A.CH;
-  const int hi = min(V, lo + A.CH);
+  const int hi = min(vlim, lo + A.CH);
   const int NV = A.NV;
   VS_TR_DECL(A);
   VS_TR(A, 0);

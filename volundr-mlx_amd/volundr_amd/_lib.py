@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libvolundr_sampling.so"
 VS_OK, VS_EINVAL, VS_EWORKSPACE, VS_EHIP = 0, -1, -2, -3
 VS_F32, VS_BF16, VS_F16 = 0, 1, 2
 VS_ROW_GREEDY = 1
+VS_ROW_ARGMAX_VV = 2
 OUT_DRAW_BOUNDARY = 1 << 0
 OUT_TOPP_BOUNDARY = 1 << 1
 OUT_GREEDY = 1 << 3
@@ -24,22 +25,22 @@ OUT_GATHER = 1 << 6
 OUT_HIST_FULL = 1 << 7
 OUT_TIMEOUT = 1 << 31
 
-# vs_row_params, 88 bytes (layout fixed by the C header)
+# vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([
     ("temperature", "<f4"), ("repetition_penalty", "<f4"), ("frequency_penalty", "<f4"),
     ("presence_penalty", "<f4"), ("top_k", "<i4"), ("flags", "<u4"),
     ("top_p", "<f8"), ("min_p", "<f8"), ("u", "<f8"), ("hist_begin", "<i8"), ("hist_end", "<i8"),
     ("bias_begin", "<i4"), ("bias_end", "<i4"), ("supp_begin", "<i4"), ("supp_end", "<i4"),
-    ("stop_begin", "<i4"), ("stop_end", "<i4"),
+    ("stop_begin", "<i4"), ("stop_end", "<i4"), ("vocab_valid", "<i4"), ("reserved", "<u4"),
 ])
-assert ROW_DTYPE.itemsize == 88
+assert ROW_DTYPE.itemsize == 96
 
 # vs_row_state, 32 bytes: the per-request sampler state of vs_sample_batch_state
 STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4"), ("hist_cap", "<i4"),
                         ("produced", "<i4"), ("min_new_tokens", "<i4")])
 assert STATE_DTYPE.itemsize == 32
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version")

@@ -14,7 +14,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import ROW_DTYPE, VS_BF16, VS_F16, VS_F32, VS_ROW_GREEDY, check
+from ._lib import ROW_DTYPE, VS_BF16, VS_F16, VS_F32, VS_ROW_ARGMAX_VV, VS_ROW_GREEDY, check
 
 _DTYPES = {torch.float32: VS_F32, torch.bfloat16: VS_BF16, torch.float16: VS_F16}
 _ws_lock = threading.Lock()
@@ -91,8 +91,16 @@ class DeviceRows:
     B: int
 
 
+def argmax_only_ok(sp, vocab_valid: int) -> bool:
+    """True when Sampling.needs_logits(vocab_valid, produced) (session.py:469-474) is False for some produced count:
+    a greedy request with no bias, neutral penalties and no suppressed id below vocab_valid. Whether its stop mask
+    is active (produced < min_new_tokens) is the one per-step condition left; the kernel decides it."""
+    return (sp.greedy and not sp.logit_bias and sp.repetition_penalty == 1.0 and sp.frequency_penalty == 0.0
+            and sp.presence_penalty == 0.0 and not any(t < vocab_valid for t in sp.suppress_tokens))
+
+
 def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, extras=None,
-              stop_always: bool = False) -> PackedRows:
+              stop_always: bool = False, argmax_vv=None) -> PackedRows:
     """Pack the per-row parameters the way Sampler.sample reads them (volundr-mlx/sampler.py:100-156).
 
     samplings : Sampling-like objects (session.Sampling); u : B uniform draws in [0, 1)
@@ -101,6 +109,9 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
     extras    : per-row budget biases [(id, bias)] applied before logit_bias (sampler.py:104-106)
     stop_always : pack the stop ids of every row with min_new_tokens > 0 whatever `produced` is (the state entry
                   point applies them while its device-side produced < min_new_tokens)
+    argmax_vv : per-row vocab_valid or None: a row given one is a request that needs no logits while its stop mask
+                is off, and then takes mx.argmax(logits[:vv]) as Sampler.choose does (sampler.py:95-96); its
+                Sampling must pass argmax_only_ok and it must carry no extras
     """
     B = len(samplings)
     P = np.zeros(B, dtype=ROW_DTYPE)
@@ -120,6 +131,16 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
             k = 1                                # max(min(k, n), 1) == 1 for k < 0 (:134)
         p["top_k"] = min(int(k), 2**31 - 1)
         p["flags"] = VS_ROW_GREEDY if sp.greedy else 0
+        p["vocab_valid"] = V
+        vvr = None if argmax_vv is None else argmax_vv[r]
+        if vvr is not None:
+            vvr = int(vvr)
+            if vvr < 1:
+                raise ValueError("vocab_valid must be >= 1")
+            if not argmax_only_ok(sp, vvr) or (extras is not None and extras[r]):
+                raise ValueError(f"row {r} needs the sampler's logits: it cannot take the argmax-only route")
+            p["flags"] |= VS_ROW_ARGMAX_VV
+            p["vocab_valid"] = min(vvr, V)
         p["top_p"] = float(sp.top_p)
         p["min_p"] = float(sp.min_p)
         p["u"] = float(u[r])
@@ -197,10 +218,11 @@ def sample_rows(logits: torch.Tensor, rows: DeviceRows, out: Optional[SampleOut]
 
 
 def sample_batch(logits: torch.Tensor, samplings: Sequence, u, histories=None, produced=None,
-                 extras=None) -> SampleOut:
-    """Sampler.sample (sampler.py:100-156) for every row of logits [B, V], with the uniform draws supplied."""
+                 extras=None, argmax_vv=None) -> SampleOut:
+    """Sampler.sample (sampler.py:100-156) for every row of logits [B, V], with the uniform draws supplied (rows
+    given an argmax_vv take Sampler.choose's argmax over [:vv] instead, see pack_rows)."""
     _require_cuda(logits, "logits")
-    rows = pack_rows(samplings, u, logits.shape[-1], histories, produced, extras).to(logits.device)
+    rows = pack_rows(samplings, u, logits.shape[-1], histories, produced, extras, argmax_vv=argmax_vv).to(logits.device)
     return sample_rows(logits, rows)
 
 

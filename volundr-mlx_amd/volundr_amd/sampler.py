@@ -21,43 +21,62 @@ SAMPLING_EPS = 1e-6
 
 
 class Budget:
-    """Reasoning budget (volundr-mlx/sampler.py:18-55): count tokens since `<|think|>` opened (in the prompt's last
-    16 tokens, or generated); after n of them with no `<|/think|>`, force `<|/think|>` and mask `<|think|>` for the
-    rest of the request; with a soft bias b, add b to the `<|/think|>` logit from 80% of the budget on."""
+    """Reasoning budget of a request (behaviour of volundr-mlx/sampler.py:18-55), written as a four-state machine.
+
+    States and what `act(produced)` answers before output token `produced` is chosen:
+      IDLE    no think span is open                                      -> ("none", None)
+      OPEN    a span opened at output position `origin`; with d = produced - origin:
+                d >= n           -> becomes FORCED                       -> ("force", end)
+                soft != 0 and d >= 0.8 n                                 -> ("bias", [(end, soft)])
+                otherwise                                                -> ("none", None)
+      CLOSED  the model closed the span itself                           -> ("none", None)
+      FORCED  the budget closed it                                       -> ("bias", [(start, -inf)]) for good
+    Transitions on `accept(j, tok)` (tok is output token j): `start` in IDLE opens the span at origin j + 1; `end` in
+    OPEN closes it (CLOSED). CLOSED and FORCED never reopen. The start of a request: if the last `start` among the
+    prompt's final 16 tokens is not followed there by `end`, the span is already OPEN with origin 0.
+    """
+
+    IDLE, OPEN, CLOSED, FORCED = range(4)
 
     def __init__(self, n, soft, prompt, start, end):
         self.start, self.end, self.n, self.soft = start, end, int(n), float(soft)
-        tail = list(prompt[-16:])
-        self.open = None
-        # the last `start` in the tail opens the budget unless an `end` follows it
-        for i in reversed(range(len(tail))):
-            if tail[i] == start:
-                if end not in tail[i + 1:]:
-                    self.open = 0
-                break
-        self.closed = False
-        self.forced = False
+        self.state, self.origin = Budget.IDLE, 0
+        window = list(prompt)[-16:]
+        opens = [i for i, tok in enumerate(window) if tok == start]
+        if opens and end not in window[opens[-1] + 1:]:
+            self.state = Budget.OPEN
+
+    # the reference's field names, read by callers that inspect the budget
+    @property
+    def open(self):
+        return self.origin if self.state == Budget.OPEN else None
+
+    @property
+    def closed(self):
+        return self.state in (Budget.CLOSED, Budget.FORCED)
+
+    @property
+    def forced(self):
+        return self.state == Budget.FORCED
 
     def accept(self, j, t):
-        if t == self.start:
-            if self.open is None and not self.closed:
-                self.open = j + 1
-        elif t == self.end and self.open is not None:
-            self.open = None
-            self.closed = True
+        if t == self.start:  # a start token is never also read as an end token
+            if self.state == Budget.IDLE:
+                self.state, self.origin = Budget.OPEN, j + 1
+        elif t == self.end and self.state == Budget.OPEN:
+            self.state = Budget.CLOSED
 
     def act(self, produced):
         """-> ("none" | "force" | "bias", payload) before sampling output token `produced`."""
-        if self.closed:
-            return ("bias", [(self.start, -np.inf)]) if self.forced else ("none", None)
-        if self.open is None:
+        if self.state == Budget.FORCED:
+            return ("bias", [(self.start, -np.inf)])
+        if self.state != Budget.OPEN:
             return ("none", None)
-        k = produced - self.open
-        if k >= self.n:
-            self.forced = self.closed = True
-            self.open = None
+        spent = produced - self.origin
+        if spent >= self.n:
+            self.state = Budget.FORCED
             return ("force", self.end)
-        if self.soft != 0.0 and k >= 0.8 * self.n:
+        if self.soft != 0.0 and spent >= 0.8 * self.n:
             return ("bias", [(self.end, self.soft)])
         return ("none", None)
 
@@ -139,10 +158,11 @@ class Sampler:
 def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Optional[Sequence[int]] = None):
     """One batched device call for the rows of logits [B, V] that the per-row loop of scheduler.py:416-425 would
     hand to Sampler.choose: returns the chosen token per sampler, updating each sampler's state exactly as
-    `choose` does (the draw is consumed only by rows that sample)."""
+    `choose` does (budget force and bias, sampler.py:85-92; the draw is consumed only by rows that sample; rows that
+    need no logits take the argmax over [:vocab_valid], sampler.py:95-96)."""
     rows = list(range(len(samplers))) if rows is None else list(rows)
     toks: list = [None] * len(samplers)
-    todo, sps, us, hists, prods, extras, rng0 = [], [], [], [], [], [], []
+    todo, sps, us, hists, prods, extras, rng0, avv = [], [], [], [], [], [], [], []
     for i, s in enumerate(samplers):
         forced, extra = s._extra()
         if forced is not None:
@@ -151,24 +171,17 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
             continue
         todo.append(i)
         sp = s.sp
-        if not (extra or sp.needs_logits(s.vv, s.produced)):
-            # the GPU argmax over the valid vocabulary: a greedy row with no edits, same as the verify argmax
-            sp = _ArgmaxOnly(sp)
+        argmax_only = not (extra or sp.needs_logits(s.vv, s.produced))
         sps.append(sp)
         rng0.append(s.rng)
         us.append(s.uniform() if not sp.greedy else 0.0)
-        hists.append(s.history if not isinstance(sp, _ArgmaxOnly) else [])
+        hists.append([] if argmax_only else s.history)
         prods.append(s.produced)
         extras.append(list(extra))
+        avv.append(s.vv if argmax_only else None)
     if todo:
         sub = logits[[rows[i] for i in todo]]
-        # argmax-only rows must not see columns >= vocab_valid (sampler.py:96 slices [:vv]); mask them to -inf
-        need_vv = [k for k, sp in enumerate(sps) if isinstance(sp, _ArgmaxOnly) and samplers[todo[k]].vv < sub.shape[1]]
-        if need_vv:
-            sub = sub.clone()
-            for k in need_vv:
-                sub[k, samplers[todo[k]].vv:] = float("-inf")
-        out = ops.sample_batch(sub, sps, us, hists, prods, extras)
+        out = ops.sample_batch(sub, sps, us, hists, prods, extras, argmax_vv=avv)
         ids = out.ids.cpu().tolist()
         lps = out.logprobs.cpu().tolist()
         fl = out.flags.cpu().tolist()
@@ -182,16 +195,3 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
             samplers[i].accept(ids[k])
             toks[i] = ids[k]
     return toks
-
-
-class _ArgmaxOnly:
-    """A greedy view of a Sampling with no edits: the row takes np.argmax, first maximum."""
-
-    def __init__(self, sp):
-        self._sp = sp
-        self.temperature, self.top_p, self.top_k, self.min_p = 1.0, 1.0, 1, 0.0
-        self.presence_penalty = self.frequency_penalty = 0.0
-        self.repetition_penalty = 1.0
-        self.min_new_tokens = 0
-        self.logit_bias, self.suppress_tokens, self.stop_token_ids = [], [], []
-        self.greedy = True

@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 from ._lib import STATE_DTYPE, check
-from .ops import _DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, pack_rows, workspace
+from .ops import _DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, pack_rows, workspace
 
 
 class DeviceSamplers:
@@ -53,7 +53,11 @@ class DeviceSamplers:
             pool[r * self.cap:r * self.cap + h.size] = h
         self.state = torch.from_numpy(st.view(np.uint8).copy()).to(dev)
         self.pool = torch.from_numpy(pool).to(dev)
-        self.rows = pack_rows([s.sp for s in self.samplers], np.zeros(self.B), self.V, stop_always=True).to(dev)
+        # requests that need no logits take Sampler.choose's argmax over [:vocab_valid] (sampler.py:95-96) whenever
+        # their stop mask is off; the kernel applies the mask while its own produced < min_new_tokens
+        avv = [s.vv if argmax_only_ok(s.sp, s.vv) else None for s in self.samplers]
+        self.rows = pack_rows([s.sp for s in self.samplers], np.zeros(self.B), self.V, stop_always=True,
+                              argmax_vv=avv).to(dev)
         self.out = alloc_out(self.B, dev)
         L = _lib.load()
         self._ws = workspace(dev, L.vs_sample_workspace_bytes(self.B, self.V))
