@@ -103,6 +103,21 @@ int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, con
 
 size_t vs_sample_workspace_bytes(int B, int V);
 
+/* vs_sample_batch without a workspace argument and without any allocation: the kernels use a fixed device array
+ * of vs_sample_noalloc_scratch_bytes() bytes (about 19.8 MB) in the library, one per device, kept until the process
+ * ends. It covers every batch size (batches above 64 rows run as consecutive launches that reuse it); a shape whose
+ * workspace would exceed it fails with VS_EWORKSPACE. The first call on a device looks the array up and zeroes it
+ * (a fill kernel on `stream`); every call leaves it zeroed. All calls on one device share the array: calls that
+ * overlap on one device (different streams, or threads without ordering) race and give wrong results.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). */
+int vs_sample_batch_noalloc(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
+                            const int32_t* hist, const int32_t* bias_ids, const float* bias_vals,
+                            const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
+                            int32_t* out_keep, vs_stream_t stream);
+
+size_t vs_sample_noalloc_scratch_bytes(void);
+
 /* Per-request sampler state kept on the device (Sampler, sampler.py:58-81). 32 bytes, 8-byte aligned. */
 typedef struct vs_row_state {
   uint64_t rng;           /* xorshift64* state (Sampler.rng); the host seeds it as Sampler.__init__ does */

@@ -19,6 +19,8 @@
 #include "vs_common.h"
 #include "vs_host.h"
 
+#include <mutex>
+
 #pragma clang fp contract(off)
 
 namespace vs {
@@ -2585,4 +2587,63 @@ extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V
   if (!state) return fail(VS_EINVAL, "vs_sample_batch_state: null state");
   return sample_launch(logits, dtype, B, V, ld, params, state, pool, nullptr, bias_ids, bias_vals, mask_ids, out_ids,
                        out_logprob, out_flags, out_keep, ws, ws_bytes, stream);
+}
+
+// =================================================================================================================
+// Allocation-free entry point: the workspace is a file-scope device array instead of a caller buffer
+// =================================================================================================================
+// One workspace of RPL_MAX rows covers every launch (larger batches run in launches of at most RPL_MAX rows that
+// reuse it), so the array has a fixed size of RPL_MAX * ROW_WS bytes (about 19.8 MB) per device, held until the
+// process ends. The kernels leave it zeroed after every call; it is zeroed once per device at its first use.
+namespace {
+constexpr size_t SCRATCH_BYTES = (size_t)RPL_MAX * ROW_WS;
+static_assert(SCRATCH_BYTES % 16 == 0, "the zero fill writes 16-byte words");
+static __device__ __align__(256) char scratch[SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];  // device address of `scratch` per device (the host symbol is only a stand-in)
+
+__global__ __launch_bounds__(256) void scratch_zero_kernel(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's address of `scratch`; on the first call for a device it is looked up and zeroed (a fill
+// kernel on `stream`, so the first call is stream-ordered like every later one).
+int scratch_ptr(void** out, hipStream_t stream) {
+  int d = 0;
+  hipError_t e = hipGetDevice(&d);
+  if (e != hipSuccess) return hip_fail(e, "vs_sample_batch_noalloc: hipGetDevice");
+  if (d < 0 || d >= 64) return fail(VS_EINVAL, "vs_sample_batch_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[d]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e, "vs_sample_batch_noalloc: hipGetSymbolAddress(scratch)");
+    hipLaunchKernelGGL(scratch_zero_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)p, SCRATCH_BYTES / 16);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "vs_sample_batch_noalloc: scratch zero fill");
+    g_scratch_ptr[d] = p;
+  }
+  *out = g_scratch_ptr[d];
+  return VS_OK;
+}
+}  // namespace
+
+extern "C" size_t vs_sample_noalloc_scratch_bytes(void) { return SCRATCH_BYTES; }
+
+extern "C" int vs_sample_batch_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
+                                       const vs_row_params* params, const int32_t* hist, const int32_t* bias_ids,
+                                       const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids,
+                                       float* out_logprob, uint32_t* out_flags, int32_t* out_keep,
+                                       vs_stream_t stream) {
+  if (B < 0) return fail(VS_EINVAL, "vs_sample_batch_noalloc: B < 0");
+  if (B == 0) return VS_OK;
+  if (vs_sample_workspace_bytes(B, V) > SCRATCH_BYTES)
+    return fail(VS_EWORKSPACE, "vs_sample_batch_noalloc: the call needs more than the fixed scratch array");
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws, (hipStream_t)stream);
+  if (rc != VS_OK) return rc;
+  return sample_launch(logits, dtype, B, V, ld, params, nullptr, nullptr, hist, bias_ids, bias_vals, mask_ids, out_ids,
+                       out_logprob, out_flags, out_keep, ws, SCRATCH_BYTES, stream);
 }

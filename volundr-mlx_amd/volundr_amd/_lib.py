@@ -43,7 +43,8 @@ assert STATE_DTYPE.itemsize == 32
 ABI_VERSION = 6
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
-           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version")
+           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
+           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes")
 
 _lib = None
 
@@ -63,6 +64,10 @@ def load():
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     L.vs_sample_batch.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     L.vs_sample_batch.restype = i32
+    L.vs_sample_batch_noalloc.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.vs_sample_batch_noalloc.restype = i32
+    L.vs_sample_noalloc_scratch_bytes.argtypes = []
+    L.vs_sample_noalloc_scratch_bytes.restype = sz
     L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     L.vs_sample_batch_state.restype = i32
     L.vs_lmhead_verify_greedy.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, sz,
