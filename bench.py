@@ -44,7 +44,7 @@ def algo_bytes_sample(d, B):
     """Logits read once + histories read once + per-row params + outputs (ids, logprob, flags, keep)."""
     x = d["logits"]
     h = 0 if d["hists"] is None else d["hists"].size * 4
-    return x.size * 4 + h + B * 88 + B * 16
+    return x.size * 4 + h + B * 96 + B * 16
 
 
 def algo_bytes_verify(d):
@@ -86,7 +86,7 @@ def bench_sample(torch, dev, d, steps, warmup, nslots):
     warm = time_calls(torch, call, 1, steps, warmup)
     flags = call.out.flags.cpu().numpy()
     assert not any((int(f) & 0xFFFFFFFF) >> 31 for f in flags), "timeout flag set"
-    return cold, warm, algo_bytes_sample(d, B)
+    return cold, warm, algo_bytes_sample(d, B), call.out
 
 
 def bench_state(torch, dev, d, steps, warmup, nslots):
@@ -182,6 +182,41 @@ def bench_lmhead(torch, dev, steps, warmup, B=1, T=17):
     return f, u, algo
 
 
+def launch_floor(torch, dev, steps):
+    """Microseconds per launch of an empty kernel issued back to back through the library's C ABI (the same way the
+    sampling kernel is launched), for a one-workgroup grid and for full-chip grids of 512-thread workgroups."""
+    from volundr_amd import _lib
+
+    L = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    for key, (blocks, threads, lds) in {"1x64": (1, 64, 0), "256x512": (256, 512, 0),
+                                         "256x512_lds96k": (256, 512, 96 * 1024)}.items():
+        call = lambda i: _lib.check(L.vs_launch_floor(blocks, threads, lds, stream), "vs_launch_floor")  # noqa: E731
+        e2e, _ = time_calls(torch, call, 1, steps, 20)
+        res[key] = round(e2e, 2)
+    return res
+
+
+def boundary_rows(d, out):
+    """For the benched seed, computed outside the timed region: the oracle's count of rows whose draw lies within
+    1e-6 of a CDF boundary or whose top-p cut lies within 1e-6 of a cumulative boundary (the rows the parity
+    contract would excuse; near-flat top-p rows have CDF steps of ~7e-6, so many qualify), and how many rows'
+    tokens and kept-set sizes actually differ from the oracle's."""
+    from oracle import sampler_ref as S
+
+    ids = out.ids.cpu().numpy()
+    keep = out.keep.cpu().numpy()
+    nb = nd = nk = 0
+    for i in range(d["logits"].shape[0]):
+        c = S.counts_from_history(d["hists"][i]) if d["hists"] is not None else {}
+        r = S.sample(d["logits"][i], d["params"][i], float(d["u"][i]), c)
+        nb += int(r.kind == "sample" and (r.draw_boundary or r.topp_boundary))
+        nd += int(ids[i] != r.token)
+        nk += int(r.kind == "sample" and keep[i] != r.keep)
+    return {"boundary_rows": nb, "token_mismatches": nd, "keep_mismatches": nk, "rows": int(d["logits"].shape[0])}
+
+
 def cpu_baseline(d, budget_s=10.0):
     """The oracle (NumPy restatement of sampler.py) row by row, single-threaded, for about budget_s seconds."""
     from oracle import sampler_ref as S
@@ -251,7 +286,7 @@ def main():
         (e2e, kern), (e2e_w, kern_w), algo, ntok = bench_verify(torch, dev, d, a.steps, a.warmup, a.slots)
         B = d["logits_bf16"].shape[0]
     else:
-        (e2e, kern), (e2e_w, kern_w), algo = bench_sample(torch, dev, d, a.steps, a.warmup, a.slots)
+        (e2e, kern), (e2e_w, kern_w), algo, sout = bench_sample(torch, dev, d, a.steps, a.warmup, a.slots)
         B = d["logits"].shape[0]
         ntok = B
     others = {}
@@ -268,8 +303,10 @@ def main():
             if name == a.config or not sel(name):
                 continue
             dd = synth.CONFIGS[name](seed=0)
-            (oe, ok), (we, wk), ab = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
+            (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
+            if not a.no_cpu:
+                others[name].update(boundary_rows(dd, oout))
         if sel("c3_state"):
             dd = synth.CONFIGS["c3"](seed=0)
             (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)
@@ -297,6 +334,8 @@ def main():
             others[key]["unfused_us_per_step"] = round(ue, 2)
             others[key]["frac_of_8tbs"] = round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
+    parity = None if (a.no_cpu or verify) else boundary_rows(d, sout)
+    floor = launch_floor(torch, dev, a.steps)
     # One kernel per step, launched back to back: the per-step time is the kernel's average launch duration plus
     # the inter-dispatch gap (rocprofv3 --kernel-trace agrees within a few percent); per-launch event pairs add
     # their own overhead and are reported separately.
@@ -313,6 +352,8 @@ def main():
         "kernel_us_event_pairs": round(kern, 2), "warm_us_per_step": round(e2e_w, 2),
         "warm_kernel_us_event_pairs": round(kern_w, 2),
         "kernels_per_step": 1,
+        "launch_floor_us": floor,
+        "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(ach / PEAK_GBPS, 4), "traffic": load_traffic(a.config),
                      "algo_bytes": algo},

@@ -209,6 +209,11 @@ size_t vs_draft_workspace_bytes(int n, int S, int V);
  * process. No counterpart in the reference (its sampler is single-threaded host code). */
 int vs_set_spin_limit(unsigned polls);
 
+/* Launch one empty kernel of `blocks` workgroups of `threads` threads with `lds_bytes` of dynamic LDS on `stream`:
+ * a measurement hook (the launch floor a kernel of that shape pays, launched back to back). No counterpart in the
+ * reference. */
+int vs_launch_floor(int blocks, int threads, size_t lds_bytes, vs_stream_t stream);
+
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 

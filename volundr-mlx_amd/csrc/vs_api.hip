@@ -45,7 +45,21 @@ const DevInfo* dev_info() {
 
 }  // namespace vs
 
+namespace {
+// An empty kernel: the launch-floor measurement of vs_launch_floor (what a launch of a given shape costs with no
+// work in it, back to back on one stream).
+__global__ void vs_empty_kernel(int) {}
+}  // namespace
+
 extern "C" {
+
+int vs_launch_floor(int blocks, int threads, size_t lds_bytes, vs_stream_t stream) {
+  if (blocks < 1 || threads < 1 || threads > 1024) return vs::fail(VS_EINVAL, "vs_launch_floor: bad shape");
+  hipLaunchKernelGGL(vs_empty_kernel, dim3(blocks), dim3(threads), lds_bytes, (hipStream_t)stream, 0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return vs::hip_fail(e, "vs_launch_floor: launch");
+  return VS_OK;
+}
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
