@@ -205,9 +205,16 @@ size_t vs_draft_workspace_bytes(int n, int S, int V);
 
 /* Polls an inter-workgroup wait of vs_sample_batch / vs_sample_batch_state makes before it gives up and flags its
  * row VS_OUT_TIMEOUT (0 restores the default, ~2M polls). A testing hook: a tiny limit forces the timeout path, whose
- * rows report VS_OUT_TIMEOUT, commit no request state and leave the workspace zeroed. Applies to later calls of the
- * process. No counterpart in the reference (its sampler is single-threaded host code). */
+ * rows report VS_OUT_TIMEOUT, commit no request state and leave the workspace zeroed. Applies to later plain
+ * launches of the process (cooperative launches keep the default). No counterpart in the reference (its sampler is
+ * single-threaded host code). */
 int vs_set_spin_limit(unsigned polls);
+
+/* on != 0: later sampling calls of the process launch cooperatively (every workgroup of the grid resident at once,
+ * so a row barrier cannot starve when other streams hold CUs; ~18 us more per call); 0: plain launches (the
+ * default, unless the environment sets VS_COOPERATIVE=1). The Python layer uses it to retry a call whose rows
+ * reported VS_OUT_TIMEOUT. No counterpart in the reference. */
+int vs_set_cooperative(int on);
 
 /* Launch one empty kernel of `blocks` workgroups of `threads` threads with `lds_bytes` of dynamic LDS on `stream`:
  * a measurement hook (the launch floor a kernel of that shape pays, launched back to back). No counterpart in the

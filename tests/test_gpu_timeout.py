@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from volundr_amd import DeviceSamplers, Sampler, VsError, _lib, ops, synth
+from volundr_amd import DeviceSamplers, Sampler, _lib, ops, synth
 from volundr_amd._lib import OUT_TIMEOUT
 from volundr_amd.session import Sampling
 
@@ -51,16 +51,34 @@ def test_timeouts_flagged_and_workspace_left_clean(dev):
     assert _flags(again) == fl0
 
 
-def test_sampler_raises_on_timeout_and_recovers(dev):
+def test_sampler_falls_back_to_a_cooperative_launch(dev):
+    """A row whose barrier times out under a plain launch is repeated with a cooperative launch (the spin limit
+    applies to plain launches only): Sampler.sample returns the same token and logprob as an unforced call, and
+    consumes one draw, as the reference's sample() does."""
     sp = Sampling(temperature=0.8, top_p=0.9)  # FULL class on a full-vocabulary row: row barriers
-    s = Sampler(sp, vocab_valid=163840, request_id=3)
     x = torch.randn(163840, generator=torch.Generator().manual_seed(2)).to(dev)
-    rng0, n0 = s.rng, len(s.history)
-    with pytest.raises(VsError):
-        _forced(lambda: s.sample(x))
-    tok = s.sample(x)  # works again (the draw of the failed call was consumed by Sampler.uniform, as on the host)
-    assert 0 <= tok < 163840
-    assert s.rng != rng0 and len(s.history) == n0  # sample() does not accept
+    a = Sampler(sp, vocab_valid=163840, request_id=3)
+    b = Sampler(sp, vocab_valid=163840, request_id=3)
+    b.rng = a.rng
+    want = a.sample(x)
+    print("[timeout] forced Sampler.sample", flush=True)
+    got = _forced(lambda: b.sample(x))
+    assert got == want and b.last_logprob == a.last_logprob and b.rng == a.rng
+    assert len(b.history) == 0  # sample() does not accept
+
+
+def test_sample_rows_for_falls_back(dev):
+    from volundr_amd.sampler import sample_rows_for
+
+    d = synth.CONFIGS["c3"](seed=3)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    mk = lambda: [Sampler(sp, vocab_valid=x.shape[1], request_id=r) for r, sp in enumerate(d["params"])]  # noqa
+    a, b = mk(), mk()
+    for sa, sb in zip(a, b):
+        sb.rng = sa.rng
+    want = sample_rows_for(x, a)
+    got = _forced(lambda: sample_rows_for(x, b))
+    assert got == want and [s.rng for s in a] == [s.rng for s in b]
 
 
 def test_device_state_not_committed_for_timed_out_rows(dev):

@@ -12,6 +12,7 @@ namespace vs {
 static thread_local std::string g_err;
 unsigned long long* g_trace = nullptr;
 unsigned g_spin_limit = 0;
+int g_cooperative = 0;
 
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(int code, const std::string& msg) {
@@ -67,6 +68,11 @@ int vs_version(void) { return 6; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;
+  return VS_OK;
+}
+
+int vs_set_cooperative(int on) {
+  vs::g_cooperative = on ? 1 : 0;
   return VS_OK;
 }
 

@@ -328,7 +328,15 @@ __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) { return ld_de
 __device__ __forceinline__ u64 ld_relaxed64(const u64* p) { return ld_dev(p); }
 __device__ __forceinline__ double ld_relaxed_f64(const double* p) { return ld_dev(p); }
 // Wait until every memory operation this wave issued has completed (stores acknowledged by the coherent level).
-__device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// The s_waitcnt orders the hardware; the two signal fences order the compiler: no load or store may be moved
+// across the wait in either direction (a signal fence emits no instruction). Without them nothing in the
+// language would stop the compiler from sinking a data store below the wait, and hence below the counter RMW
+// that follows it, since the wait builtin is not a memory operation.
+__device__ __forceinline__ void publish_wait() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 __device__ __forceinline__ uint32_t ctr_add(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

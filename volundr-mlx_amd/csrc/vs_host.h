@@ -21,6 +21,8 @@ const DevInfo* dev_info();
 
 // Polls of an inter-workgroup wait before it gives up (0: the default). Set by vs_set_spin_limit.
 extern unsigned g_spin_limit;
+// Non-zero: sampling kernels are launched cooperatively (set by vs_set_cooperative).
+extern int g_cooperative;
 
 // Phase-timestamp buffer of development builds (VS_TRACE); always null in the shipped library.
 extern unsigned long long* g_trace;

@@ -2454,7 +2454,7 @@ static bool use_cooperative() {
     const char* v = getenv("VS_COOPERATIVE");
     return v && v[0] == '1';
   }();
-  return coop;
+  return coop || g_cooperative != 0;
 }
 
 extern "C" size_t vs_sample_workspace_bytes(int B, int V) {
@@ -2528,7 +2528,10 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.lds_ch = lds_ch;
   a.kcap = kcap;
   a.kmax = kmax;
-  a.spin_limit = g_spin_limit ? g_spin_limit : 1u << 21;
+  // The testing spin limit applies to plain launches only: a cooperative launch guarantees that every workgroup of
+  // a row is resident, so its waits keep the default bound.
+  const bool coop = use_cooperative();
+  a.spin_limit = (g_spin_limit && !coop) ? g_spin_limit : 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.zspan_max = (63 - bits) * 0.6931471805599453 - 13.815510557964274;  // ln(fix_scale) - ln(1e6)
   a.params = list_k > 0 ? nullptr : params;
@@ -2555,7 +2558,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
     // workgroup of a row is resident and the row barriers complete; a plain launch is ~18 us cheaper than a
     // cooperative one on MI355X. VS_COOPERATIVE=1 requests the residency guarantee of a cooperative launch; without
     // it, a barrier that cannot complete ends with VS_OUT_TIMEOUT on that row instead of hanging.
-    if (use_cooperative())
+    if (coop)
       e = hipLaunchCooperativeKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);
     else
       e = hipLaunchKernel(kfn, dim3(a.B * G), dim3(SNT), kargs, (unsigned)lds, (hipStream_t)stream);

@@ -44,7 +44,7 @@ ABI_VERSION = 6
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
-           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor")
+           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_set_cooperative")
 
 _lib = None
 
@@ -77,6 +77,8 @@ def load():
     L.vs_lmhead_workspace_bytes.restype = sz
     L.vs_launch_floor.argtypes = [i32, i32, sz, vp]
     L.vs_launch_floor.restype = i32
+    L.vs_set_cooperative.argtypes = [i32]
+    L.vs_set_cooperative.restype = i32
     L.vs_set_spin_limit.argtypes = [ctypes.c_uint]
     L.vs_set_spin_limit.restype = i32
     L.vs_topk_batch.argtypes = [vp, i32, i32, i32, i64, i32, vp, vp, vp, sz, vp]

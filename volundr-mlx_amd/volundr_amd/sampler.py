@@ -13,7 +13,7 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 from ._lib import OUT_NOFINITE, OUT_TIMEOUT, VsError
 
 MASK = (1 << 64) - 1
@@ -144,15 +144,34 @@ class Sampler:
             x = torch.as_tensor(np.asarray(x, dtype=np.float32)).cuda()
         rng0 = self.rng
         u = self.uniform() if not self.sp.greedy else 0.0
-        out = ops.sample_batch(x.reshape(1, -1), [self.sp], [u], [self.history], [self.produced], [list(extra)])
+        out = _sample_checked(x.reshape(1, -1), [self.sp], [u], [self.history], [self.produced], [list(extra)])
         flags = int(out.flags[0].item()) & 0xFFFFFFFF
-        if flags & OUT_TIMEOUT:
-            ops.reset_workspace(x.device)
-            raise VsError("vs_sample_batch: an inter-workgroup wait timed out")
         if flags & OUT_NOFINITE:  # sampler.py:131-132 returns before drawing (:154): the generator is not advanced
             self.rng = rng0
         self.last_logprob = float(out.logprobs[0].item())
         return int(out.ids[0].item())
+
+
+def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
+    """ops.sample_batch with the recovery of a row barrier that could not complete (VS_OUT_TIMEOUT: other work held
+    the CUs a row's workgroups needed at once). The flagged call committed nothing and left its workspace zeroed, so
+    it is repeated once with a cooperative launch, which makes every workgroup resident together; a second timeout
+    raises VsError."""
+    out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
+    if not any((int(f) & 0xFFFFFFFF) & OUT_TIMEOUT for f in out.flags.cpu().tolist()):
+        return out
+    L = _lib.load()
+    ops.reset_workspace(logits.device)
+    L.vs_set_cooperative(1)
+    try:
+        out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
+        flags = out.flags.cpu().tolist()
+    finally:
+        L.vs_set_cooperative(0)
+    if any((int(f) & 0xFFFFFFFF) & OUT_TIMEOUT for f in flags):
+        ops.reset_workspace(logits.device)
+        raise VsError("vs_sample_batch: an inter-workgroup wait timed out, also under a cooperative launch")
+    return out
 
 
 def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Optional[Sequence[int]] = None):
@@ -181,13 +200,10 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
         avv.append(s.vv if argmax_only else None)
     if todo:
         sub = logits[[rows[i] for i in todo]]
-        out = ops.sample_batch(sub, sps, us, hists, prods, extras, argmax_vv=avv)
+        out = _sample_checked(sub, sps, us, hists, prods, extras, argmax_vv=avv)
         ids = out.ids.cpu().tolist()
         lps = out.logprobs.cpu().tolist()
         fl = out.flags.cpu().tolist()
-        if any((f & 0xFFFFFFFF) & OUT_TIMEOUT for f in fl):
-            ops.reset_workspace(logits.device)
-            raise VsError("vs_sample_batch: an inter-workgroup wait timed out")
         for k, i in enumerate(todo):
             if (fl[k] & 0xFFFFFFFF) & OUT_NOFINITE:
                 samplers[i].rng = rng0[k]  # no draw consumed (sampler.py:131-132)
