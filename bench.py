@@ -183,8 +183,10 @@ def bench_lmhead(torch, dev, steps, warmup, B=1, T=17):
 
 
 def launch_floor(torch, dev, steps):
-    """Microseconds per launch of an empty kernel issued back to back through the library's C ABI (the same way the
-    sampling kernel is launched), for a one-workgroup grid and for full-chip grids of 512-thread workgroups."""
+    """Microseconds per launch of an empty kernel issued back to back through the library's C ABI, for a
+    one-workgroup grid and for full-chip grids of 512-thread workgroups: one launch per Python call (the way the
+    benchmark loops issue the sampling kernel, host overhead included) and 100 launches per call (the device-side
+    floor: dispatch, start-up and completion of a kernel of that shape)."""
     from volundr_amd import _lib
 
     L = _lib.load()
@@ -192,9 +194,11 @@ def launch_floor(torch, dev, steps):
     res = {}
     for key, (blocks, threads, lds) in {"1x64": (1, 64, 0), "256x512": (256, 512, 0),
                                          "256x512_lds96k": (256, 512, 96 * 1024)}.items():
-        call = lambda i: _lib.check(L.vs_launch_floor(blocks, threads, lds, stream), "vs_launch_floor")  # noqa: E731
-        e2e, _ = time_calls(torch, call, 1, steps, 20)
-        res[key] = round(e2e, 2)
+        for reps in (1, 100):
+            call = lambda i: _lib.check(L.vs_launch_floor(blocks, threads, lds, reps, stream),  # noqa: E731
+                                        "vs_launch_floor")
+            e2e, _ = time_calls(torch, call, 1, max(steps // reps, 5), 5)
+            res[f"{key}{'' if reps == 1 else '_device'}"] = round(e2e / reps, 2)
     return res
 
 

@@ -216,10 +216,10 @@ int vs_set_spin_limit(unsigned polls);
  * reported VS_OUT_TIMEOUT. No counterpart in the reference. */
 int vs_set_cooperative(int on);
 
-/* Launch one empty kernel of `blocks` workgroups of `threads` threads with `lds_bytes` of dynamic LDS on `stream`:
- * a measurement hook (the launch floor a kernel of that shape pays, launched back to back). No counterpart in the
- * reference. */
-int vs_launch_floor(int blocks, int threads, size_t lds_bytes, vs_stream_t stream);
+/* Launch `reps` empty kernels of `blocks` workgroups of `threads` threads with `lds_bytes` of dynamic LDS back to
+ * back on `stream` from one host call: a measurement hook (the launch floor a kernel of that shape pays; reps > 1
+ * takes the caller's per-call host overhead out of the figure). No counterpart in the reference. */
+int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stream_t stream);
 
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);

@@ -24,22 +24,26 @@ def keys_of(vals, idx):
     return (ord32(vals) << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx.astype(np.uint64))
 
 
-def heads_bound(head_keys, keff):
-    """The kernel's bisection: th = the largest 32-bit value reached by >= keff heads; M = th << 32 (0 if fewer
-    than keff heads are non-zero)."""
+BOUND_BITS = 16  # bits of the ord32 value the kernel's bisections resolve (vs_sample.hip BOUND_BITS)
+
+
+def heads_bound(head_keys, keff, bits=BOUND_BITS):
+    """The kernel's bisection over the top `bits` bits: th = the largest such value reached by >= keff heads;
+    M = th << 32 (0 if fewer than keff heads are non-zero)."""
     hh = (head_keys >> np.uint64(32)).astype(np.uint64)
     if int((hh != 0).sum()) < keff:
         return np.uint64(0)
     th = 0
-    for b in range(31, -1, -1):
+    for b in range(31, 31 - bits, -1):
         c = th | (1 << b)
         if int((hh >= c).sum()) >= keff:
             th = c
     return np.uint64(th) << np.uint64(32)
 
 
+@pytest.mark.parametrize("bits", [16, 32])
 @pytest.mark.parametrize("seed", range(40))
-def test_topk_merge_bound_never_cuts_the_top(seed):
+def test_topk_merge_bound_never_cuts_the_top(seed, bits):
     rng = np.random.default_rng(seed)
     G = int(rng.choice([3, 8, 16, 40, 64]))
     k = int(rng.integers(1, 8 * G + 1))
@@ -65,7 +69,7 @@ def test_topk_merge_bound_never_cuts_the_top(seed):
             part = keys[g * chunk:(g + 1) * chunk]
             wmax = sorted((int(part[w::8].max()) if part[w::8].size else 0 for w in range(8)), reverse=True)
             heads.extend(wmax[:r])
-    M = heads_bound(np.array(heads, dtype=np.uint64), keff)
+    M = heads_bound(np.array(heads, dtype=np.uint64), keff, bits)
     top = np.sort(keys)[::-1][:keff]
     assert int(top[-1]) >= int(M)
     assert int((keys >= M).sum()) >= keff
@@ -90,3 +94,44 @@ def test_fixed_point_normaliser_within_5e7(bits):
         zfix = np.array([float(v) for v in cfx]) / scale
         rel = np.abs(zfix - cf) / cf
         assert rel.max() <= 5e-7, (bits, trial, rel.max())
+
+
+def test_truncated_bound_is_close():
+    """The 16-bit bound is below the exact one by less than a factor 1 + 2^-7 in value (positive values)."""
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        vals = (np.abs(rng.standard_normal(64)) * rng.choice([0.01, 1, 100]) + 1e-3).astype(np.float32)
+        keys = keys_of(vals, np.arange(64))
+        keff = int(rng.integers(1, 65))
+        exact = heads_bound(keys, keff, 32) >> np.uint64(32)
+        trunc = heads_bound(keys, keff, 16) >> np.uint64(32)
+        assert trunc <= exact
+        ve = np.array([exact & 0x7FFFFFFF], np.uint32).view(np.float32)[0]
+        vt = np.array([trunc & 0x7FFFFFFF], np.uint32).view(np.float32)[0]
+        assert vt <= ve <= vt * (1 + 2.0 ** -7) * (1 + 1e-7)
+
+
+def fixed_mass(e, S):
+    """The kernel's integer form of round(e * 2^S) from the bits of a float32 0 <= e <= 1 (vs_sample.hip
+    fixed_mass)."""
+    b = int(np.array([e], np.float32).view(np.uint32)[0])
+    E = b >> 23
+    m = (b & 0x7FFFFF) | 0x800000
+    k = E - 150 + S
+    if E == 0:
+        return 0
+    if k >= 0:
+        return m << k
+    r = -k
+    return 0 if r >= 25 else (m + (1 << (r - 1))) >> r
+
+
+@pytest.mark.parametrize("S", [29, 38, 45, 46])
+def test_fixed_mass_matches_float64_rounding(S):
+    rng = np.random.default_rng(S)
+    es = np.concatenate([np.exp(-rng.random(4000) * 60).astype(np.float32),
+                         np.array([0.0, 1.0, 0.5, 2.0 ** -S, 2.0 ** -(S + 1), 3 * 2.0 ** -(S + 2), 1e-30],
+                                  np.float32)])
+    for e in es:
+        want = int(np.floor(np.float64(e) * 2.0 ** S + 0.5))
+        assert fixed_mass(float(e), S) == want, (e, S)

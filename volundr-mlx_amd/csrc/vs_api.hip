@@ -54,9 +54,10 @@ __global__ void vs_empty_kernel(int) {}
 
 extern "C" {
 
-int vs_launch_floor(int blocks, int threads, size_t lds_bytes, vs_stream_t stream) {
-  if (blocks < 1 || threads < 1 || threads > 1024) return vs::fail(VS_EINVAL, "vs_launch_floor: bad shape");
-  hipLaunchKernelGGL(vs_empty_kernel, dim3(blocks), dim3(threads), lds_bytes, (hipStream_t)stream, 0);
+int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stream_t stream) {
+  if (blocks < 1 || threads < 1 || threads > 1024 || reps < 1) return vs::fail(VS_EINVAL, "vs_launch_floor: bad shape");
+  for (int i = 0; i < reps; ++i)
+    hipLaunchKernelGGL(vs_empty_kernel, dim3(blocks), dim3(threads), lds_bytes, (hipStream_t)stream, 0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return vs::hip_fail(e, "vs_launch_floor: launch");
   return VS_OK;

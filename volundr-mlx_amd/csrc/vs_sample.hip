@@ -38,6 +38,7 @@ constexpr int GSMALL = 128;      // kept sets up to this size are finished in on
 constexpr int GCAP2 = 512;       // elements gathered from the located value bins (<= SNT: one per thread in the final scans)
 static_assert(GCAP2 <= SNT, "the final in-bin scans hold one gathered element per thread");
 constexpr int NSET = 4;          // coarse value bins refined in the second histogram round
+constexpr int BIGCAP = 5120;     // kept logits of the selected coarse bins that one workgroup resolves after a gather
 constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
@@ -95,7 +96,8 @@ constexpr size_t OFF_PART = sizeof(RowCtl);
 constexpr size_t OFF_CAND = OFF_PART + sizeof(Part) * GMAX;
 constexpr size_t OFF_GATHER = OFF_CAND + sizeof(u64) * KEYS_CAP;
 constexpr size_t OFF_HIST = OFF_GATHER + sizeof(u64) * GCAP;
-constexpr size_t ROW_WS = OFF_HIST + sizeof(HistSlot) * MAX_ROUNDS;
+constexpr size_t OFF_BIG = OFF_HIST + sizeof(HistSlot) * MAX_ROUNDS;
+constexpr size_t ROW_WS = OFF_BIG + sizeof(u64) * BIGCAP;
 
 struct SampleArgs {
   const void* logits;
@@ -112,7 +114,8 @@ struct SampleArgs {
   int kcap;    // candidate-list capacity per workgroup (a power of two)
   int kmax;    // largest top_k of the TOPK class for this launch
   uint32_t spin_limit;
-  double fix_scale;  // probability -> fixed point
+  double fix_scale;  // probability -> fixed point (2^fix_shift)
+  int fix_shift;
   double zspan_max;     // ln(fix_scale) - ln(1e6): the kept-value span up to which z comes from fixed point
   const vs_row_params* params;
   vs_row_state* state;  // device-resident request state, or null
@@ -151,6 +154,10 @@ struct Smem {
   uint32_t* fc;  // NSET*256 fine-bin counts
   u64* ffix;     // NSET*256 fine-bin fixed-point masses
   double* ff64;  // NSET*256 fine-bin float64 masses
+  uint32_t* rc;  // 256-bin histogram of a workgroup-local radix select (count, fixed-point and float64 mass,
+  u64* rfix;     // largest key), used while the other histograms must keep their contents
+  double* rf64;
+  u64* rmk;
 };
 
 __host__ __device__ inline size_t xv_bytes(int CH) { return ((size_t)CH * 4 + 15) & ~(size_t)15; }
@@ -189,10 +196,19 @@ __device__ __forceinline__ Smem carve(char* base, int CH) {
   s.ff64 = (double*)p;
   p += NSET * NBIN * 8;
   s.fc = (uint32_t*)p;
+  p += NSET * NBIN * 4;
+  s.rfix = (u64*)p;
+  p += NBIN * 8;
+  s.rf64 = (double*)p;
+  p += NBIN * 8;
+  s.rmk = (u64*)p;
+  p += NBIN * 8;
+  s.rc = (uint32_t*)p;
   return s;
 }
 static size_t smem_bytes(int CH) {
-  return region0(CH) + 2 * KCAP * 8 + NBIN * (8 + 8 + 8 + 4) + NRED * (8 + 8 + 4) + NMISC * 4 + NSET * NBIN * (8 + 8 + 4);
+  return region0(CH) + 2 * KCAP * 8 + NBIN * (8 + 8 + 8 + 4) + NRED * (8 + 8 + 4) + NMISC * 4 + NSET * NBIN * (8 + 8 + 4) +
+         NBIN * (8 + 8 + 8 + 4);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -453,7 +469,10 @@ __device__ __forceinline__ void wave_sample_em(const Smem& s, const u64* a, int 
       if (q < E && i0 + q < n) {
         const float xs = key_value(a[i0 + q]) / tt;
         const float d = xs - xs0;  // float32 subtraction (:142)
-        pr[q] = exp((double)d);    // float64 exp
+        // exp in float32, widened: relative error <= 2^-23 per mass (the reference's float64 exp of the same d
+        // differs by less; sums and cumulative sums inherit that bound, far inside the 1e-6 boundary band and the
+        // 1e-5 logprob tolerance; pr[0] = exp(0) = 1 exactly, so a dominant first token's logprob stays exact)
+        pr[q] = (double)expf(d);
         ls += pr[q];
       }
     }
@@ -617,6 +636,9 @@ __device__ __forceinline__ void rank_sort(const u64* in, int n, u64* out, int ko
 }
 
 constexpr int SEGW = KEYS_CAP / SNW;  // per-wave candidate segment
+// Bits of an ord32 value resolved by the ballot bisections that bound the k-th largest logit from below (sign,
+// exponent and 7 mantissa bits).
+constexpr int BOUND_BITS = 16;
 // Key-area offset (u64 words) of the value-bin prefix sums: above what the final in-bin resolution uses
 // (4352 words), 3 * 256 coarse + 3 * NSET * 256 fine words.
 constexpr int PFX_OFF = 4352;
@@ -710,7 +732,9 @@ __device__ __forceinline__ LaneBound lane_max_bound(uint32_t tmax, int k, const 
   const int got = nz < q ? nz : q;
   uint32_t wb = 0;
   if (got > 0) {
-    for (int b = 31; b >= 0; --b) {
+    // the top BOUND_BITS bits only: the result (low bits zero) is still a valid lower bound, within a factor of
+    // 1 + 2^-7 of the exact q-th largest value, for half the dependent ballot steps
+    for (int b = 31; b >= 32 - BOUND_BITS; --b) {
       const uint32_t c = wb | (1u << b);
       if ((int)__popcll(__ballot(tmax >= c)) >= got) wb = c;
     }
@@ -810,6 +834,36 @@ __device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Fi
     if (A.out_flags) A.out_flags[r] = flags;
     if (A.out_keep) A.out_keep[r] = f.keep;
   }
+}
+
+// round(e * 2^S) for a float 0 <= e <= 1 and 0 < S <= 63 - 24 (half-way cases rounded up), from the bits of e:
+// e = m * 2^(E - 150) with a 24-bit m, so the product is m shifted by k = E - 150 + S, exact when k >= 0. Equal to
+// (u64)((double)e * 2^S + 0.5), without the float64 work.
+__device__ __forceinline__ u64 fixed_mass(float e, int S) {
+  const uint32_t b = __float_as_uint(e);
+  const int E = (int)(b >> 23);
+  const uint32_t m = (b & 0x7FFFFFu) | 0x800000u;
+  const int k = E - 150 + S;
+  // both candidates computed, then selected (no branch): k >= 0 shifts left exactly; 1 <= -k <= 31 rounds the
+  // right shift (half-way up), and m >> 25.. is 0 anyway, which the clamp to 31 keeps
+  const int kl = k > 0 ? k : 0;
+  const int r = k < 0 ? (-k < 31 ? -k : 31) : 1;
+  const u64 up = (u64)m << kl;
+  const uint32_t dn = (m + (1u << (r - 1))) >> r;
+  const u64 v = k >= 0 ? up : (u64)dn;
+  return E == 0 ? (u64)0 : v;
+}
+
+// e^d for d <= 0 with about 2 ulp relative error: 2^(d log2 e) from the hardware base-2 exponential, with the
+// rounding error of the product d * log2(e) (exact through an fma, plus the constant's own tail) applied as a
+// first-order correction: e^d = 2^y * 2^(lo) ~ 2^y (1 + lo ln 2) for the tiny lo.
+__device__ __forceinline__ float exp_nonpos(float d) {
+  const float L = 1.44269502162933349609375f;  // log2(e) rounded to float
+  const float Llo = 1.9259629891e-8f;          // log2(e) - L
+  const float y = d * L;
+  const float lo = fmaf(d, L, -y) + d * Llo;
+  const float e = __builtin_amdgcn_exp2f(y);
+  return fmaf(e, lo * 0.693147180559945309f, e);
 }
 
 // Sorted-id range search: first position in ids[b, e) with ids[p] >= x.
@@ -978,6 +1032,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int NV = A.NV;
   VS_TR_DECL(A);
   VS_TR(A, 0);
+  VS_TRC(A, 30);
 
   // ---- load the chunk into VGPRs (one HBM read) ----
   float v[EPT_MAX];
@@ -1413,6 +1468,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           const int idx = t + u * SNT;
           r8[u] = idx < tot ? ld_dev(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
         }
+#ifdef VS_TRACE
+        publish_wait();
+        VS_TRX(50);
+#endif
         const int ln = lane_id();
         const bool hb8 = r <= 8;  // heads bound (else, sorted lists only, the smallest r-th key)
         int nf2 = 0, full = 0;
@@ -1437,6 +1496,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             h2 = full ? h : h2;
           }
         }
+#ifdef VS_TRACE
+        publish_wait();
+        VS_TRX(51);
+#endif
         n = wave_sum(nf2);
         bam = wave_max(k2);
         keff = k < n ? k : n;  // sampler.py:133-134
@@ -1452,15 +1515,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             hh[u] = (uint32_t)(hv[u] >> 32);
             nzh += (int)__popcll(__ballot(hh[u] != 0));
           }
-          uint32_t th = 0;
+          uint32_t th = 0;  // the top BOUND_BITS bits: a lower bound just as valid (see lane_max_bound)
           if (hu == 1) {
 #pragma unroll
-            for (int b = 31; b >= 0; --b) {
+            for (int b = 31; b >= 32 - BOUND_BITS; --b) {
               const uint32_t c = th | (1u << b);
               th = (int)__popcll(__ballot(hh[0] >= c)) >= keff ? c : th;
             }
           } else {
-            for (int b = 31; b >= 0; --b) {
+            for (int b = 31; b >= 32 - BOUND_BITS; --b) {
               const uint32_t c = th | (1u << b);
               int cnt = 0;
 #pragma unroll
@@ -1474,6 +1537,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           const u64 mb = wave_min(h2);
           M = nfull * r >= keff ? mb : (u64)0;
         }
+        VS_TRX(52);
         // a survivor is >= M and, in a sorted list, at a position below keff
         int cnt = 0;
 #pragma unroll
@@ -1578,6 +1642,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   ++nbar;
   ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
   VS_TR(A, 3);
+  VS_TRC(A, 31);
   Final fin;
   fin.token = -1;
   fin.lp = 0.0f;
@@ -1697,8 +1762,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // The per-element test of every pass: xs = x / t (float32, sampler.py:141, computed once and reused for
         // the bin and the mass), the key, and whether x is in the kept set; mode is uniform, combined with bit
         // operations so that no pass branches on it.
-        auto keep_xs = [&](float x, int e, u64& kk, float& xs) -> bool {
-          xs = x / tt;
+        auto keep_xs = [&](float x, int e, u64& kk, float& xs, auto unit_t) -> bool {
+          xs = decltype(unit_t)::value ? x : x / tt;  // x / 1 == x exactly (signed zeros, infinities, NaN)
           kk = key64(x, (uint32_t)e);
           const bool m1 = (mode == 1) & (kk >= Tk);
           const bool m2 = (mode == 2) & ((x >= xhi) | (xs >= thr));
@@ -1724,9 +1789,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         };
         auto mass = [&](float xs, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
           const float d = xs - xs0;
-          const double pr = (double)expf(d);
-          *fx = (u64)(pr * scale + 0.5);
-          return pr;
+          const float e = exp_nonpos(d);
+          *fx = fixed_mass(e, A.fix_shift);  // == (u64)((double)e * scale + 0.5), in integer arithmetic
+          return (double)e;
         };
         VS_TR(A, 4);
         // ---- value-bin pass 1: coarse mass histogram of the kept set + its size + a bounded gather ----
@@ -1774,12 +1839,49 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // kept count exceeds GSMALL and no gather happens.
         const bool few = nq * 4 <= SNT;
         // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it
-        auto pass1 = [&](auto with_f64) -> int {
+        // and per unit temperature (no division: about a fifth of the work per logit)
+        auto pass1 = [&](auto with_f64, auto unit_t) -> int {
           int cnt = 0;
+#ifdef VS_EXP_DUP_EXP
+          float dup_acc = 0.0f;
+#endif
+          if (!few) {
+            // Dense case (many qualifying lanes): every position of the chunk, four LDS reads in flight per lane,
+            // and no branch per logit: a logit outside the kept set adds nothing (a zero increment to a bin of
+            // its own, so that it does not contend with the kept ones) and gets the id 0xFFFF.
+            const int nel = hi - lo;
+            for (int i0 = t; i0 < nel; i0 += 4 * SNT) {
+              float xq[4];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const int iq = i0 + u * SNT;
+                xq[u] = s.xv[iq < nel ? iq : 0];
+              }
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * SNT;
+                const float x = xq[u];
+                u64 kk;
+                float xs;
+                const bool keep = (i < nel) & (x >= xlb) & keep_xs(x, lo + i, kk, xs, unit_t);
+                u64 fx;
+                const double pr = mass(xs, &fx);
+                const int fo = fine_of(xs);
+                if (i < nel) fid[i] = keep ? (uint16_t)fo : (uint16_t)0xFFFFu;
+                const int c = fo >> 8;
+                const int dmy = t & (NBIN - 1);
+                atomicAdd(keep ? &s.hc[c] : &s.rc[dmy], keep ? 1u : 0u);
+                atomicAdd(keep ? &s.hfix[c] : &s.rfix[dmy], keep ? fx : (u64)0);
+                if constexpr (decltype(with_f64)::value) unsafeAtomicAdd(keep ? &s.hf64[c] : &s.rf64[dmy], keep ? pr : 0.0);
+                cnt += keep ? 1 : 0;
+              }
+            }
+            return cnt;
+          }
           FOR_KEPT({
             u64 kk;
             float xs;
-            if (keep_xs(x, e, kk, xs)) {
+            if (keep_xs(x, e, kk, xs, unit_t)) {
               ++cnt;
               u64 fx;
               const double pr = mass(xs, &fx);
@@ -1788,6 +1890,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               const int c = fo >> 8;
               atomicAdd(&s.hc[c], 1u);
               atomicAdd(&s.hfix[c], fx);
+#ifdef VS_EXP_DUP_ATOM
+              atomicAdd(&s.rc[c], 1u);
+              atomicAdd(&s.rfix[c], fx);
+#endif
+#ifdef VS_EXP_DUP_EXP
+              dup_acc += expf(xs * 0.5f - xs0);
+#endif
               if constexpr (decltype(with_f64)::value) unsafeAtomicAdd(&s.hf64[c], pr);
               if (few) {
                 const int p = atomicAdd(&s.misc[15], 1);
@@ -1795,9 +1904,16 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
             }
           })
+#ifdef VS_EXP_DUP_EXP
+          if (dup_acc == 12345.0f) s.rc[t & 255] = 1u;
+#endif
           return cnt;
         };
-        const int cbr = zfix_only ? pass1(std::false_type{}) : pass1(std::true_type{});
+        const bool unit_t = tt == 1.0f;
+        const int cbr = zfix_only ? (unit_t ? pass1(std::false_type{}, std::true_type{})
+                                            : pass1(std::false_type{}, std::false_type{}))
+                                  : (unit_t ? pass1(std::true_type{}, std::true_type{})
+                                            : pass1(std::true_type{}, std::false_type{}));
         int cb;
         if (few) {
           __syncthreads();
@@ -1820,7 +1936,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             FOR_KEPT({
               u64 kk;
               float xs;
-              if (keep_xs(x, e, kk, xs)) s.keys[atomicAdd(&s.misc[15], 1)] = kk;
+              if (keep_xs(x, e, kk, xs, std::false_type{})) s.keys[atomicAdd(&s.misc[15], 1)] = kk;
             })
             __syncthreads();
           }
@@ -1919,8 +2035,273 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               ++ns;
             }
             VS_TRX(45);
+            // kept logits of the row in the selected coarse bins (global counts)
+            int ncand = 0;
+#pragma unroll
+            for (int q = 0; q < NSET; ++q) ncand += q < ns ? (int)s.hc[set[q]] : 0;
+            const int bigcap = BIGCAP < A.lds_ch / 2 ? BIGCAP : A.lds_ch / 2;  // they must fit the chunk area
             if (ns > NSET) {
               radix = true;
+            } else if (ncand <= bigcap) {
+              // ---- the selected coarse bins hold few enough logits: gather them all, and let the row's last
+              // workgroup resolve the top-p cut and the draw on its own (a fine histogram of the gathered keys, then
+              // the exact key order inside the located fine bins), with no further row barrier ----
+              static_assert(NSET == 4, "the coarse-bin test below names four set slots");
+              int sd4[NSET];
+#pragma unroll
+              for (int q = 0; q < NSET; ++q) sd4[q] = q < ns ? set[q] : -1;
+              u64* stg = s.tk;  // staging: 2 * KCAP keys (the qualifying-lane list is not read on this path)
+              u64* big = (u64*)(rws + OFF_BIG);
+              if (t == 0) {
+                s.misc[16] = 0;
+                s.misc[19] = 0;
+              }
+              __syncthreads();
+#define BIG_PRED                                                                                        \
+  ((id != 0xFFFFu) & (((int)(id >> 8) == sd4[0]) | ((int)(id >> 8) == sd4[1]) | ((int)(id >> 8) == sd4[2]) | \
+                      ((int)(id >> 8) == sd4[3])))
+              FOR_FID(BIG_PRED, {
+                const int p = atomicAdd(&s.misc[16], 1);
+                if (p < 2 * KCAP) stg[p] = key64(s.xv[i], (uint32_t)(lo + i));
+              })
+              __syncthreads();
+              const int nloc = s.misc[16];
+              if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
+              __syncthreads();
+              if (nloc) {
+                const int base = s.misc[17];
+                if (nloc <= 2 * KCAP) {
+                  for (int i = t; i < nloc; i += SNT) st_dev(&big[base + i], stg[i]);
+                } else {  // more than the staging area: a second visit stores them directly
+                  FOR_FID(BIG_PRED, {
+                    const int p = atomicAdd(&s.misc[19], 1);
+                    st_dev(&big[base + p], key64(s.xv[i], (uint32_t)(lo + i)));
+                  })
+                }
+              }
+#undef BIG_PRED
+              g0_writes = false;
+              VS_TR(A, 6);
+              if (!arrive_done()) {
+                VS_TR_FLUSH(A);
+                return;
+              }
+              VS_TR(A, 7);
+              // ---- final (last workgroup of the row): the gathered keys go to the chunk area, are histogrammed by
+              // fine bin and placed in fine-bin order (an index array), so that each pick reads its bin's members
+              // directly ----
+              int m = (int)ld_relaxed(&ctl->g2count);
+              m = m < bigcap ? m : bigcap;  // == ncand
+              u64* bk = (u64*)s.xv;
+              uint16_t* ord = (uint16_t*)s.keys;           // [BIGCAP] gathered positions in fine-bin order
+              uint32_t* cur = (uint32_t*)(s.keys + 2048);  // [NSET * NBIN] per-bin placement cursors
+              static_assert(BIGCAP * 2 <= 2048 * 8, "the order array stays below the cursors");
+              static_assert(2048 + NSET * NBIN / 2 <= PFX_OFF, "the cursors stay below the prefix sums");
+              for (int i = t; i < NSET * NBIN; i += SNT) {
+                s.fc[i] = 0;
+                s.ffix[i] = 0;
+                s.ff64[i] = 0.0;
+                cur[i] = 0;
+              }
+              constexpr int NL = (BIGCAP + SNT - 1) / SNT;
+              int bb[NL];  // each held key's fine bin (set * NBIN + fine digit)
+              {
+                u64 r[NL];
+#pragma unroll
+                for (int u = 0; u < NL; ++u) {  // every load in flight at once
+                  const int i = t + u * SNT;
+                  r[u] = i < m ? ld_dev(&big[i]) : (u64)0;
+                }
+                __syncthreads();  // the fine bins are clear
+                auto set_of = [&](int c) -> int { return sd4[1] == c ? 1 : (sd4[2] == c ? 2 : (sd4[3] == c ? 3 : 0)); };
+#pragma unroll
+                for (int u = 0; u < NL; ++u) {
+                  const int i = t + u * SNT;
+                  bb[u] = 0;
+                  if (i < m) {
+                    bk[i] = r[u];
+                    const float xs = key_value(r[u]) / tt;
+                    const int fo = fine_of(xs);
+                    u64 fx;
+                    const double pr = mass(xs, &fx);
+                    const int b2 = set_of(fo >> 8) * NBIN + (fo & 0xFF);
+                    bb[u] = b2;
+                    atomicAdd(&s.fc[b2], 1u);
+                    atomicAdd(&s.ffix[b2], fx);
+                    if (!zfix_only) unsafeAtomicAdd(&s.ff64[b2], pr);
+                  }
+                }
+              }
+              __syncthreads();
+              u64* fpc = cpc + 3 * NBIN;  // [NSET][NBIN] each
+              u64* fpw = fpc + NSET * NBIN;
+              double* fpf = (double*)(fpw + NSET * NBIN);
+              {
+                const int j = t / WAVE;
+                if (j < ns)
+                  hist_prefix(s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN, fpc + j * NBIN, fpw + j * NBIN,
+                              fpf + j * NBIN);
+              }
+              __syncthreads();
+              // first position of fine bin b2 in the order array: the sets one after another, each in scan order
+              auto bin_start = [&](int b2) -> int {
+                const int j = b2 / NBIN;
+                int base = 0;
+#pragma unroll
+                for (int q = 0; q < NSET; ++q) base += q < j ? (int)fpc[q * NBIN] : 0;
+                return base + (int)(fpc[b2] - (u64)s.fc[b2]);
+              };
+#pragma unroll
+              for (int u = 0; u < NL; ++u) {
+                const int i = t + u * SNT;
+                if (i < m) ord[bin_start(bb[u]) + (int)atomicAdd(&cur[bb[u]], 1u)] = (uint16_t)i;
+              }
+              __syncthreads();
+              VS_TR(A, 27);
+              struct BLoc {
+                int id, set_j;
+                u64 cnt_before, fix_before;
+                double f64_before;
+              };
+              auto blocate = [&](double target) -> BLoc {
+                BLoc r;
+                const ScanOut co = cfind(target);
+                int j = -1;
+#pragma unroll
+                for (int q = 0; q < NSET; ++q)
+                  if (q < ns && sd4[q] == co.digit) j = q;
+                r.set_j = j;
+                r.cnt_before = co.cnt_before;
+                r.fix_before = co.fix_before;
+                r.f64_before = co.f64_before;
+                r.id = co.digit << 8;
+                if (j >= 0) {
+                  const ScanOut fo = hist_find(s.fc + j * NBIN, s.ffix + j * NBIN, s.ff64 + j * NBIN, fpc + j * NBIN,
+                                               fpw + j * NBIN, fpf + j * NBIN, target - (double)co.fix_before);
+                  r.id |= fo.digit;
+                  r.cnt_before += fo.cnt_before;
+                  r.fix_before += fo.fix_before;
+                  r.f64_before += fo.f64_before;
+                }
+                return r;
+              };
+              struct BPick {
+                u64 key, cnt_in, fix_in, fix;
+                double f64_in, f64;
+              };
+              // The first member (descending key) of the located fine bin whose cumulative mass inside the bin
+              // reaches `tgt` (the bin's last member if none does, which only rounding can cause).
+              // Up to 64 members: every wave computes it on its own (bitonic sort in registers, wave scans and a
+              // ballot), so no barrier is needed. More: the whole workgroup, by a mass-weighted radix select.
+              auto bpick = [&](const BLoc& lc, double tgt) -> BPick {
+                BPick pk;
+                pk.key = 0;
+                pk.cnt_in = pk.fix_in = pk.fix = 0;
+                pk.f64_in = pk.f64 = 0.0;
+                if (lc.set_j < 0) return pk;
+                const int b2 = lc.set_j * NBIN + (lc.id & 0xFF);
+                const int nb = (int)s.fc[b2];
+                const int st0 = bin_start(b2);
+                if (nb <= WAVE) {
+                  const int L = lane_id();
+                  u64 e1[1] = {L < nb ? bk[ord[st0 + L]] : (u64)0};
+                  wave_sort_desc<1>(e1);
+                  const u64 kk = e1[0];
+                  const bool mem = L < nb;
+                  u64 fx = 0;
+                  double pr = 0.0;
+                  if (mem) pr = mass(key_value(kk) / tt, &fx);
+                  const u64 inc = wave_scan(fx);
+                  const double incf = wave_scan(pr);
+                  const unsigned long long hb = __ballot(mem & ((double)inc >= tgt));
+                  const int ln = hb ? __ffsll((long long)hb) - 1 : (nb > 0 ? nb - 1 : 0);
+                  if (nb > 0) {
+                    pk.key = lane_bcast(kk, ln);
+                    pk.fix = lane_bcast(fx, ln);
+                    pk.fix_in = lane_bcast(inc - fx, ln);
+                    pk.f64 = lane_bcast(pr, ln);
+                    pk.f64_in = lane_bcast(incf - pr, ln);
+                    pk.cnt_in = (u64)ln;
+                  }
+                  return pk;
+                }
+                // many members (long runs of tied values): mass-weighted radix select on the 64-bit keys
+                u64 prefix = 0;
+                int shift = 56;
+                for (;;) {
+                  if (t < NBIN) {
+                    s.rc[t] = 0;
+                    s.rfix[t] = 0;
+                    s.rf64[t] = 0.0;
+                    s.rmk[t] = 0;
+                  }
+                  __syncthreads();
+                  for (int q = t; q < nb; q += SNT) {
+                    const u64 kk = bk[ord[st0 + q]];
+                    if (prefix_match(kk, shift, prefix)) {
+                      u64 fx;
+                      const double pr = mass(key_value(kk) / tt, &fx);
+                      const int d = (int)((kk >> shift) & 0xFF);
+                      atomicAdd(&s.rc[d], 1u);
+                      atomicAdd(&s.rfix[d], fx);
+                      unsafeAtomicAdd(&s.rf64[d], pr);
+                      atomicMax(&s.rmk[d], kk);
+                    }
+                  }
+                  __syncthreads();
+                  const ScanOut o = scan256(s, s.rc, s.rfix, s.rf64, s.rmk, false, tgt - (double)pk.fix_in);
+                  pk.cnt_in += o.cnt_before;
+                  pk.fix_in += o.fix_before;
+                  pk.f64_in += o.f64_before;
+                  if (o.cnt <= 1 || shift == 0) {
+                    pk.key = o.mk;
+                    pk.fix = o.fix;
+                    pk.f64 = o.f64;
+                    break;
+                  }
+                  prefix = (prefix << 8) | (u64)o.digit;
+                  shift -= 8;
+                }
+                return pk;
+              };
+              uint32_t flags = VS_OUT_COOP | VS_OUT_GATHER;
+              int keep = total;
+              u64 zfix = Sfix;
+              double zf = Sf;
+              bool good = true;
+              if (has_tp) {  // sampler.py:145-148
+                const BLoc lp_ = blocate(tgt_p);
+                good = lp_.set_j >= 0;
+                const BPick pp = bpick(lp_, tgt_p - (double)lp_.fix_before);
+                keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
+                zfix = lp_.fix_before + pp.fix_in + pp.fix;
+                zf = zfix_only ? (double)zfix * inv_scale : lp_.f64_before + pp.f64_in + pp.f64;
+                const double tol = 1e-6 * (double)Sfix;
+                if (fabs((double)(zfix - pp.fix) - tgt_p) < tol || fabs((double)zfix - tgt_p) < tol)
+                  flags |= VS_OUT_TOPP_BOUNDARY;
+              }
+              // sampler.py:153-156
+              const double tgt_d = P.u * (double)zfix;
+              const BLoc ld = blocate(tgt_d);
+              good = good && ld.set_j >= 0;
+              const BPick pd = bpick(ld, tgt_d - (double)ld.fix_before);
+              const float d = key_value(pd.key) / tt - xs0;
+              const double before = (double)(ld.fix_before + pd.fix_in);
+              const double tol = 1e-6 * (double)zfix;
+              if (fabs(before - tgt_d) < tol || fabs(before + (double)pd.fix - tgt_d) < tol)
+                flags |= VS_OUT_DRAW_BOUNDARY;
+              // The draw range and the top-p bin are in the gathered set by construction (their coarse bins were
+              // selected from bounds on z); a miss would be a defect, reported as an invalid row.
+              fin.token = (int32_t)key_index(pd.key);
+              fin.lp = (float)((double)d - log(zf));
+              fin.keep = keep;
+              fin.flags = good && pd.key != 0 ? flags : VS_OUT_TIMEOUT;
+              VS_TR(A, 8);
+              if (t < WAVE) write_out(A, row, fin, st, rng_next);  // every wave holds the same answer
+              __syncthreads();
+              cleanup(slot);
+              VS_TR_FLUSH(A);
+              return;
             } else {
               // ---- value-bin pass 2: fine histograms of the selected coarse bins ----
               for (int i = t; i < NSET * NBIN; i += SNT) {
@@ -2266,7 +2647,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             FOR_KEPT({
               u64 kk;
               float xs;
-              if (keep_xs(x, e, kk, xs)) {
+              if (keep_xs(x, e, kk, xs, std::false_type{})) {
                 u64 fx;
                 const double pr = mass(xs, &fx);
                 hist_add(s, kk, 56, fx, pr);
@@ -2325,7 +2706,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   FOR_KEPT({
                     u64 kk;
                     float xs;
-                    if (keep_xs(x, e, kk, xs) && (kk >> (shift + 8)) == prefix) {
+                    if (keep_xs(x, e, kk, xs, std::false_type{}) && (kk >> (shift + 8)) == prefix) {
                       u64 fx;
                       const double pr = mass(xs, &fx);
                       hist_add(s, kk, shift, fx, pr);
@@ -2370,7 +2751,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 FOR_KEPT({
                   u64 kk;
                   float xs;
-                  if (keep_xs(x, e, kk, xs)) {
+                  if (keep_xs(x, e, kk, xs, std::false_type{})) {
                     u64 fx;
                     const double pr = mass(xs, &fx);
                     if (!(pr / Sf < pthr)) {
@@ -2533,6 +2914,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   const bool coop = use_cooperative();
   a.spin_limit = (g_spin_limit && !coop) ? g_spin_limit : 1u << 21;
   a.fix_scale = ldexp(1.0, 63 - bits);
+  a.fix_shift = 63 - bits;
   a.zspan_max = (63 - bits) * 0.6931471805599453 - 13.815510557964274;  // ln(fix_scale) - ln(1e6)
   a.params = list_k > 0 ? nullptr : params;
   a.list_k = list_k;

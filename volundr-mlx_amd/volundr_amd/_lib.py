@@ -75,7 +75,7 @@ def load():
     L.vs_lmhead_verify_greedy.restype = i32
     L.vs_lmhead_workspace_bytes.argtypes = [i32, i32]
     L.vs_lmhead_workspace_bytes.restype = sz
-    L.vs_launch_floor.argtypes = [i32, i32, sz, vp]
+    L.vs_launch_floor.argtypes = [i32, i32, sz, i32, vp]
     L.vs_launch_floor.restype = i32
     L.vs_set_cooperative.argtypes = [i32]
     L.vs_set_cooperative.restype = i32
