@@ -1,6 +1,6 @@
 // vs_lmhead.hip - the bf16 lm_head GEMM with the greedy-verify epilogue fused in, for gfx950: logits are never
 // written to HBM; each workgroup reduces its slice of the vocabulary to per-position (first-max key, max, sum-exp)
-// partials and a second small launch merges them into argmax, accept length and logprob.
+// partials, and the last workgroup to finish merges them into argmax, accept length and logprob.
 //
 // Reference: logits = lm_head(h) in bf16 (volundr-mlx/volundr.py:958-968, bf16 weight [vocab_size, hidden]; spec
 // verify's head call, spec/verify.py:223), then tok = argmax(logits[:, :vv]) and nacc = sum(cumprod(inp[1:] ==
@@ -34,15 +34,23 @@ constexpr int LNW = LNT / WAVE;     // waves per workgroup
 constexpr int KS = 32;              // k per MFMA
 constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
 constexpr int LPMAX = 2048;         // workgroups per launch
+constexpr size_t LWS_HEAD = 256;    // workspace head: the arrival counter (zero between calls)
+constexpr int LMPW = 4;             // positions one wave of the merging workgroup reduces at a time
 
-struct LPart {
-  u64 amkey;
-  float mf;
-  uint32_t pad;
-  double se;
-  u64 pad2;
+// Workgroup partials, position-major and one array per field ([R][P] each), so that the merge's lanes, which walk
+// the workgroups of one position, read consecutive words: (first-max key, float64 sum-exp, float32 max).
+struct LParts {
+  u64* amkey;
+  double* se;
+  float* mf;
 };
-static_assert(sizeof(LPart) == 32, "LPart layout");
+__device__ __forceinline__ LParts lparts(char* ws, int R) {
+  LParts q;
+  q.amkey = (u64*)(ws + LWS_HEAD);
+  q.se = (double*)(q.amkey + (size_t)R * LPMAX);
+  q.mf = (float*)(q.se + (size_t)R * LPMAX);
+  return q;
+}
 
 struct LHArgs {
   const uint16_t* h;  // [R, ldh] bf16
@@ -50,13 +58,14 @@ struct LHArgs {
   const uint16_t* W;  // [N, ldw] bf16
   int64_t ldw;
   int N, vv, K, B, T, R, ntiles;
+  int merge_in;  // the last workgroup merges the partials (else vs_lmhead_merge_kernel does, one per position)
   const int32_t* drafts;  // [B, T-1]
   int32_t* out_argmax;    // [R]
   int32_t* out_accept;    // [B]
   float* out_lp;          // [R] or null
   uint16_t* out_logits;   // [R, ldo] bf16 or null
   int64_t ldo;
-  char* ws;  // LPart [P][R]: the workgroup partials
+  char* ws;  // [LWS_HEAD bytes: the arrival counters] then the workgroup partials (LParts)
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
@@ -97,11 +106,16 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   const int nchunks = K / KC;
   const int t0 = (int)((long long)wg * A.ntiles / P), t1 = (int)((long long)(wg + 1) * A.ntiles / P);
   const int rounds = (t1 - t0 + LNW * NTW - 1) / (LNW * NTW);
-  LPart* parts = (LPart*)A.ws;
+  uint32_t* arrivals = (uint32_t*)A.ws;
+  const LParts parts = lparts(A.ws, A.R);
+  __shared__ uint32_t last_flag;
   VS_TR_DECL(A);
   VS_TR(A, 0);
-  // accept lengths start at T-1 (every draft accepted); the merge kernel lowers them to the first mismatch
-  if (wg == 0 && t < A.B) A.out_accept[t] = A.T - 1;
+  // accept lengths start at T-1 (every draft accepted); the merge lowers them to the first mismatch. A coherent
+  // store: the merging workgroup may run on another XCD, and workgroup 0 arrives (after waiting for this store)
+  // before the merge starts.
+  if (wg == 0)
+    for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
 
   // padded positions R..RP-1 read as zeros in both buffers
   {
@@ -329,18 +343,115 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       k = rk[w][t] > k ? rk[w][t] : k;
       lse_merge(m, s, rm[w][t], rs[w][t]);
     }
-    LPart* pp = parts + (size_t)wg * R + t;
-    st_dev(&pp->amkey, k);
-    st_dev(&pp->mf, m);
-    st_dev(&pp->se, s);
+    const size_t ix = (size_t)t * LPMAX + wg;
+    st_dev(&parts.amkey[ix], k);
+    st_dev(&parts.mf[ix], m);
+    st_dev(&parts.se[ix], s);
   }
   VS_TR(A, 20);
+  if (!A.merge_in) {
+    VS_TR_FLUSH(A);
+    return;
+  }
+  // The last workgroup to arrive merges every position's P partials (no second launch): wave w takes positions
+  // w, w + LNW, ..., LMPW of them at a time, each lane P / 64 partials of each, every load in flight at once;
+  // first-max argmax, logprob, and the accept length as the first mismatching draft position
+  // (specdec.py:327: nacc = the leading matches).
+  // Arrival in two levels, so that no counter takes more than P / 8 + 8 atomics (hundreds of same-address atomics
+  // from every CU serialise at the coherent level): the workgroups of one XCD (blockIdx % 8) count on their own
+  // counter, the last of each XCD on the top counter.
+  {
+    const int xcd = wg & 7;
+    const uint32_t nx = (uint32_t)((P - xcd + 7) / 8);  // workgroups of this XCD
+    if (block_arrive(arrivals + 1 + xcd, &last_flag) != nx - 1) {
+      VS_TR_FLUSH(A);
+      return;
+    }
+    const uint32_t nlevels = (uint32_t)(P < 8 ? P : 8);
+    if (block_arrive(arrivals, &last_flag) != nlevels - 1) {
+      VS_TR_FLUSH(A);
+      return;
+    }
+  }
+  VS_TR(A, 21);
+  constexpr int LPL = LPMAX / WAVE;  // partials per lane at most
+  for (int p0 = wv; p0 < R; p0 += LNW * LMPW) {
+    u64 kk[LMPW][LPL / 8];
+    float mm[LMPW][LPL / 8];
+    double ss[LMPW][LPL / 8];
+    const int per = (P + WAVE - 1) / WAVE;  // partials per lane
+    // up to LPL / 8 = 4 partials per lane are held per position (P <= 256 here; larger P loops below)
+    u64 kb[LMPW];
+    float mb[LMPW];
+    double sb[LMPW];
+#pragma unroll
+    for (int q = 0; q < LMPW; ++q) {
+      kb[q] = 0;
+      mb[q] = -__builtin_inff();
+      sb[q] = 0.0;
+    }
+    for (int u0 = 0; u0 < per; u0 += LPL / 8) {
+#pragma unroll
+      for (int q = 0; q < LMPW; ++q) {
+        const int pos = p0 + q * LNW;
+#pragma unroll
+        for (int u = 0; u < LPL / 8; ++u) {
+          const int i = (u0 + u) * WAVE + ln;
+          const bool in = pos < R && u0 + u < per && i < P;
+          // unconditional loads from a clamped (valid) address, masked afterwards: a coherent load cannot be
+          // speculated, so a guarded one would become a branch and serialise the round trips
+          const size_t ix = (size_t)(pos < R ? pos : 0) * LPMAX + (in ? i : 0);
+          const u64 k0 = ld_dev(&parts.amkey[ix]);
+          const float m0 = ld_dev(&parts.mf[ix]);
+          const double s0 = ld_dev(&parts.se[ix]);
+          kk[q][u] = in ? k0 : (u64)0;
+          mm[q][u] = in ? m0 : -__builtin_inff();
+          ss[q][u] = in ? s0 : 0.0;
+        }
+      }
+      // the row maximum first (one wave max), then every partial sum rescaled to it once: no pairwise merges
+#pragma unroll
+      for (int q = 0; q < LMPW; ++q) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int u = 0; u < LPL / 8; ++u) {
+          kb[q] = kk[q][u] > kb[q] ? kk[q][u] : kb[q];
+          mx = mm[q][u] > mx ? mm[q][u] : mx;
+        }
+        mx = wave_max(mx);
+        const float mt = mx > mb[q] ? mx : mb[q];  // the running maximum over the batches of partials
+        double acc = sb[q] > 0.0 && is_finite(mt) ? sb[q] * (double)expf(mb[q] - mt) : 0.0;
+#pragma unroll
+        for (int u = 0; u < LPL / 8; ++u)
+          acc += (ss[q][u] > 0.0 && is_finite(mt)) ? ss[q][u] * (double)expf(mm[q][u] - mt) : 0.0;
+        mb[q] = mt;
+        sb[q] = acc;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < LMPW; ++q) {
+      const int pos = p0 + q * LNW;
+      const u64 k = wave_max(kb[q]);
+      const float m = mb[q];  // already the same in every lane
+      const double sm = wave_sum(sb[q]);
+      if (ln == 0 && pos < R) {
+        const float xj = am_is_nan(k) ? __builtin_nanf("") : key_value(k);
+        const int32_t tok = (int32_t)key_index(k);
+        A.out_argmax[pos] = tok;
+        if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && sm > 0.0) ? (float)((double)xj - ((double)m + log(sm))) : 0.0f;
+        const int b = pos / A.T, tp = pos % A.T;
+        if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
+      }
+    }
+  }
+  if (t < 9) st_dev(arrivals + t, 0u);  // zero again for the next call on this workspace
+  VS_TR(A, 22);
   VS_TR_FLUSH(A);
 }
 
-// Merge of the P workgroup partials of each position (one 256-thread workgroup per position; a separate launch so
-// the positions merge in parallel on as many CUs): first-max argmax, logprob, and the accept length as the lowest
-// mismatching draft position (specdec.py:327: nacc = leading matches), by atomicMin into out_accept.
+
+// Merge for many positions (a separate launch, one 256-thread workgroup per position, so that the positions merge
+// in parallel on as many CUs): the position's P partials, the maximum first, then each sum rescaled to it once.
 constexpr int MNT = 256;
 constexpr int MPT = LPMAX / MNT;  // partials per thread at most
 __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
@@ -348,65 +459,72 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
   __shared__ float rm[MNT / WAVE];
   __shared__ double rs[MNT / WAVE];
   const int pos = blockIdx.x, t = threadIdx.x, wv = t / WAVE, ln = lane_id();
-  const LPart* parts = (const LPart*)A.ws;
+  const LParts parts = lparts(A.ws, A.R);
   u64 kk[MPT];
   float mm[MPT];
   double ss[MPT];
 #pragma unroll
-  for (int u = 0; u < MPT; ++u) {  // every load issued before the first is used
+  for (int u = 0; u < MPT; ++u) {  // every load issued before the first is used (clamped, masked below)
     const int i0 = u * MNT + t;
-    const int i = i0 < P ? i0 : P - 1;
-    const LPart* pp = parts + (size_t)i * A.R + pos;
-    kk[u] = ld_dev(&pp->amkey);  // device-coherent reads of the other workgroups' partials
-    mm[u] = ld_dev(&pp->mf);
-    ss[u] = ld_dev(&pp->se);
+    const size_t ix = (size_t)pos * LPMAX + (i0 < P ? i0 : P - 1);
+    kk[u] = ld_dev(&parts.amkey[ix]);
+    mm[u] = ld_dev(&parts.mf[ix]);
+    ss[u] = ld_dev(&parts.se[ix]);
   }
   u64 k = 0;
   float m = -__builtin_inff();
-  double s = 0.0;
 #pragma unroll
   for (int u = 0; u < MPT; ++u) {
-    if (u * MNT + t < P) {
-      k = kk[u] > k ? kk[u] : k;
-      lse_merge(m, s, mm[u], ss[u]);
-    }
+    const bool in = u * MNT + t < P;
+    k = (in && kk[u] > k) ? kk[u] : k;
+    m = (in && mm[u] > m) ? mm[u] : m;
   }
   k = wave_max(k);
-#pragma unroll
-  for (int sh = 1; sh < WAVE; sh *= 2) {
-    const float om = lane_xor_rt(m, sh);
-    const double os = lane_xor_rt(s, sh);
-    lse_merge(m, s, om, os);
-  }
+  m = wave_max(m);
   if (ln == 0) {
     rk[wv] = k;
     rm[wv] = m;
-    rs[wv] = s;
   }
   __syncthreads();
-  if (t == 0) {
 #pragma unroll
-    for (int w = 1; w < MNT / WAVE; ++w) {
-      k = rk[w] > k ? rk[w] : k;
-      lse_merge(m, s, rm[w], rs[w]);
-    }
+  for (int w = 0; w < MNT / WAVE; ++w) {
+    k = rk[w] > k ? rk[w] : k;
+    m = rm[w] > m ? rm[w] : m;
+  }
+  double sm = 0.0;
+#pragma unroll
+  for (int u = 0; u < MPT; ++u)
+    sm += (u * MNT + t < P && ss[u] > 0.0 && is_finite(m)) ? ss[u] * (double)expf(mm[u] - m) : 0.0;
+  sm = wave_sum(sm);
+  if (ln == 0) rs[wv] = sm;
+  __syncthreads();
+  if (t == 0) {
+    sm = 0.0;
+#pragma unroll
+    for (int w = 0; w < MNT / WAVE; ++w) sm += rs[w];
     const float xj = am_is_nan(k) ? __builtin_nanf("") : key_value(k);
     const int32_t tok = (int32_t)key_index(k);
     A.out_argmax[pos] = tok;
-    if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && s > 0.0) ? (float)((double)xj - ((double)m + log(s))) : 0.0f;
+    if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && sm > 0.0) ? (float)((double)xj - ((double)m + log(sm))) : 0.0f;
     const int b = pos / A.T, tp = pos % A.T;
     if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
   }
 }
+
+// Positions up to which the last workgroup merges them itself (beyond, the merge's serial work in one workgroup
+// outweighs a second launch).
+constexpr int LMERGE_IN = 32;
 
 template <int NTT, int NTW, int KC>
 static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
   hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW, KC>), dim3(P), dim3(LNT), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "vs_lmhead_verify_greedy: launch");
-  hipLaunchKernelGGL(vs_lmhead_merge_kernel, dim3(a.R), dim3(MNT), 0, stream, a, P);
-  e = hipGetLastError();
-  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_verify_greedy: launch");
+  if (!a.merge_in) {
+    hipLaunchKernelGGL(vs_lmhead_merge_kernel, dim3(a.R), dim3(MNT), 0, stream, a, P);
+    e = hipGetLastError();
+  }
+  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_verify_greedy: merge launch");
 }
 
 }  // namespace vs
@@ -415,7 +533,7 @@ using namespace vs;
 
 extern "C" size_t vs_lmhead_workspace_bytes(int B, int T) {
   const size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
-  return sizeof(LPart) * (size_t)LPMAX * R;
+  return LWS_HEAD + (size_t)(8 + 8 + 4) * LPMAX * R;
 }
 
 extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K,
@@ -455,6 +573,7 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   a.T = T;
   a.R = (int)R;
   a.ntiles = (N + 15) / 16;
+  a.merge_in = R <= LMERGE_IN;
   a.drafts = drafts;
   a.out_argmax = out_argmax;
   a.out_accept = out_accept;
