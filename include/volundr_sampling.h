@@ -104,7 +104,7 @@ int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, con
 size_t vs_sample_workspace_bytes(int B, int V);
 
 /* vs_sample_batch without a workspace argument and without any allocation: the kernels use a fixed device array
- * of vs_sample_noalloc_scratch_bytes() bytes (about 19.8 MB) in the library, one per device, kept until the process
+ * of vs_sample_noalloc_scratch_bytes() bytes (about 22.4 MB) in the library, one per device, kept until the process
  * ends. It covers every batch size (batches above 64 rows run as consecutive launches that reuse it); a shape whose
  * workspace would exceed it fails with VS_EWORKSPACE. The first call on a device looks the array up and zeroes it
  * (a fill kernel on `stream`); every call leaves it zeroed. All calls on one device share the array: calls that

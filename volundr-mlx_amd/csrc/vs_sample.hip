@@ -2978,7 +2978,7 @@ extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V
 // Allocation-free entry point: the workspace is a file-scope device array instead of a caller buffer
 // =================================================================================================================
 // One workspace of RPL_MAX rows covers every launch (larger batches run in launches of at most RPL_MAX rows that
-// reuse it), so the array has a fixed size of RPL_MAX * ROW_WS bytes (about 19.8 MB) per device, held until the
+// reuse it), so the array has a fixed size of RPL_MAX * ROW_WS bytes (about 22.4 MB) per device, held until the
 // process ends. The kernels leave it zeroed after every call; it is zeroed once per device at its first use.
 namespace {
 constexpr size_t SCRATCH_BYTES = (size_t)RPL_MAX * ROW_WS;
