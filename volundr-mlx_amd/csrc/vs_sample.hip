@@ -1909,11 +1909,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #endif
           return cnt;
         };
-        const bool unit_t = tt == 1.0f;
-        const int cbr = zfix_only ? (unit_t ? pass1(std::false_type{}, std::true_type{})
-                                            : pass1(std::false_type{}, std::false_type{}))
-                                  : (unit_t ? pass1(std::true_type{}, std::true_type{})
-                                            : pass1(std::true_type{}, std::false_type{}));
+        const int cbr = zfix_only ? pass1(std::false_type{}, std::false_type{}) : pass1(std::true_type{}, std::false_type{});
         int cb;
         if (few) {
           __syncthreads();
