@@ -210,6 +210,13 @@ size_t vs_draft_workspace_bytes(int n, int S, int V);
  * single-threaded host code). */
 int vs_set_spin_limit(unsigned polls);
 
+/* Testing flags for later calls of the process (0 restores the default behaviour). VS_DEBUG_FORCE_RADIX: rows of
+ * the FULL class (top-k off or above 256) with large kept sets resolve top-p and the draw with the cooperative radix
+ * select, the fallback otherwise reached only with min-p or with value bins too full to refine. No counterpart in
+ * the reference. */
+enum { VS_DEBUG_FORCE_RADIX = 1u };
+int vs_set_debug(unsigned flags);
+
 /* on != 0: later sampling calls of the process launch cooperatively (every workgroup of the grid resident at once,
  * so a row barrier cannot starve when other streams hold CUs; ~18 us more per call); 0: plain launches (the
  * default, unless the environment sets VS_COOPERATIVE=1). The Python layer uses it to retry a call whose rows

@@ -13,6 +13,7 @@ static thread_local std::string g_err;
 unsigned long long* g_trace = nullptr;
 unsigned g_spin_limit = 0;
 int g_cooperative = 0;
+unsigned g_debug = 0;
 
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(int code, const std::string& msg) {
@@ -69,6 +70,11 @@ int vs_version(void) { return 6; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;
+  return VS_OK;
+}
+
+int vs_set_debug(unsigned flags) {
+  vs::g_debug = flags;
   return VS_OK;
 }
 

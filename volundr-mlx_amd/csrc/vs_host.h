@@ -23,6 +23,8 @@ const DevInfo* dev_info();
 extern unsigned g_spin_limit;
 // Non-zero: sampling kernels are launched cooperatively (set by vs_set_cooperative).
 extern int g_cooperative;
+// VS_DEBUG_* testing flags (set by vs_set_debug).
+extern unsigned g_debug;
 
 // Phase-timestamp buffer of development builds (VS_TRACE); always null in the shipped library.
 extern unsigned long long* g_trace;

@@ -114,6 +114,7 @@ struct SampleArgs {
   int kcap;    // candidate-list capacity per workgroup (a power of two)
   int kmax;    // largest top_k of the TOPK class for this launch
   uint32_t spin_limit;
+  uint32_t debug;  // VS_DEBUG_* testing flags (vs_set_debug)
   double fix_scale;  // probability -> fixed point (2^fix_shift)
   int fix_shift;
   double zspan_max;     // ln(fix_scale) - ln(1e6): the kept-value span up to which z comes from fixed point
@@ -1987,7 +1988,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               fin = wave_sample(s, s.tk, total, P);
               fin.flags |= VS_OUT_GATHER;
             }
-          } else if (P.min_p > 0.0) {
+          } else if (P.min_p > 0.0 || (A.debug & VS_DEBUG_FORCE_RADIX)) {
             radix = true;  // min-p on a large kept set: the radix path below handles it
           } else {
             // ---- large kept set: locate the top-p and draw positions by value bins ----
@@ -2909,6 +2910,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   // a row is resident, so its waits keep the default bound.
   const bool coop = use_cooperative();
   a.spin_limit = (g_spin_limit && !coop) ? g_spin_limit : 1u << 21;
+  a.debug = g_debug;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.fix_shift = 63 - bits;
   a.zspan_max = (63 - bits) * 0.6931471805599453 - 13.815510557964274;  // ln(fix_scale) - ln(1e6)

@@ -24,6 +24,7 @@ OUT_COOP = 1 << 5
 OUT_GATHER = 1 << 6
 OUT_HIST_FULL = 1 << 7
 OUT_TIMEOUT = 1 << 31
+DEBUG_FORCE_RADIX = 1
 
 # vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([
@@ -44,7 +45,7 @@ ABI_VERSION = 6
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
-           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_set_cooperative")
+           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_set_cooperative", "vs_set_debug")
 
 _lib = None
 
@@ -77,6 +78,8 @@ def load():
     L.vs_lmhead_workspace_bytes.restype = sz
     L.vs_launch_floor.argtypes = [i32, i32, sz, i32, vp]
     L.vs_launch_floor.restype = i32
+    L.vs_set_debug.argtypes = [ctypes.c_uint]
+    L.vs_set_debug.restype = i32
     L.vs_set_cooperative.argtypes = [i32]
     L.vs_set_cooperative.restype = i32
     L.vs_set_spin_limit.argtypes = [ctypes.c_uint]
