@@ -86,7 +86,7 @@ def test_fixed_point_normaliser_within_5e7(bits):
         d = -rng.uniform(0, span, size=n)
         d[0] = 0.0  # the row maximum: mass exactly 1
         pr = np.exp(d.astype(np.float32)).astype(np.float64)  # masses as the kernel computes them (float32 exp)
-        fx = np.floor(pr * scale + 0.5).astype(np.uint64)
+        fx = np.rint(pr * scale).astype(np.uint64)
         # every prefix (the top-p cut and the draw use prefixes in descending order)
         order = np.argsort(-pr, kind="stable")
         cf = np.cumsum(pr[order])
@@ -112,26 +112,23 @@ def test_truncated_bound_is_close():
 
 
 def fixed_mass(e, S):
-    """The kernel's integer form of round(e * 2^S) from the bits of a float32 0 <= e <= 1 (vs_sample.hip
-    fixed_mass)."""
-    b = int(np.array([e], np.float32).view(np.uint32)[0])
-    E = b >> 23
-    m = (b & 0x7FFFFF) | 0x800000
-    k = E - 150 + S
-    if E == 0:
-        return 0
-    if k >= 0:
-        return m << k
-    r = -k
-    return 0 if r >= 25 else (m + (1 << (r - 1))) >> r
+    """The kernel's float32 form of round-to-nearest-even(e * 2^S) for a float32 0 <= e <= 1 (vs_sample.hip
+    fixed_mass): the part at and above 2^32, truncated, and the exact rest below it, rounded."""
+    f = np.float32
+    e = f(e)
+    h = np.trunc(e * f(2.0 ** (S - 32)))
+    r = f(np.float64(e * f(2.0 ** S)) - np.float64(h) * 2.0 ** 32)  # the fma: one rounding of the exact value
+    assert np.float64(r) == np.float64(e) * 2.0 ** S - np.float64(h) * 2.0 ** 32  # the rest is exact
+    return (int(h) << 32) | int(np.rint(r))
 
 
-@pytest.mark.parametrize("S", [29, 38, 45, 46])
+@pytest.mark.parametrize("S", [29, 38, 45, 46, 56, 62])
 def test_fixed_mass_matches_float64_rounding(S):
     rng = np.random.default_rng(S)
     es = np.concatenate([np.exp(-rng.random(4000) * 60).astype(np.float32),
-                         np.array([0.0, 1.0, 0.5, 2.0 ** -S, 2.0 ** -(S + 1), 3 * 2.0 ** -(S + 2), 1e-30],
+                         np.array([0.0, 1.0, 0.5, 2.0 ** -S, 2.0 ** -(S + 1), 3 * 2.0 ** -(S + 1),
+                                   5 * 2.0 ** -(S + 1), 3 * 2.0 ** -(S + 2), 1e-30, 1e-40, 2.0 ** -24],
                                   np.float32)])
     for e in es:
-        want = int(np.floor(np.float64(e) * 2.0 ** S + 0.5))
+        want = int(np.rint(np.float64(e) * 2.0 ** S))  # ties to even
         assert fixed_mass(float(e), S) == want, (e, S)

@@ -354,6 +354,11 @@ __device__ __forceinline__ void hist_prefix(const uint32_t* hc, const u64* hw, c
   }
 }
 
+// The smallest integer >= t (0 for t <= 0, the largest u64 from 2^64 up).
+__device__ __forceinline__ u64 ceil_u64(double t) {
+  return t <= 0.0 ? (u64)0 : (t >= 18446744073709551616.0 ? ~(u64)0 : (u64)__builtin_ceil(t));
+}
+
 // scan256's answer from prefix arrays (hist_prefix): the first digit in scan order whose bin is non-empty and whose
 // inclusive weight reaches `target` (the last non-empty digit when none does, which only rounding can cause), with
 // the sums before it. Every wave computes it on its own, so no barrier is needed; the caller has synchronised after
@@ -369,10 +374,11 @@ __device__ __forceinline__ ScanOut hist_find(const uint32_t* hc, const u64* hw, 
     c[i] = hc[d];
     w[i] = pw[d];
   }
+  const u64 tg = ceil_u64(target);  // an integer sum reaches target iff it reaches ceil(target)
   int hit = 4, last = -1;
 #pragma unroll
   for (int i = 3; i >= 0; --i) {
-    hit = (c[i] > 0 && (double)w[i] >= target) ? i : hit;
+    hit = (c[i] > 0 && w[i] >= tg) ? i : hit;
     last = (last < 0 && c[i] > 0) ? i : last;
   }
   const unsigned long long hb = __ballot(hit < 4);
@@ -837,22 +843,14 @@ __device__ __forceinline__ void write_out(const SampleArgs& A, int row, const Fi
   }
 }
 
-// round(e * 2^S) for a float 0 <= e <= 1 and 0 < S <= 63 - 24 (half-way cases rounded up), from the bits of e:
-// e = m * 2^(E - 150) with a 24-bit m, so the product is m shifted by k = E - 150 + S, exact when k >= 0. Equal to
-// (u64)((double)e * 2^S + 0.5), without the float64 work.
-__device__ __forceinline__ u64 fixed_mass(float e, int S) {
-  const uint32_t b = __float_as_uint(e);
-  const int E = (int)(b >> 23);
-  const uint32_t m = (b & 0x7FFFFFu) | 0x800000u;
-  const int k = E - 150 + S;
-  // both candidates computed, then selected (no branch): k >= 0 shifts left exactly; 1 <= -k <= 31 rounds the
-  // right shift (half-way up), and m >> 25.. is 0 anyway, which the clamp to 31 keeps
-  const int kl = k > 0 ? k : 0;
-  const int r = k < 0 ? (-k < 31 ? -k : 31) : 1;
-  const u64 up = (u64)m << kl;
-  const uint32_t dn = (m + (1u << (r - 1))) >> r;
-  const u64 v = k >= 0 ? up : (u64)dn;
-  return E == 0 ? (u64)0 : v;
+// round(e * 2^S) to the nearest integer, ties to even, for a float 0 <= e <= 1 and 0 < S <= 63, in float
+// arithmetic (sh = 2^(S - 32), sc = 2^S): h = trunc(e * sh) is the part of e * 2^S at and above 2^32 (an integral
+// float, exact), and e * sc - h * 2^32 is the rest, exact because it is e's mantissa without its top bits. A rest
+// with a fraction is below 2^24, so its rounding cannot carry into h. Equal to rint((double)e * 2^S).
+__device__ __forceinline__ u64 fixed_mass(float e, float sh, float sc) {
+  const float h = __builtin_truncf(e * sh);
+  const float r = __builtin_fmaf(-h, 4294967296.0f, e * sc);
+  return ((u64)(uint32_t)h << 32) | (u64)(uint32_t)__builtin_rintf(r);
 }
 
 // e^d for d <= 0 with about 2 ulp relative error: 2^(d log2 e) from the hardware base-2 exponential, with the
@@ -1782,6 +1780,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // to exp(-40)) the passes also keep float64 sums per bin.
         const bool zfix_only = (double)span <= A.zspan_max;
         const double inv_scale = 1.0 / scale;  // a power of two: exact
+        const float fsc = __builtin_amdgcn_ldexpf(1.0f, A.fix_shift), fsh = __builtin_amdgcn_ldexpf(1.0f, A.fix_shift - 32);
         auto fine_of = [&](float xs) -> int {  // xs = x / t
           const float u = xs0 - xs;
           int f = (int)(u * fscale);
@@ -1791,7 +1790,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         auto mass = [&](float xs, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
           const float d = xs - xs0;
           const float e = exp_nonpos(d);
-          *fx = fixed_mass(e, A.fix_shift);  // == (u64)((double)e * scale + 0.5), in integer arithmetic
+          *fx = fixed_mass(e, fsh, fsc);  // == rint((double)e * scale)
           return (double)e;
         };
         VS_TR(A, 4);
@@ -1839,13 +1838,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // With few qualifying lanes the kept logits are also listed in LDS for the gather below; otherwise the
         // kept count exceeds GSMALL and no gather happens.
         const bool few = nq * 4 <= SNT;
-        // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it
-        // and per unit temperature (no division: about a fifth of the work per logit)
+        // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it, and a
+        // third for the dense case at unit temperature without float64 sums (no division: a sixth of its work)
         auto pass1 = [&](auto with_f64, auto unit_t) -> int {
           int cnt = 0;
-#ifdef VS_EXP_DUP_EXP
-          float dup_acc = 0.0f;
-#endif
           if (!few) {
             // Dense case (many qualifying lanes): every position of the chunk, four LDS reads in flight per lane,
             // and no branch per logit: a logit outside the kept set adds nothing (a zero increment to a bin of
@@ -1879,6 +1875,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             }
             return cnt;
           }
+          if constexpr (decltype(unit_t)::value) return cnt;  // only called dense
           FOR_KEPT({
             u64 kk;
             float xs;
@@ -1891,13 +1888,6 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               const int c = fo >> 8;
               atomicAdd(&s.hc[c], 1u);
               atomicAdd(&s.hfix[c], fx);
-#ifdef VS_EXP_DUP_ATOM
-              atomicAdd(&s.rc[c], 1u);
-              atomicAdd(&s.rfix[c], fx);
-#endif
-#ifdef VS_EXP_DUP_EXP
-              dup_acc += expf(xs * 0.5f - xs0);
-#endif
               if constexpr (decltype(with_f64)::value) unsafeAtomicAdd(&s.hf64[c], pr);
               if (few) {
                 const int p = atomicAdd(&s.misc[15], 1);
@@ -1905,12 +1895,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
             }
           })
-#ifdef VS_EXP_DUP_EXP
-          if (dup_acc == 12345.0f) s.rc[t & 255] = 1u;
-#endif
           return cnt;
         };
-        const int cbr = zfix_only ? pass1(std::false_type{}, std::false_type{}) : pass1(std::true_type{}, std::false_type{});
+        const int cbr = !zfix_only ? pass1(std::true_type{}, std::false_type{})
+                        : (!few && tt == 1.0f) ? pass1(std::false_type{}, std::true_type{})
+                                               : pass1(std::false_type{}, std::false_type{});
         int cb;
         if (few) {
           __syncthreads();
@@ -2047,36 +2036,68 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               int sd4[NSET];
 #pragma unroll
               for (int q = 0; q < NSET; ++q) sd4[q] = q < ns ? set[q] : -1;
-              u64* stg = s.tk;  // staging: 2 * KCAP keys (the qualifying-lane list is not read on this path)
               u64* big = (u64*)(rws + OFF_BIG);
-              if (t == 0) {
-                s.misc[16] = 0;
-                s.misc[19] = 0;
-              }
+              if (t == 0) s.misc[16] = 0;
               __syncthreads();
-#define BIG_PRED                                                                                        \
-  ((id != 0xFFFFu) & (((int)(id >> 8) == sd4[0]) | ((int)(id >> 8) == sd4[1]) | ((int)(id >> 8) == sd4[2]) | \
-                      ((int)(id >> 8) == sd4[3])))
-              FOR_FID(BIG_PRED, {
-                const int p = atomicAdd(&s.misc[16], 1);
-                if (p < 2 * KCAP) stg[p] = key64(s.xv[i], (uint32_t)(lo + i));
-              })
-              __syncthreads();
-              const int nloc = s.misc[16];
-              if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
-              __syncthreads();
-              if (nloc) {
-                const int base = s.misc[17];
-                if (nloc <= 2 * KCAP) {
-                  for (int i = t; i < nloc; i += SNT) st_dev(&big[base + i], stg[i]);
-                } else {  // more than the staging area: a second visit stores them directly
-                  FOR_FID(BIG_PRED, {
-                    const int p = atomicAdd(&s.misc[19], 1);
-                    st_dev(&big[base + p], key64(s.xv[i], (uint32_t)(lo + i)));
-                  })
+              {
+                // The selected coarse bins are the draw's digits dhi..dlo and the top-p digit: two ranges of fine-bin
+                // ids [a, a + n), tested on two ids at once with 16-bit vector arithmetic (the difference wraps, so
+                // an id below a is out of range too). n excludes 0xFFFF, the id of a logit outside the kept set.
+                typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+                auto pk = [](uint32_t v) -> u16x2 { return __builtin_bit_cast(u16x2, v); };
+                auto up = [](u16x2 v) -> uint32_t { return __builtin_bit_cast(uint32_t, v); };
+                auto rng = [](int d0, int d1) -> uint32_t {  // (n << 16) | a for the digits d0..d1
+                  return ((uint32_t)(((d1 - d0 + 1) << 8) - (d1 == 255 ? 1 : 0)) << 16) | ((uint32_t)d0 << 8);
+                };
+                const uint32_t r1 = rng(dhi, dlo);
+                const uint32_t r2 = (has_tp && (cpo.digit < dhi || cpo.digit > dlo)) ? rng(cpo.digit, cpo.digit) : 0u;
+                const u16x2 a1 = pk((r1 & 0xFFFFu) * 0x10001u), n1 = pk((r1 >> 16) * 0x10001u);
+                const u16x2 a2 = pk((r2 & 0xFFFFu) * 0x10001u), n2 = pk((r2 >> 16) * 0x10001u);
+                const u16x2 one = pk(0x10001u);
+                static_assert(EPT_MAX * SNT / 8 <= 4 * SNT, "four 16-byte id words per lane cover the chunk");
+                const int n8 = (hi - lo + 7) / 8;
+                const uint4* f4 = (const uint4*)fid;
+                uint4 q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const int w = t + u * SNT;
+                  q[u] = f4[w < n8 ? w : 0];
+                }
+                // bit k (k < 16) / 16 + k: the low / high id of dword k = 4u + j of the lane's words; a half of
+                // x1 | x2 is non-zero for an id in a range, and the saturating 1 - x marks the others
+                uint32_t miss = 0;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const uint32_t wd[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+                  for (int j = 0; j < 4; ++j) {
+                    const u16x2 v = pk(wd[j]);
+                    const uint32_t x1 = up(__builtin_elementwise_min((u16x2)(v - a1), n1)) ^ up(n1);
+                    const uint32_t x2 = up(__builtin_elementwise_min((u16x2)(v - a2), n2)) ^ up(n2);
+                    miss |= up(__builtin_elementwise_sub_sat(one, pk(x1 | x2))) << (4 * u + j);
+                  }
+                  if (t + u * SNT >= n8) miss |= 0x000F000Fu << (4 * u);
+                }
+                uint32_t hm = ~miss;
+                const int nm = __builtin_popcount(hm);
+                const int incl = wave_scan(nm);
+                const int wtot = lane_bcast(incl, WAVE - 1);
+                int wb = 0;
+                if (lane_id() == 0 && wtot) wb = atomicAdd(&s.misc[16], wtot);
+                wb = lane_bcast(wb, 0);
+                __syncthreads();
+                const int nloc = s.misc[16];
+                if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
+                __syncthreads();
+                int p = (nloc ? s.misc[17] : 0) + wb + incl - nm;
+                while (hm) {
+                  const int bt = __builtin_ctz(hm);
+                  hm &= hm - 1;
+                  const int k = bt & 15;
+                  const int i = 8 * (t + (k >> 2) * SNT) + 2 * (k & 3) + (bt >> 4);
+                  st_dev(&big[p++], key64(s.xv[i], (uint32_t)(lo + i)));
                 }
               }
-#undef BIG_PRED
               g0_writes = false;
               VS_TR(A, 6);
               if (!arrive_done()) {
@@ -2110,6 +2131,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   r[u] = i < m ? ld_dev(&big[i]) : (u64)0;
                 }
                 __syncthreads();  // the fine bins are clear
+                VS_TRX(53);
                 auto set_of = [&](int c) -> int { return sd4[1] == c ? 1 : (sd4[2] == c ? 2 : (sd4[3] == c ? 3 : 0)); };
 #pragma unroll
                 for (int u = 0; u < NL; ++u) {
@@ -2131,6 +2153,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               __syncthreads();
               u64* fpc = cpc + 3 * NBIN;  // [NSET][NBIN] each
+              VS_TRX(54);
               u64* fpw = fpc + NSET * NBIN;
               double* fpf = (double*)(fpw + NSET * NBIN);
               {
@@ -2140,6 +2163,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                               fpf + j * NBIN);
               }
               __syncthreads();
+              VS_TRX(55);
               // first position of fine bin b2 in the order array: the sets one after another, each in scan order
               auto bin_start = [&](int b2) -> int {
                 const int j = b2 / NBIN;
@@ -2188,8 +2212,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               };
               // The first member (descending key) of the located fine bin whose cumulative mass inside the bin
               // reaches `tgt` (the bin's last member if none does, which only rounding can cause).
-              // Up to 64 members: every wave computes it on its own (bitonic sort in registers, wave scans and a
-              // ballot), so no barrier is needed. More: the whole workgroup, by a mass-weighted radix select.
+              // Up to 64 members: every wave computes it on its own, so no barrier is needed: lane L holds member L
+              // and sums the masses of the members with larger keys (its rank in the bin; keys are distinct), one
+              // member per trip read with readlane; the pick is the member whose mass crosses tgt, found by a
+              // ballot. More: the whole workgroup, by a mass-weighted radix select.
               auto bpick = [&](const BLoc& lc, double tgt) -> BPick {
                 BPick pk;
                 pk.key = 0;
@@ -2200,26 +2226,45 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 const int nb = (int)s.fc[b2];
                 const int st0 = bin_start(b2);
                 if (nb <= WAVE) {
+                  if (nb == 0) return pk;
                   const int L = lane_id();
-                  u64 e1[1] = {L < nb ? bk[ord[st0 + L]] : (u64)0};
-                  wave_sort_desc<1>(e1);
-                  const u64 kk = e1[0];
                   const bool mem = L < nb;
+                  const u64 kk = mem ? bk[ord[st0 + L]] : (u64)0;
                   u64 fx = 0;
                   double pr = 0.0;
                   if (mem) pr = mass(key_value(kk) / tt, &fx);
-                  const u64 inc = wave_scan(fx);
-                  const double incf = wave_scan(pr);
-                  const unsigned long long hb = __ballot(mem & ((double)inc >= tgt));
-                  const int ln = hb ? __ffsll((long long)hb) - 1 : (nb > 0 ? nb - 1 : 0);
-                  if (nb > 0) {
-                    pk.key = lane_bcast(kk, ln);
-                    pk.fix = lane_bcast(fx, ln);
-                    pk.fix_in = lane_bcast(inc - fx, ln);
-                    pk.f64 = lane_bcast(pr, ln);
-                    pk.f64_in = lane_bcast(incf - pr, ln);
-                    pk.cnt_in = (u64)ln;
+                  u64 ex = 0;  // mass of the larger keys
+                  double exf = 0.0;
+                  int rk = 0;  // their number
+                  if (zfix_only) {
+                    for (int j = 0; j < nb; ++j) {
+                      const bool gt = lane_bcast(kk, j) > kk;
+                      const u64 fj = lane_bcast(fx, j);
+                      ex += gt ? fj : (u64)0;
+                      rk += gt ? 1 : 0;
+                    }
+                  } else {
+                    for (int j = 0; j < nb; ++j) {
+                      const bool gt = lane_bcast(kk, j) > kk;
+                      const u64 fj = lane_bcast(fx, j);
+                      const double pj = lane_bcast(pr, j);
+                      ex += gt ? fj : (u64)0;
+                      exf += gt ? pj : 0.0;
+                      rk += gt ? 1 : 0;
+                    }
                   }
+                  // in descending key order the inclusive sum first reaches tgt at one member: the first one, or
+                  // the one whose exclusive sum is still below it (the last member, rank nb - 1, when none does)
+                  const u64 tg = ceil_u64(tgt);
+                  const unsigned long long hb = __ballot(mem & (ex + fx >= tg) & ((ex < tg) | (rk == 0)));
+                  const unsigned long long lb = __ballot(mem & (rk == nb - 1));
+                  const int ln = hb ? __ffsll((long long)hb) - 1 : __ffsll((long long)lb) - 1;
+                  pk.key = lane_bcast(kk, ln);
+                  pk.fix = lane_bcast(fx, ln);
+                  pk.fix_in = lane_bcast(ex, ln);
+                  pk.f64 = lane_bcast(pr, ln);
+                  pk.f64_in = lane_bcast(exf, ln);
+                  pk.cnt_in = (u64)lane_bcast(rk, ln);
                   return pk;
                 }
                 // many members (long runs of tied values): mass-weighted radix select on the 64-bit keys
@@ -2268,8 +2313,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               bool good = true;
               if (has_tp) {  // sampler.py:145-148
                 const BLoc lp_ = blocate(tgt_p);
+                VS_TRX(56);
                 good = lp_.set_j >= 0;
                 const BPick pp = bpick(lp_, tgt_p - (double)lp_.fix_before);
+                VS_TRX(57);
                 keep = (int)(lp_.cnt_before + pp.cnt_in) + 1;
                 zfix = lp_.fix_before + pp.fix_in + pp.fix;
                 zf = zfix_only ? (double)zfix * inv_scale : lp_.f64_before + pp.f64_in + pp.f64;
@@ -2280,8 +2327,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               // sampler.py:153-156
               const double tgt_d = P.u * (double)zfix;
               const BLoc ld = blocate(tgt_d);
+              VS_TRX(58);
               good = good && ld.set_j >= 0;
               const BPick pd = bpick(ld, tgt_d - (double)ld.fix_before);
+              VS_TRX(59);
               const float d = key_value(pd.key) / tt - xs0;
               const double before = (double)(ld.fix_before + pd.fix_in);
               const double tol = 1e-6 * (double)zfix;
