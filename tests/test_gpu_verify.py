@@ -64,6 +64,43 @@ def test_nonfinite(dev):
     assert o.argmax.cpu().tolist() == [[5, 0, 9]] and o.accept.item() == 2
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_nonfinite_across_workgroups(dev, dtype):
+    """NaN ranks first (np.argmax), +inf beats every finite value, all -inf gives index 0, signed zeros tie (first
+    index wins), and the maximum may sit in the row's last element: positions spread over several workgroups."""
+    V, T = 40000, 8
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((1, T, V)) - 10.0).astype(np.float32)
+    x[0, 0, 100] = 3.0
+    x[0, 0, 30000] = np.nan
+    x[0, 1, 25000] = np.nan
+    x[0, 1, 39000] = np.nan
+    x[0, 2, 35000] = np.inf
+    x[0, 2, 12000] = np.inf
+    x[0, 3, :] = -np.inf
+    x[0, 4, :] = -np.inf
+    x[0, 4, 20000] = 1.5
+    x[0, 5, 500] = -0.0
+    x[0, 5, 300] = 0.0
+    x[0, 6, 200] = -0.0
+    x[0, 6, 800] = 0.0
+    x[0, 7, V - 1] = 6.0
+    xt = torch.from_numpy(x).to(dev).to(dtype)
+    ref_in = xt.float().cpu().numpy()
+    want = np.argmax(ref_in, axis=-1).astype(np.int32)
+    assert want[0].tolist() == [30000, 25000, 12000, 0, 20000, 300, 200, V - 1]
+    drafts = want[:, :-1].copy()
+    print(f"[nonfinite] V={V} T={T} {dtype}", flush=True)
+    o = verify_greedy(xt, torch.from_numpy(drafts).to(dev), V)
+    torch.cuda.synchronize()
+    assert np.array_equal(o.argmax.cpu().numpy(), want)
+    assert o.accept.item() == T - 1
+    _, _, lp = VR.verify(ref_in, drafts, V)
+    g = o.logprobs.cpu().numpy().astype(np.float64)
+    fin = [4, 5, 6, 7]  # finite maximum and no NaN or +inf in the position
+    assert np.all(np.abs(g[0, fin] - lp[0, fin]) <= 1e-5 * np.abs(lp[0, fin]) + 1e-10), (g[0, fin], lp[0, fin])
+
+
 @pytest.mark.parametrize("T", [2, 32, 33, 34, 40])
 def test_accept_lengths_around_the_packed_limit(dev, T):
     """Blocks of up to 33 positions carry the accept information in one packed word, longer ones take the

@@ -45,6 +45,22 @@ struct VerifyArgs {
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
+// v_max3_f32 (a quiet NaN operand is passed over; callers test for NaNs apart), without the canonicalising maxima
+// the compiler adds around fmaxf; v_max3_u32; a packed 16-bit maximum.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t max3u(uint32_t a, uint32_t b, uint32_t c) {
+  const uint32_t m = a > b ? a : b;
+  return m > c ? m : c;
+}
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
 template <int DT>
 struct VTraits;
 template <>
@@ -59,6 +75,15 @@ struct VTraits<VS_F32> {
   }
   __device__ static float get(const uint4& r, int q) { return ((const float*)&r)[q]; }
   __device__ static float one(const void* p, int64_t i) { return ((const float*)p)[i]; }
+  // best = max(best, the four values); mag = max(mag, their magnitude bits); a NaN has magnitude > NAN_MAG
+  static constexpr uint32_t NAN_MAG = 0x7F800000u;
+  __device__ static void max_mag(const uint4& r, float& best, uint32_t& mag) {
+    best = max3f(best, __uint_as_float(r.x), __uint_as_float(r.y));
+    best = max3f(best, __uint_as_float(r.z), __uint_as_float(r.w));
+    mag = max3u(mag, r.x & 0x7FFFFFFFu, r.y & 0x7FFFFFFFu);
+    mag = max3u(mag, r.z & 0x7FFFFFFFu, r.w & 0x7FFFFFFFu);
+  }
+  __device__ static bool has_nan(uint32_t mag) { return mag > NAN_MAG; }
 };
 template <>
 struct VTraits<VS_BF16> {
@@ -79,6 +104,16 @@ struct VTraits<VS_BF16> {
     return __uint_as_float((q & 1) ? (w & 0xFFFF0000u) : (w << 16));
   }
   __device__ static float one(const void* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
+  // as for float32, with the two 16-bit magnitudes of a word kept apart (one packed maximum per word)
+  __device__ static void max_mag(const uint4& r, float& best, uint32_t& mag) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      best = max3f(best, __uint_as_float(w[i] << 16), __uint_as_float(w[i] & 0xFFFF0000u));
+      mag = pk_max_u16(mag, w[i] & 0x7FFF7FFFu);
+    }
+  }
+  __device__ static bool has_nan(uint32_t mag) { return (mag & 0xFFFFu) > 0x7F80u || (mag >> 16) > 0x7F80u; }
 };
 template <>
 struct VTraits<VS_F16> {
@@ -99,6 +134,15 @@ struct VTraits<VS_F16> {
     return f16_to_f32((uint16_t)((q & 1) ? (w >> 16) : (w & 0xFFFFu)));
   }
   __device__ static float one(const void* p, int64_t i) { return f16_to_f32(((const uint16_t*)p)[i]); }
+  __device__ static void max_mag(const uint4& r, float& best, uint32_t& mag) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      best = max3f(best, get(r, 2 * i), get(r, 2 * i + 1));
+      mag = pk_max_u16(mag, w[i] & 0x7FFF7FFFu);
+    }
+  }
+  __device__ static bool has_nan(uint32_t mag) { return (mag & 0xFFFFu) > 0x7C00u || (mag >> 16) > 0x7C00u; }
 };
 
 template <int DT>
@@ -159,31 +203,41 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     VS_TR(A, 5);
 #endif
     // Every element past the chunk now reads -inf, and a lane's elements inside the chunk come first in its (u, q)
-    // order, so no element needs a range test: -inf after a taken element is never taken (strict >), adds nothing
-    // to the sums and is not finite. A lane with no element inside the chunk contributes no key.
+    // order, so no element needs a range test. A lane with no element inside the chunk contributes no key.
+    // np.argmax ranks a NaN first, so the lane's maximum matters only when it holds none: the maximum comes from
+    // three-input max instructions (two elements each; a quiet NaN operand is passed over) and the NaN flag from
+    // the largest magnitude bits, then a backward sweep of equality selects leaves the first index holding the maximum
+    // (with every element -inf, the first element, as np.argmax has it).
     const int base0 = lo + t * VEC;
     const bool any_in = base0 < hi;
-    // Branch-free (selects; & and | on bools: && and || compile to branches). NaN compares as -inf for the first
-    // maximum and only raises a flag; the (rare) first NaN index is found by a second scan. With every element
-    // -inf or NaN the first maximum is the lane's first element, as np.argmax has it.
     float best = -__builtin_inff();
-    int bi = base0;
-    bool anynan = false;
+    uint32_t mag = 0;
 #pragma unroll
     for (int u = 0; u < VNF; ++u) {
       if (u >= A.NV) break;  // uniform: the work scales with the chunk, not with the register budget
+      TR::max_mag(rv[u], best, mag);
+    }
+    const bool anynan = TR::has_nan(mag);
+    int bi = base0;
 #pragma unroll
-      for (int q = 0; q < VEC; ++q) {
-        const float x = TR::get(rv[u], q);
-        const bool isnan = x != x;
-        const float xc = isnan ? -__builtin_inff() : x;
-        const bool take = xc > best;
-        best = take ? xc : best;
-        bi = take ? base0 + u * VNT * VEC + q : bi;
-        anynan = anynan | isnan;
-        m = __builtin_fmaxf(m, is_finite(x) ? x : -__builtin_inff());
+    for (int u = VNF - 1; u >= 0; --u) {
+      if (u >= A.NV) continue;
+#pragma unroll
+      for (int q = VEC - 1; q >= 0; --q) bi = TR::get(rv[u], q) == best ? base0 + u * VNT * VEC + q : bi;
+    }
+    // the finite maximum: the maximum itself unless it is +inf (then a sweep over the finite elements) or NaN
+    if (is_finite(best)) {
+      m = best;
+    } else if (best > 0.0f) {
+#pragma unroll
+      for (int u = 0; u < VNF; ++u) {
+        if (u >= A.NV) break;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const float x = TR::get(rv[u], q);
+          m = __builtin_fmaxf(m, is_finite(x) ? x : -__builtin_inff());
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);  // one vector at a time (hoisting every widening costs VGPRs)
     }
     VS_TR(A, 6);
     int nani = -1;
@@ -208,19 +262,33 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     for (int u = 0; u < VNF; ++u) asm volatile("" : "+v"(rv[u].x), "+v"(rv[u].y), "+v"(rv[u].z), "+v"(rv[u].w));
     if (is_finite(m)) {
       const float L2E = 1.44269504088896340736f;
-      float acc = 0.0f;
+      float acc0 = 0.0f, acc1 = 0.0f;  // two chains of additions
+      if (!anynan & is_finite(best)) {
+        // no NaN and no +inf: a -inf element gives exp2(-inf) = 0 without a test
 #pragma unroll
-      for (int u = 0; u < VNF; ++u) {
-        if (u >= A.NV) break;
+        for (int u = 0; u < VNF; ++u) {
+          if (u >= A.NV) break;
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const float x = TR::get(rv[u], q);
-          const float d = is_finite(x) ? (x - m) * L2E : -__builtin_inff();
-          acc += __builtin_amdgcn_exp2f(d);  // exp2(-inf) = 0: masked terms add nothing, without a branch
-          if (q == VEC - 1) __builtin_amdgcn_sched_barrier(0);
+          for (int q = 0; q < VEC; q += 2) {
+            acc0 += __builtin_amdgcn_exp2f((TR::get(rv[u], q) - m) * L2E);
+            acc1 += __builtin_amdgcn_exp2f((TR::get(rv[u], q + 1) - m) * L2E);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < VNF; ++u) {
+          if (u >= A.NV) break;
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            const float x = TR::get(rv[u], q);
+            const float d = is_finite(x) ? (x - m) * L2E : -__builtin_inff();
+            acc0 += __builtin_amdgcn_exp2f(d);  // exp2(-inf) = 0: masked terms add nothing, without a branch
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      se = (double)acc;
+      se = (double)acc0 + (double)acc1;
     }
   } else {
   // General path (chunks longer than the register budget): one streaming pass with the first-max key, a running
