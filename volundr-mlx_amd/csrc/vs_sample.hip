@@ -1839,7 +1839,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // kept count exceeds GSMALL and no gather happens.
         const bool few = nq * 4 <= SNT;
         // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it, and a
-        // third for the dense case at unit temperature without float64 sums (no division: a sixth of its work)
+        // third for the dense case at unit temperature without float64 sums and without a top-k cut: no division,
+        // and the kept set is x >= xkeep (finite), since x / 1 == x
+        const float xkeep = mode == 2 ? fmaxf(xlb, fminf(xhi, thr)) : fmaxf(xlb, -__FLT_MAX__);
         auto pass1 = [&](auto with_f64, auto unit_t) -> int {
           int cnt = 0;
           if (!few) {
@@ -1860,7 +1862,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 const float x = xq[u];
                 u64 kk;
                 float xs;
-                const bool keep = (i < nel) & (x >= xlb) & keep_xs(x, lo + i, kk, xs, unit_t);
+                bool keep;
+                if constexpr (decltype(unit_t)::value) {  // mode 0 or 2 at unit temperature: one bound, finite
+                  xs = x;
+                  keep = (i < nel) & (x >= xkeep) & (x < __builtin_inff());
+                } else {
+                  keep = (i < nel) & (x >= xlb) & keep_xs(x, lo + i, kk, xs, unit_t);
+                }
                 u64 fx;
                 const double pr = mass(xs, &fx);
                 const int fo = fine_of(xs);
@@ -1898,8 +1906,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           return cnt;
         };
         const int cbr = !zfix_only ? pass1(std::true_type{}, std::false_type{})
-                        : (!few && tt == 1.0f) ? pass1(std::false_type{}, std::true_type{})
-                                               : pass1(std::false_type{}, std::false_type{});
+                        : (!few && tt == 1.0f && mode != 1) ? pass1(std::false_type{}, std::true_type{})
+                                                            : pass1(std::false_type{}, std::false_type{});
         int cb;
         if (few) {
           __syncthreads();
