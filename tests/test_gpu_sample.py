@@ -246,6 +246,20 @@ def test_nonfinite_rows(dev):
     assert out.ids.cpu().tolist() == [0, 7, 100, 0, 2999]
 
 
+def test_full_rows_with_masked_logits(dev):
+    """FULL-class rows over the whole vocabulary with -inf scattered through every workgroup's chunk (masked
+    tokens): lanes holding a non-finite logit take the exact statistics loop, the others the three-input one."""
+    V = 163840
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((3, V)) * 2).astype(np.float32)
+    x[0, ::7] = -np.inf
+    x[1, 100000:] = -np.inf
+    x[2, 1::3] = -np.inf
+    x[2, 5] = np.inf
+    ps = [Sampling(temperature=0.8, top_p=0.9), Sampling(top_p=0.95), Sampling(temperature=1.0, top_p=0.7)]
+    run(dev, x, ps, [0.25, 0.6, 0.9], label="masked full rows")
+
+
 def test_signed_zero_and_ties(dev):
     V = 600
     x = np.zeros((3, V), np.float32)

@@ -129,6 +129,28 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 
+// v_max3_f32 / v_min3_f32 (a quiet NaN operand is passed over: callers test for NaNs apart), without the
+// canonicalising operations the compiler adds around fmaxf / fminf; v_max3_u32; a packed 16-bit maximum.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float min3f(float a, float b, float c) {
+  float r;
+  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ uint32_t max3u(uint32_t a, uint32_t b, uint32_t c) {
+  const uint32_t m = a > b ? a : b;
+  return m > c ? m : c;
+}
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
 template <int CTRL, int ROWM = 0xF, int BANKM = 0xF>
 __device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWM, BANKM, false);

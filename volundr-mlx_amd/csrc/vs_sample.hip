@@ -786,11 +786,10 @@ struct Stats {
   uint32_t mx1, mx2;
   u64 am;
 };
-__device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, u64 am, const Smem& s) {
+__device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, const Smem& s) {
   n = wave_sum(n);
   mx1 = wave_max(mx1);
   mx2 = wave_max(mx2);
-  am = wave_max(am);
   const int w = threadIdx.x / WAVE;
   uint32_t* m1 = (uint32_t*)(s.misc + M_STAT1);
   uint32_t* m2 = (uint32_t*)(s.misc + M_STAT2);
@@ -799,7 +798,6 @@ __device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, 
     s.redi[w] = n;
     m1[w] = mx1;
     m2[w] = mx2;
-    s.red64[w] = am;
   }
   __syncthreads();
   Stats r = {0, 0, 0, 0};
@@ -808,7 +806,6 @@ __device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, 
     r.n += s.redi[i];
     r.mx1 = m1[i] > r.mx1 ? m1[i] : r.mx1;
     r.mx2 = m2[i] > r.mx2 ? m2[i] : r.mx2;
-    r.am = s.red64[i] > r.am ? s.red64[i] : r.am;
   }
   __syncthreads();
   return r;
@@ -1609,19 +1606,44 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   // ---- row statistics: finite count, largest and smallest finite logit, np.argmax key ----
   uint32_t lane_mk = 0;  // ord32 of this lane's largest finite logit, 0 when it has none
   {
-    int nf = 0;
+    // Raw maximum and minimum by three-input instructions (reads past the chunk repeat the lane's first
+    // position, which changes neither) and the largest magnitude bits: a lane whose magnitudes stay
+    // below +inf's holds only finite logits, and its finite count is its position count. A lane with a NaN or an
+    // infinity takes the exact loop.
+    const int nel = hi - lo;
+    const int t0 = t < nel ? t : 0;
     float fmx = -__builtin_inff(), fmn = __builtin_inff();
-    FOR_XV({
-      if (is_finite(x)) {
-        ++nf;
-        fmx = x > fmx ? x : fmx;
-        fmn = x < fmn ? x : fmn;
+    uint32_t mag = 0;
+    {
+      static_assert(EPT_MAX % 2 == 0, "positions are taken in pairs");
+      float xq[EPT_MAX];  // every read in flight at once (CH <= EPT_MAX * SNT)
+      xq[0] = s.xv[t0];
+#pragma unroll
+      for (int u = 1; u < EPT_MAX; ++u) xq[u] = u * SNT < nel ? s.xv[t + u * SNT < nel ? t + u * SNT : t0] : xq[0];
+#pragma unroll
+      for (int u = 0; u < EPT_MAX; u += 2) {
+        fmx = max3f(fmx, xq[u], xq[u + 1]);
+        fmn = min3f(fmn, xq[u], xq[u + 1]);
+        mag = max3u(mag, __float_as_uint(xq[u]) & 0x7FFFFFFFu, __float_as_uint(xq[u + 1]) & 0x7FFFFFFFu);
       }
-    })
+    }
+    int nf = t < nel ? (nel - t + SNT - 1) / SNT : 0;
+    if (mag >= 0x7F800000u) {
+      nf = 0;
+      fmx = -__builtin_inff();
+      fmn = __builtin_inff();
+      FOR_XV({
+        if (is_finite(x)) {
+          ++nf;
+          fmx = x > fmx ? x : fmx;
+          fmn = x < fmn ? x : fmn;
+        }
+      })
+    }
     const uint32_t mk = nf ? ord32(fmx) : 0u, nmk = nf ? ~ord32(fmn) : 0u;
     lane_mk = mk;
     VS_TR(A, 20);
-    Stats st = block_stats(nf, mk, nmk, 0, s);
+    Stats st = block_stats(nf, mk, nmk, s);
     if (st.n == 0) st.am = chunk_amkey();
     VS_TR(A, 21);
     if (t == 0) {

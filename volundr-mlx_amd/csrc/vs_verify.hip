@@ -45,22 +45,6 @@ struct VerifyArgs {
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
-// v_max3_f32 (a quiet NaN operand is passed over; callers test for NaNs apart), without the canonicalising maxima
-// the compiler adds around fmaxf; v_max3_u32; a packed 16-bit maximum.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-__device__ __forceinline__ uint32_t max3u(uint32_t a, uint32_t b, uint32_t c) {
-  const uint32_t m = a > b ? a : b;
-  return m > c ? m : c;
-}
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
-}
-
 template <int DT>
 struct VTraits;
 template <>
