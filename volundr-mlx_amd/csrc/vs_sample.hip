@@ -1277,20 +1277,41 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 
   if (cls == CLS_TOPK) {
     // ---- local top-k by key among finite logits (sampler.py:133-136, ties toward the lower index) ----
+    VS_TRX(17);
     const int k = top_k;
     if (t == 0) {
       s.misc[4] = 0;
       s.misc[9] = 0;
       s.misc[14] = 0;
     }
+    // the lane's largest finite logit: a three-input maximum over every position read at once, unless the
+    // magnitude bits show a NaN or an infinity (then the exact loop)
     float fmx = -__builtin_inff();
-    bool hasf = false;
-    FOR_XV({
-      if (is_finite(x)) {
-        hasf = true;
-        fmx = fmaxf(fmx, x);
+    bool hasf;
+    {
+      const int nel = hi - lo;
+      const int t0 = t < nel ? t : 0;
+      float xq[EPT_MAX];
+#pragma unroll
+      for (int u = 0; u < EPT_MAX; ++u) xq[u] = s.xv[t + u * SNT < nel ? t + u * SNT : t0];  // no branch per read
+      uint32_t mag = 0;
+#pragma unroll
+      for (int u = 0; u < EPT_MAX; u += 2) {
+        fmx = max3f(fmx, xq[u], xq[u + 1]);
+        mag = max3u(mag, __float_as_uint(xq[u]) & 0x7FFFFFFFu, __float_as_uint(xq[u + 1]) & 0x7FFFFFFFu);
       }
-    })
+      hasf = t < nel;
+      if (mag >= 0x7F800000u) {
+        fmx = -__builtin_inff();
+        hasf = false;
+        FOR_XV({
+          if (is_finite(x)) {
+            hasf = true;
+            fmx = fmaxf(fmx, x);
+          }
+        })
+      }
+    }
     const uint32_t tmax = hasf ? ord32(fmx) : 0u;  // ord32 of a finite value is never 0
     VS_TR(A, 10);
     // Only logits >= L can be in the local top-k (L = 0: no bound, every finite logit is a candidate).
@@ -1617,9 +1638,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     {
       static_assert(EPT_MAX % 2 == 0, "positions are taken in pairs");
       float xq[EPT_MAX];  // every read in flight at once (CH <= EPT_MAX * SNT)
-      xq[0] = s.xv[t0];
 #pragma unroll
-      for (int u = 1; u < EPT_MAX; ++u) xq[u] = u * SNT < nel ? s.xv[t + u * SNT < nel ? t + u * SNT : t0] : xq[0];
+      for (int u = 0; u < EPT_MAX; ++u) xq[u] = s.xv[t + u * SNT < nel ? t + u * SNT : t0];  // no branch per read
 #pragma unroll
       for (int u = 0; u < EPT_MAX; u += 2) {
         fmx = max3f(fmx, xq[u], xq[u + 1]);
