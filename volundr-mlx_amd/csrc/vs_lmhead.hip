@@ -69,13 +69,6 @@ struct LHArgs {
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
-// float32 -> bf16, round to nearest even (NaN stays NaN)
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-
 // (m, s) pairs: s = sum exp(x - m) over finite x, accumulated in float64; the rescale factor exp(m - mm) <= 1 is a
 // float32 expf (relative error ~1e-7, far inside the logprob tolerance; a float64 exp per merge step made the
 // cross-lane and cross-workgroup merges cost tens of microseconds)
@@ -275,41 +268,93 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       wo1[j] = no1[j];
     }
     VS_TR(A, 2 + 3 * r);
-    // epilogue of the round: lane holds vocabulary rows tile*16 + 4*kg + q of positions tt*16 + m16
+    // epilogue of the round: lane holds vocabulary rows tile*16 + 4*kg + q of positions tt*16 + m16. The values
+    // are rounded to bf16 (the hardware conversion, round to nearest even); a lane whose in-range values are all
+    // finite (magnitude bits below +inf's) takes the short path: the maximum by three-input instructions, its first
+    // vocabulary row by a backward sweep of equality selects (rows grow with j and q), and exp2 sums; otherwise the
+    // exact per-value path.
+    const float L2E = 1.44269504088896340736f;
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
       const int pos = tt * 16 + m16;
-      float vm = -__builtin_inff();
       float xs[NTW][4];
+      float best = -__builtin_inff();
+      uint32_t mag = 0;
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int v = tile[j] * 16 + kg * 4 + q;
-          const uint16_t xb = f32_to_bf16_rne(acc[j][tt][q]);
-          const float x = bf16_to_f32(xb);
-          const bool in = tile[j] < t1 && v < A.vv;
-          if (A.out_logits && tile[j] < t1 && v < A.N && pos < R) A.out_logits[(int64_t)pos * A.ldo + v] = xb;
+          const bool in = (tile[j] < t1) & (v < A.vv);
+          const float x = (float)(__bf16)acc[j][tt][q];
           xs[j][q] = in ? x : -__builtin_inff();
-          if (in) {
-            const u64 k = amkey64(x, (uint32_t)v);
-            pk[tt] = k > pk[tt] ? k : pk[tt];
-          }
-          if (in && is_finite(x)) vm = x > vm ? x : vm;
+          mag = in ? max3u(mag, __float_as_uint(x) & 0x7FFFFFFFu, 0u) : mag;
         }
+        best = max3f(best, max3f(xs[j][0], xs[j][1], xs[j][2]), xs[j][3]);
       }
-      if (vm > pm[tt]) {
-        if (ps[tt] > 0.0) ps[tt] *= (double)expf(pm[tt] - vm);
-        pm[tt] = vm;
-      }
-      if (is_finite(pm[tt])) {
-        float sacc = 0.0f;
+      if (A.out_logits) {
 #pragma unroll
         for (int j = 0; j < NTW; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (is_finite(xs[j][q])) sacc += expf(xs[j][q] - pm[tt]);
-        ps[tt] += (double)sacc;
+          for (int q = 0; q < 4; ++q) {
+            const int v = tile[j] * 16 + kg * 4 + q;
+            if (tile[j] < t1 && v < A.N && pos < R)
+              A.out_logits[(int64_t)pos * A.ldo + v] = __builtin_bit_cast(uint16_t, (__bf16)acc[j][tt][q]);
+          }
+      }
+      if (mag < 0x7F800000u) {
+        if (best > -__builtin_inff()) {  // some value in range
+          int bi = 0;
+#pragma unroll
+          for (int j = NTW - 1; j >= 0; --j)
+#pragma unroll
+            for (int q = 3; q >= 0; --q) bi = xs[j][q] == best ? tile[j] * 16 + kg * 4 + q : bi;
+          const u64 k = amkey64(best, (uint32_t)bi);
+          pk[tt] = k > pk[tt] ? k : pk[tt];
+          if (best > pm[tt]) {
+            if (ps[tt] > 0.0) ps[tt] *= (double)__builtin_amdgcn_exp2f((pm[tt] - best) * L2E);
+            pm[tt] = best;
+          }
+        }
+        if (is_finite(pm[tt])) {
+          float s0 = 0.0f, s1 = 0.0f;  // two chains of additions; exp2(-inf) = 0 for the values out of range
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            s0 += __builtin_amdgcn_exp2f((xs[j][0] - pm[tt]) * L2E);
+            s1 += __builtin_amdgcn_exp2f((xs[j][1] - pm[tt]) * L2E);
+            s0 += __builtin_amdgcn_exp2f((xs[j][2] - pm[tt]) * L2E);
+            s1 += __builtin_amdgcn_exp2f((xs[j][3] - pm[tt]) * L2E);
+          }
+          ps[tt] += (double)s0 + (double)s1;
+        }
+      } else {
+        float vm = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int v = tile[j] * 16 + kg * 4 + q;
+            const float x = xs[j][q];
+            if ((tile[j] < t1) & (v < A.vv)) {
+              const u64 k = amkey64(x, (uint32_t)v);
+              pk[tt] = k > pk[tt] ? k : pk[tt];
+              if (is_finite(x)) vm = x > vm ? x : vm;
+            }
+          }
+        }
+        if (vm > pm[tt]) {
+          if (ps[tt] > 0.0) ps[tt] *= (double)expf(pm[tt] - vm);
+          pm[tt] = vm;
+        }
+        if (is_finite(pm[tt])) {
+          float sacc = 0.0f;
+#pragma unroll
+          for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (is_finite(xs[j][q])) sacc += expf(xs[j][q] - pm[tt]);
+          ps[tt] += (double)sacc;
+        }
       }
     }
   }
@@ -420,25 +465,40 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
         }
         mx = wave_max(mx);
         const float mt = mx > mb[q] ? mx : mb[q];  // the running maximum over the batches of partials
-        double acc = sb[q] > 0.0 && is_finite(mt) ? sb[q] * (double)expf(mb[q] - mt) : 0.0;
+        const float L2E = 1.44269504088896340736f;
+        double acc = sb[q] > 0.0 && is_finite(mt) ? sb[q] * (double)__builtin_amdgcn_exp2f((mb[q] - mt) * L2E) : 0.0;
 #pragma unroll
         for (int u = 0; u < LPL / 8; ++u)
-          acc += (ss[q][u] > 0.0 && is_finite(mt)) ? ss[q][u] * (double)expf(mm[q][u] - mt) : 0.0;
+          acc += (ss[q][u] > 0.0 && is_finite(mt)) ? ss[q][u] * (double)__builtin_amdgcn_exp2f((mm[q][u] - mt) * L2E)
+                                                   : 0.0;
         mb[q] = mt;
         sb[q] = acc;
       }
     }
+    // the reductions of the LMPW positions, then lane q finishes position q (its outputs in parallel)
+    u64 kf = 0;
+    float mf = 0.0f;
+    double sf = 0.0;
 #pragma unroll
     for (int q = 0; q < LMPW; ++q) {
-      const int pos = p0 + q * LNW;
       const u64 k = wave_max(kb[q]);
-      const float m = mb[q];  // already the same in every lane
       const double sm = wave_sum(sb[q]);
-      if (ln == 0 && pos < R) {
-        const float xj = am_is_nan(k) ? __builtin_nanf("") : key_value(k);
-        const int32_t tok = (int32_t)key_index(k);
+      kf = ln == q ? k : kf;
+      mf = ln == q ? mb[q] : mf;  // mb is already the same in every lane
+      sf = ln == q ? sm : sf;
+    }
+    {
+      const int pos = p0 + ln * LNW;
+      if (ln < LMPW && pos < R) {
+        const float xj = am_is_nan(kf) ? __builtin_nanf("") : key_value(kf);
+        const int32_t tok = (int32_t)key_index(kf);
         A.out_argmax[pos] = tok;
-        if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && sm > 0.0) ? (float)((double)xj - ((double)m + log(sm))) : 0.0f;
+        // log(s) = log1p(s - 1): s >= 1 (the maximum's own term), so the float log keeps its relative accuracy
+        // also when one token dominates (s - 1 tiny)
+        if (A.out_lp)
+          A.out_lp[pos] = (is_finite(xj) && sf > 0.0)
+                              ? (float)((double)xj - ((double)mf + (double)log1pf((float)(sf - 1.0))))
+                              : 0.0f;
         const int b = pos / A.T, tp = pos % A.T;
         if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
       }
