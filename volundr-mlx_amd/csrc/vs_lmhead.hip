@@ -454,6 +454,10 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
           ss[q][u] = in ? s0 : 0.0;
         }
       }
+#ifdef VS_TRACE
+      publish_wait();
+      VS_TR(A, 23);
+#endif
       // the row maximum first (one wave max), then every partial sum rescaled to it once: no pairwise merges
 #pragma unroll
       for (int q = 0; q < LMPW; ++q) {
@@ -475,6 +479,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
         sb[q] = acc;
       }
     }
+    VS_TR(A, 24);
     // the reductions of the LMPW positions, then lane q finishes position q (its outputs in parallel)
     u64 kf = 0;
     float mf = 0.0f;
@@ -487,6 +492,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       mf = ln == q ? mb[q] : mf;  // mb is already the same in every lane
       sf = ln == q ? sm : sf;
     }
+    VS_TR(A, 25);
     {
       const int pos = p0 + ln * LNW;
       if (ln < LMPW && pos < R) {
