@@ -11,7 +11,8 @@ Infinity Cache. Printed (one JSON line on stdout):
               launch stream; rocprofv3's average kernel duration agrees within a few percent) vs 8 TB/s
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
-is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts);
+is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts),
+"c3_greedy" C3's logits and histories with every row greedy (temperature 0);
 "draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary;
 "lmhead_verify_*" is the bf16 lm_head with greedy verify fused in (vs_lmhead_verify_greedy), beside the unfused
 torch matmul + vs_verify_greedy.
@@ -329,6 +330,14 @@ def main():
             others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
             if not a.no_cpu:
                 others[name].update(boundary_rows(dd, oout))
+        if sel("c3_greedy"):
+            # C3's logits and histories with every row greedy (temperature 0, same penalties): the argmax class
+            from volundr_amd.session import Sampling
+            dd = synth.CONFIGS["c3"](seed=0)
+            dd["params"] = [Sampling(temperature=0.0, repetition_penalty=p.repetition_penalty,
+                                     presence_penalty=p.presence_penalty) for p in dd["params"]]
+            (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others["c3_greedy"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         if sel("c3_state"):
             dd = synth.CONFIGS["c3"](seed=0)
             (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)

@@ -1226,20 +1226,69 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 
   if (cls == CLS_GREEDY) {
     // ---- sampler.py:127-128: np.argmax(x), first maximum; logprob = log-softmax of the processed row ----
+    // Every position of the lane read at once; a lane whose magnitudes stay below +inf's holds only finite logits:
+    // its maximum by three-input instructions and the first position holding it by a backward sweep (positions
+    // grow with u); a lane with a NaN or an infinity takes the exact loop (NaN ranks first, np.argmax).
+    const int nel = hi - lo;
+    const int t0 = t < nel ? t : 0;
+    float xq[EPT_MAX];
+#pragma unroll
+    for (int u = 0; u < EPT_MAX; ++u) xq[u] = s.xv[t + u * SNT < nel ? t + u * SNT : t0];
+    float best = -__builtin_inff();
+    uint32_t mag = 0;
+#pragma unroll
+    for (int u = 0; u < EPT_MAX; u += 2) {
+      best = max3f(best, xq[u], xq[u + 1]);
+      mag = max3u(mag, __float_as_uint(xq[u]) & 0x7FFFFFFFu, __float_as_uint(xq[u + 1]) & 0x7FFFFFFFu);
+    }
     u64 am = 0;
     float mf = -__builtin_inff();
-    FOR_XV({
-      const u64 k = amkey64(x, (uint32_t)e);
-      am = k > am ? k : am;
-      if (is_finite(x)) mf = x > mf ? x : mf;
-    })
-    am = block_max<SNT>(am, s.red64);
-    mf = block_max<SNT>(mf, (float*)s.redf);
+    if (mag < 0x7F800000u) {
+      if (t < nel) {
+        int bu = 0;
+#pragma unroll
+        for (int u = EPT_MAX - 1; u >= 0; --u) bu = ((xq[u] == best) & (t + u * SNT < nel)) ? u : bu;
+        am = amkey64(best, (uint32_t)(lo + t + bu * SNT));
+        mf = best;
+      }
+    } else {
+      FOR_XV({
+        const u64 k = amkey64(x, (uint32_t)e);
+        am = k > am ? k : am;
+        if (is_finite(x)) mf = x > mf ? x : mf;
+      })
+    }
+    {  // both maxima in one exchange
+      am = wave_max(am);
+      mf = wave_max(mf);
+      const int w = t / WAVE;
+      if (lane_id() == 0) {
+        s.red64[w] = am;
+        ((float*)s.redf)[w] = mf;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < SNW; ++i) {
+        const u64 ki = s.red64[i];
+        const float mi = ((float*)s.redf)[i];
+        am = ki > am ? ki : am;
+        mf = mi > mf ? mi : mf;
+      }
+      __syncthreads();
+    }
+    // sum exp(x - mf) over the finite logits: exp2 of (x - mf) log2(e) per position, float sums per lane
     double se = 0.0;
     if (is_finite(mf)) {
-      FOR_XV({
-        if (is_finite(x)) se += exp((double)x - (double)mf);
-      })
+      const float L2E = 1.44269504088896340736f;
+      float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+      for (int u = 0; u < EPT_MAX; u += 2) {
+        const float x0 = xq[u], x1 = xq[u + 1];
+        s0 += __builtin_amdgcn_exp2f(((t + u * SNT < nel) & is_finite(x0)) ? (x0 - mf) * L2E : -__builtin_inff());
+        s1 += __builtin_amdgcn_exp2f(((t + (u + 1) * SNT < nel) & is_finite(x1)) ? (x1 - mf) * L2E
+                                                                                  : -__builtin_inff());
+      }
+      se = (double)s0 + (double)s1;
     }
     se = block_sum<SNT>(se, s.redf);
     put_part(am, 0, 0, mf, se);
@@ -1258,13 +1307,18 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         }
         const u64 bam = wave_max(k);
         const float M = wave_max(m);
-        const double S = wave_sum((e > 0.0 && is_finite(M)) ? e * exp((double)m - (double)M) : 0.0);
+        const float L2E = 1.44269504088896340736f;
+        const double S =
+            wave_sum((e > 0.0 && is_finite(M)) ? e * (double)__builtin_amdgcn_exp2f((m - M) * L2E) : 0.0);
         if (t == 0) {
           const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
           const int r = A.row0 + row;
           const uint32_t fl = commit_state(A, r, (int32_t)key_index(bam), VS_OUT_GREEDY, st, rng_next);
           A.out_ids[r] = (int32_t)key_index(bam);
-          A.out_lp[r] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
+          // log(S) = log1p(S - 1): S >= 1 holds the maximum's own term, so the float log1p keeps its relative
+          // accuracy when one token dominates
+          A.out_lp[r] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0))))
+                                                   : 0.0f;
           if (A.out_flags) A.out_flags[r] = fl;
           if (A.out_keep) A.out_keep[r] = 0;
         }
