@@ -155,6 +155,20 @@ def test_binned_path_many_draws(dev):
     run(dev, xs, ps, np.linspace(0.0, 0.999999, 16), label="binned draws")
 
 
+def test_near_flat_full_size_extreme_draws(dev):
+    """C5's shape at unit temperature (the dense value-bin instance without division) and at t = 0.8, with draws at
+    both ends of the CDF: the draw's coarse bins are the top one (digit 255, beside the not-kept id 0xFFFF) and the
+    last ones, with and without a top-p cut."""
+    rng = np.random.default_rng(23)
+    V = 163840
+    x = (rng.standard_normal((1, V)) * 0.1).astype(np.float32)
+    xs = np.repeat(x, 8, axis=0)
+    ps = [Sampling(temperature=1.0, top_p=0.95)] * 3 + [Sampling(temperature=1.0, top_p=1.0)] * 3 + \
+         [Sampling(temperature=0.8, top_p=0.95)] * 2
+    us = [0.0, 1e-7, 0.9999999, 0.0, 0.5, 0.9999999, 1e-7, 0.9999999]
+    run(dev, xs, ps, us, label="near-flat extremes")
+
+
 def test_ties_fall_back_to_radix(dev):
     # bf16 near-flat logits: a few hundred distinct values for 100k tokens, so value bins hold long runs of ties
     rng = np.random.default_rng(22)
