@@ -1342,10 +1342,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     // magnitude bits show a NaN or an infinity (then the exact loop)
     float fmx = -__builtin_inff();
     bool hasf;
+    float xq[EPT_MAX];  // the lane's positions t + SNT u (past the chunk: a repeat), kept for the candidate scan
     {
       const int nel = hi - lo;
       const int t0 = t < nel ? t : 0;
-      float xq[EPT_MAX];
 #pragma unroll
       for (int u = 0; u < EPT_MAX; ++u) xq[u] = s.xv[t + u * SNT < nel ? t + u * SNT : t0];  // no branch per read
       uint32_t mag = 0;
@@ -1384,38 +1384,34 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     if (lb.nlanes > 0) {
       const uint32_t L = lb.L;
       const float Lf = L ? inv_ord32(L) : -__builtin_inff();  // x >= Lf  <=>  ord32(x) >= L for finite x
-      // Every candidate sits in a lane whose maximum reaches the bound (about k lanes). Each wave scans its own
-      // qualifying lanes' elements with all its lanes (pair p -> lane q = p / M, element m = p % M) and appends
-      // the candidates to its own segment of the key area with ballots: no atomics, no block barrier.
+      // Every candidate sits in a lane whose maximum reaches the bound (about k lanes), and each lane still holds
+      // its positions in registers: a candidate mask per lane from compares alone, one wave scan for the offsets in
+      // the wave's segment of the key area, then each lane stores its own candidates (a loop as long as the
+      // busiest lane's count, usually one to three; no atomics, no block barrier).
       const int wv = t / WAVE, Ln = lane_id();
-      const bool qual = tmax != 0 && tmax >= L;
-      const unsigned long long Q = __ballot(qual);
-      const int nqw = __popcll(Q);
-      int* qlw = (int*)(s.tk + KCAP) + wv * WAVE;  // this wave's qualifying lanes
-      if (qual) qlw[__builtin_amdgcn_mbcnt_hi((uint32_t)(Q >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)Q, 0u))] = Ln;
       const int nel = hi - lo;
-      const int M = (nel + SNT - 1) / SNT;  // elements per lane
-      const float invM = 1.0f / (float)M;
-      const int totw = nqw * M;
+      uint32_t cm = 0;
+#pragma unroll
+      for (int u = 0; u < EPT_MAX; ++u) {
+        if (u % 4 == 0 && u * SNT >= nel) break;  // uniform: the chunk's positions end here
+        cm |= (uint32_t)((xq[u] >= Lf) & (__builtin_fabsf(xq[u]) < __builtin_inff())) << u;
+      }
+      // positions past the chunk (repeats of the lane's first one) are not candidates
+      const int npos = t < nel ? (nel - t + SNT - 1) / SNT : 0;
+      cm &= npos >= 32 ? ~0u : (1u << npos) - 1u;
+      const int nc = __builtin_popcount(cm);
+      const int incl = wave_scan(nc);
+      const int cw = __builtin_amdgcn_readlane(incl, WAVE - 1);
+      int pos = incl - nc;
       u64* segw = s.keys + wv * SEGW;
-      int cw = 0;
       u64 lmx = 0;  // this lane's largest candidate key
-      for (int p0 = 0; p0 < totw; p0 += WAVE) {
-        const int pp = p0 + Ln;
-        int q = (int)((float)pp * invM);  // pp < 2^24: corrected to the exact quotient below
-        q -= q * M > pp;
-        q += (q + 1) * M <= pp;
-        const int m = pp - q * M;
-        const int ql = qlw[q < nqw ? q : nqw - 1];
-        const int i = wv * WAVE + ql + SNT * m;
-        const float x = s.xv[i < nel ? i : 0];
-        const bool c = pp < totw && i < nel && x >= Lf && is_finite(x);
-        const unsigned long long mc = __ballot(c);
-        const int pos = cw + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mc, 0u));
-        const u64 kk = key64(x, (uint32_t)(lo + i));
-        if (c && pos < SEGW) segw[pos] = kk;
-        lmx = (c & (kk > lmx)) ? kk : lmx;
-        cw += __popcll(mc);
+      while (cm) {
+        const int i = t + __builtin_ctz(cm) * SNT;
+        cm &= cm - 1;
+        const u64 kk = key64(s.xv[i], (uint32_t)(lo + i));
+        if (pos < SEGW) segw[pos] = kk;
+        lmx = kk > lmx ? kk : lmx;
+        ++pos;
       }
       const u64 hwv = wave_max(lmx);  // the wave's head (0: no candidate)
       int* segc = s.misc + M_SEGC;  // [SNW] candidates per wave
