@@ -104,6 +104,33 @@ def test_lmhead_matches_verify_kernel_on_its_logits(dev):
     np.testing.assert_allclose(o.logprobs.cpu().numpy(), ov.logprobs.cpu().numpy(), rtol=1e-5, atol=1e-6)
 
 
+def test_lmhead_nonfinite_outputs(dev):
+    """Head outputs with infinities and NaN (an infinite hidden entry times weights of both signs gives +-inf rows;
+    two of opposite signs give NaN where the weights agree in sign) and a zero hidden row (every logit 0, one tie
+    over the vocabulary): the epilogue's exact per-value path, against np.argmax on the kernel's own logits and
+    against vs_verify_greedy run on them."""
+    B, T, K, N = 1, 17, 1024, 30000
+    h, w, drafts = _case(31, B, T, K, N, plant=False)
+    h = h.copy()
+    h[2, 5] = 0x7F80  # +inf
+    h[4, 5] = 0x7F80
+    h[4, 9] = 0xFF80  # -inf
+    h[6, :] = 0
+    o, got = _run(dev, h, w, drafts, B, T, N)
+    tok, acc, _ = VR.verify(got.reshape(B, T, -1), drafts, N)
+    gf = L.bf16_to_f32(got).reshape(B, T, -1)
+    assert np.isposinf(gf[0, 2]).any() and np.isnan(gf[0, 4]).any() and (gf[0, 6] == 0).all()
+    np.testing.assert_array_equal(o.argmax.cpu().numpy(), tok)
+    np.testing.assert_array_equal(o.accept.cpu().numpy(), acc)
+    assert int(o.argmax[0, 6]) == 0
+    ov = verify_greedy(_bits_tensor(got, dev).reshape(B, T, N), torch.from_numpy(drafts).to(dev), N)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o.argmax.cpu().numpy(), ov.argmax.cpu().numpy())
+    fin = np.isfinite(gf).all(axis=-1)[0]  # positions without any non-finite logit
+    np.testing.assert_allclose(o.logprobs.cpu().numpy()[0, fin], ov.logprobs.cpu().numpy()[0, fin], rtol=1e-5,
+                               atol=1e-6)
+
+
 def test_lmhead_full_size_against_torch(dev):
     """vocab 248320 x hidden 5120 (the model's head), B=1, T=17: logits against torch's float32 matmul of the same
     bf16 operands (a plain PyTorch float32 reference), rounded to bf16; argmax/accept/logprob against the verify
