@@ -10,6 +10,7 @@ Infinity Cache. Printed (one JSON line on stdout):
   roofline    algorithmic bytes per launch / per-launch time (HIP events around the K back-to-back launches on the
               launch stream; rocprofv3's average kernel duration agrees within a few percent) vs 8 TB/s
   cpu_baseline  the NumPy restatement of sampler.py (oracle/) on a bounded sample of the same rows, 1 core
+  graph_us_per_step  the same step captured in a HIP graph (hipGraph via torch.cuda.CUDAGraph), replayed
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
 is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts),
 "c3_greedy" C3's logits and histories with every row greedy (temperature 0);
@@ -73,6 +74,44 @@ def time_calls(torch, call, nslots, steps, warmup):
     torch.cuda.synchronize()
     kern = sum(a.elapsed_time(b) for a, b in ev) * 1000.0 / steps
     return e2e, kern
+
+
+def time_graph(torch, make_call, nslots, steps, warmup):
+    """-> us per step of the same calls captured in a HIP graph (up to 200 launches per graph), replayed back to
+    back. The call is bound on a side stream outside the capture (its workspace is zeroed there, eagerly), then
+    captured on that stream: only the kernels are recorded."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call = make_call()
+        for i in range(warmup):
+            call(i % nslots)
+    torch.cuda.synchronize()
+    n = max(1, min(steps, 200))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for i in range(n):
+            call(i % nslots)
+    reps = max(steps // n, 3)
+    g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1000.0 / (reps * n)
+
+
+def bench_sample_graph(torch, dev, d, steps, warmup, nslots):
+    """The benchmarked vs_sample_batch call, captured in a HIP graph (time_graph)."""
+    from volundr_amd import ops
+
+    x = torch.from_numpy(d["logits"]).to(dev)
+    slots = [x] + [x.clone() for _ in range(nslots - 1)]
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
+    return time_graph(torch, lambda: ops.PreparedSample(slots, rows), nslots, steps, warmup)
 
 
 def bench_sample(torch, dev, d, steps, warmup, nslots):
@@ -368,6 +407,8 @@ def main():
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
     parity = None if (a.no_cpu or verify) else boundary_rows(d, sout)
     floor = launch_floor(torch, dev, a.steps)
+    # the same step captured in a HIP graph and replayed (host launch cost out of the loop)
+    graph = None if verify else round(bench_sample_graph(torch, dev, d, a.steps, a.warmup, a.slots), 2)
     # One kernel per step, launched back to back: the per-step time is the kernel's average launch duration plus
     # the inter-dispatch gap (rocprofv3 --kernel-trace agrees within a few percent); per-launch event pairs add
     # their own overhead and are reported separately.
@@ -384,6 +425,7 @@ def main():
         "kernel_us_event_pairs": round(kern, 2), "warm_us_per_step": round(e2e_w, 2),
         "warm_kernel_us_event_pairs": round(kern_w, 2),
         "kernels_per_step": 1,
+        "graph_us_per_step": graph,
         "launch_floor_us": floor,
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
