@@ -314,8 +314,8 @@ def load_traffic(name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--slots", type=int, default=32, help="rotating logits buffers (cold-HBM measurement)")
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true")
