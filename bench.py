@@ -3,9 +3,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
 
 A step is one vs_sample_batch call over the B=16 x V=163840 mixed-parameter batch (configuration C3, the one
-the headline metric is quoted on), with logits, parameters and histories already resident in HBM. Logits rotate over
-`--slots` device buffers (> 256 MB in total by default), so every step reads them from HBM and not from the 256 MB
-Infinity Cache. Printed (one JSON line on stdout):
+the headline metric is quoted on), with logits, parameters and histories already resident in HBM. Logits, parameters
+and histories rotate over `--slots` device copies (> 256 MB in total by default), so every step reads them from HBM
+and not from the 256 MB Infinity Cache. Printed (one JSON line on stdout):
   value       end-to-end microseconds per step (host-issued launches back to back, HIP events on the launch stream)
   roofline    algorithmic bytes per launch / per-launch time (HIP events around the K back-to-back launches on the
               launch stream; rocprofv3's average kernel duration agrees within a few percent) vs 8 TB/s
@@ -13,6 +13,7 @@ Infinity Cache. Printed (one JSON line on stdout):
   graph_us_per_step  the same step captured in a HIP graph (hipGraph via torch.cuda.CUDAGraph), replayed
 The other configurations (C1, C2, C4, C5) are reported under "other_configs" with the same method, and "c3_state"
 is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts),
+"c3_dropin" C3 through sample_rows_for and the Sampler.choose loop (host work included, wall clock),
 "c3_greedy" C3's logits and histories with every row greedy (temperature 0);
 "draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary;
 "lmhead_verify_*" is the bf16 lm_head with greedy verify fused in (vs_lmhead_verify_greedy), beside the unfused
@@ -104,29 +105,73 @@ def time_graph(torch, make_call, nslots, steps, warmup):
     return t0.elapsed_time(t1) * 1000.0 / (reps * n)
 
 
-def bench_sample_graph(torch, dev, d, steps, warmup, nslots):
-    """The benchmarked vs_sample_batch call, captured in a HIP graph (time_graph)."""
+def prepared_slots(torch, dev, d, nslots):
+    """-> (call(i), last output): nslots copies of the batch, logits and packed rows (parameters and histories)
+    each in its own device buffers, so that a rotation over them reads every input from HBM rather than from the
+    Infinity Cache; call(i) launches vs_sample_batch on copy i."""
     from volundr_amd import ops
 
     x = torch.from_numpy(d["logits"]).to(dev)
-    slots = [x] + [x.clone() for _ in range(nslots - 1)]
-    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
-    return time_graph(torch, lambda: ops.PreparedSample(slots, rows), nslots, steps, warmup)
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"])
+    preps = [ops.PreparedSample([x if i == 0 else x.clone()], rows.to(dev)) for i in range(nslots)]
+    return (lambda i: preps[i](0)), preps
+
+
+def bench_sample_graph(torch, dev, d, steps, warmup, nslots):
+    """The benchmarked vs_sample_batch call, captured in a HIP graph (time_graph)."""
+    return time_graph(torch, lambda: prepared_slots(torch, dev, d, nslots)[0], nslots, steps, warmup)
 
 
 def bench_sample(torch, dev, d, steps, warmup, nslots):
-    from volundr_amd import ops
-
     B = d["logits"].shape[0]
-    x = torch.from_numpy(d["logits"]).to(dev)
-    slots = [x] + [x.clone() for _ in range(nslots - 1)]
-    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
-    call = ops.PreparedSample(slots, rows)
+    call, preps = prepared_slots(torch, dev, d, nslots)
     cold = time_calls(torch, call, nslots, steps, warmup)
     warm = time_calls(torch, call, 1, steps, warmup)
-    flags = call.out.flags.cpu().numpy()
+    out = preps[0].out
+    flags = out.flags.cpu().numpy()
     assert not any((int(f) & 0xFFFFFFFF) >> 31 for f in flags), "timeout flag set"
-    return cold, warm, algo_bytes_sample(d, B), call.out
+    return cold, warm, algo_bytes_sample(d, B), out
+
+
+def bench_dropin(torch, dev, d, steps):
+    """The drop-in routes of sampler.py as a scheduler calls them, host work included: one
+    sample_rows_for(logits, samplers) per step (packing, uploads, one launch, the result copies), and the per-row
+    Sampler.choose loop of scheduler.py:416-425. Wall-clock us per step (both return host ints, so both synchronise)."""
+    from volundr_amd import Sampler
+    from volundr_amd.sampler import sample_rows_for
+
+    B, Vx = d["logits"].shape
+    x = torch.from_numpy(d["logits"]).to(dev)
+
+    def mk():
+        ss = []
+        for r, sp in enumerate(d["params"]):
+            s = Sampler(sp, vocab_valid=Vx, request_id=r)
+            for tok in (d["hists"][r] if d["hists"] is not None else ()):
+                s.accept(int(tok))
+            ss.append(s)
+        return ss
+
+    n = max(steps // 50, 10)
+    ss = mk()
+    for _ in range(3):
+        sample_rows_for(x, ss)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        sample_rows_for(x, ss)
+    batched = (time.perf_counter() - t0) * 1e6 / n
+    ss = mk()
+    for i, s in enumerate(ss):
+        s.choose(x[i])
+    torch.cuda.synchronize()
+    nl = max(n // 4, 3)
+    t0 = time.perf_counter()
+    for _ in range(nl):
+        for i, s in enumerate(ss):
+            s.choose(x[i])
+    loop = (time.perf_counter() - t0) * 1e6 / nl
+    return batched, loop
 
 
 def bench_state(torch, dev, d, steps, warmup, nslots):
@@ -377,6 +422,12 @@ def main():
                                      presence_penalty=p.presence_penalty) for p in dd["params"]]
             (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others["c3_greedy"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
+        if sel("c3_dropin"):
+            dd = synth.CONFIGS["c3"](seed=0)
+            bt, lp = bench_dropin(torch, dev, dd, a.steps)
+            others["c3_dropin"] = {"sample_rows_for_us_per_step": round(bt, 1), "choose_loop_us_per_step": round(lp, 1),
+                                   "workload": "C3 through the drop-in routes, host work included (wall clock): one "
+                                               "sample_rows_for per step, and the per-row Sampler.choose loop"}
         if sel("c3_state"):
             dd = synth.CONFIGS["c3"](seed=0)
             (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)
