@@ -96,3 +96,35 @@ def test_draft_entry_points_reject_bad_shapes_without_device_calls():
     assert L.vs_topk_batch(1, 0, 1, 10, 10, 0, 1, 1, 1, 1 << 20, 0) == _lib.VS_EINVAL  # k < 1
     assert L.vs_draft_workspace_bytes(2, 7, 163840) > L.vs_sample_workspace_bytes(14, 163840)
     assert L.vs_draft_propose(1, 0, 1, 7, 10, 10, 1, 4, 4, 10, 256, 1, 1, 0, 0, 0) == _lib.VS_EINVAL  # null ws
+
+
+def test_token_history_is_list_like_and_packs_like_a_list():
+    from volundr_amd.sampler import TokenHistory
+
+    rng = np.random.default_rng(5)
+    lists = [rng.integers(0, 1000, n).tolist() for n in (0, 1, 63, 64, 65, 300)]
+    hs = []
+    for lst in lists:
+        h = TokenHistory()
+        for t in lst:
+            h.append(t)
+        assert len(h) == len(lst) and list(h) == lst and h == lst and np.asarray(h).tolist() == lst
+        if lst:
+            assert h[0] == lst[0] and h[-1] == lst[-1] and h[1:4] == lst[1:4]
+        hs.append(h)
+    assert TokenHistory(lists[-1]) == lists[-1]
+    with pytest.raises(ValueError):
+        TokenHistory().append(-1)
+    with pytest.raises(ValueError):
+        TokenHistory().append(2**31)
+    sps = [Sampling(temperature=float(rng.uniform(0.1, 2)), top_k=int(rng.integers(-2, 50)),
+                    top_p=float(rng.uniform(0.1, 1)), repetition_penalty=1.1,
+                    logit_bias=[(int(rng.integers(0, 1000)), 0.5)], suppress_tokens=[7] * (i % 2))
+           for i in range(len(lists))]
+    u = rng.random(len(lists))
+    a = pack_rows(sps, u, V=1000, histories=lists)
+    b = pack_rows(sps, u, V=1000, histories=hs)
+    assert a.params.tobytes() == b.params.tobytes()
+    for f in ("hist", "bias_ids", "bias_vals", "mask_ids"):
+        assert np.array_equal(getattr(a, f), getattr(b, f))
+    assert pack_rows([], [], V=10).params.size == 0

@@ -75,10 +75,25 @@ class PackedRows:
     mask_ids: np.ndarray    # int32
 
     def to(self, dev) -> "DeviceRows":
-        def up(a):
-            return torch.from_numpy(np.ascontiguousarray(a)).to(dev) if a.size else None
-        return DeviceRows(torch.from_numpy(self.params.view(np.uint8).copy()).to(dev), up(self.hist),
-                          up(self.bias_ids), up(self.bias_vals), up(self.mask_ids), len(self.params))
+        """One host-to-device copy: the five arrays laid end to end (each at a 256-byte offset) in one staging
+        buffer, viewed back into typed device tensors."""
+        parts = [self.params.view(np.uint8).reshape(-1)] + [np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+                                                            for a in (self.hist, self.bias_ids, self.bias_vals,
+                                                                      self.mask_ids)]
+        offs, n = [], 0
+        for p in parts:
+            offs.append(n)
+            n += (p.size + 255) // 256 * 256
+        host = np.zeros(max(n, 256), dtype=np.uint8)
+        for o, p in zip(offs, parts):
+            host[o:o + p.size] = p
+        buf = torch.from_numpy(host).to(dev)
+
+        def view(i, dt):
+            sz = parts[i].size
+            return buf[offs[i]:offs[i] + sz].view(dt) if sz else None
+        return DeviceRows(buf[:parts[0].size], view(1, torch.int32), view(2, torch.int32), view(3, torch.float32),
+                          view(4, torch.int32), len(self.params))
 
 
 @dataclass
@@ -114,24 +129,18 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
                 Sampling must pass argmax_only_ok and it must carry no extras
     """
     B = len(samplings)
-    P = np.zeros(B, dtype=ROW_DTYPE)
     u = np.asarray(u, dtype=np.float64).reshape(-1)
     if u.size != B:
         raise ValueError("one uniform draw per row is required")
-    hist_parts, bias_i, bias_v, mask = [], [], [], []
+    uf = u.tolist()
+    rows, hist_parts, bias_i, bias_v, mask = [], [], [], [], []
     hpos = bpos = mpos = 0
     for r, sp in enumerate(samplings):
-        p = P[r]
-        p["temperature"] = np.float32(sp.temperature)
-        p["repetition_penalty"] = np.float32(sp.repetition_penalty)
-        p["frequency_penalty"] = np.float32(sp.frequency_penalty)
-        p["presence_penalty"] = np.float32(sp.presence_penalty)
         k = sp.top_k if sp.top_k else 0          # sampler.py:133: None and 0 mean off
         if k < 0:
             k = 1                                # max(min(k, n), 1) == 1 for k < 0 (:134)
-        p["top_k"] = min(int(k), 2**31 - 1)
-        p["flags"] = VS_ROW_GREEDY if sp.greedy else 0
-        p["vocab_valid"] = V
+        flags = VS_ROW_GREEDY if sp.greedy else 0
+        vv = V
         vvr = None if argmax_vv is None else argmax_vv[r]
         if vvr is not None:
             vvr = int(vvr)
@@ -139,42 +148,50 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
                 raise ValueError("vocab_valid must be >= 1")
             if not argmax_only_ok(sp, vvr) or (extras is not None and extras[r]):
                 raise ValueError(f"row {r} needs the sampler's logits: it cannot take the argmax-only route")
-            p["flags"] |= VS_ROW_ARGMAX_VV
-            p["vocab_valid"] = min(vvr, V)
-        p["top_p"] = float(sp.top_p)
-        p["min_p"] = float(sp.min_p)
-        p["u"] = float(u[r])
-        h = np.asarray([] if histories is None or histories[r] is None else histories[r], dtype=np.int64).reshape(-1)
-        if h.size and (h.min() < 0 or h.max() >= 2**31):
-            raise ValueError("token histories must hold ids in [0, 2^31)")
-        p["hist_begin"], p["hist_end"] = hpos, hpos + h.size
-        hist_parts.append(h.astype(np.int32))
-        hpos += h.size
+            flags |= VS_ROW_ARGMAX_VV
+            vv = min(vvr, V)
+        hr = None if histories is None else histories[r]
+        if hasattr(hr, "array"):
+            h = hr.array()  # TokenHistory: int32, ids checked on append
+        else:
+            h = np.asarray([] if hr is None else hr, dtype=np.int64).reshape(-1)
+            if h.size and (h.min() < 0 or h.max() >= 2**31):
+                raise ValueError("token histories must hold ids in [0, 2^31)")
+            h = h.astype(np.int32)
+        hb = hpos
+        if h.size:
+            hist_parts.append(h)
+            hpos += h.size
         # additive biases in application order: budget extra, then logit_bias (sampler.py:104-109)
         items = []
         for t, d in list(extras[r] if extras is not None and extras[r] else []) + list(sp.logit_bias):
             w = _wrap_id(t, V)
             if w is not None:
                 items.append((w, np.float32(d)))
+        bb = bpos
         if items:
             ids = np.asarray([i for i, _ in items], dtype=np.int32)
             vals = np.asarray([v for _, v in items], dtype=np.float32)
             o = np.argsort(ids, kind="stable")
             bias_i.append(ids[o])
             bias_v.append(vals[o])
-        p["bias_begin"], p["bias_end"] = bpos, bpos + len(items)
-        bpos += len(items)
-        sup = sorted({w for w in (_wrap_id(t, V) for t in sp.suppress_tokens) if w is not None})
-        p["supp_begin"], p["supp_end"] = mpos, mpos + len(sup)
-        mask.append(np.asarray(sup, dtype=np.int32))
-        mpos += len(sup)
+            bpos += len(items)
+        sb = mpos
+        if sp.suppress_tokens:
+            sup = sorted({w for w in (_wrap_id(t, V) for t in sp.suppress_tokens) if w is not None})
+            mask.append(np.asarray(sup, dtype=np.int32))
+            mpos += len(sup)
+        se = mpos
         pr = 0 if produced is None else int(produced[r])
-        st = []
         if (stop_always or pr < sp.min_new_tokens) and sp.min_new_tokens > 0 and sp.stop_token_ids:
             st = sorted({w for w in (_wrap_id(t, V) for t in sp.stop_token_ids) if w is not None})
-        p["stop_begin"], p["stop_end"] = mpos, mpos + len(st)
-        mask.append(np.asarray(st, dtype=np.int32))
-        mpos += len(st)
+            mask.append(np.asarray(st, dtype=np.int32))
+            mpos += len(st)
+        # field order of ROW_DTYPE (vs_row_params)
+        rows.append((sp.temperature, sp.repetition_penalty, sp.frequency_penalty, sp.presence_penalty,
+                     min(int(k), 2**31 - 1), flags, float(sp.top_p), float(sp.min_p), uf[r], hb, hpos,
+                     bb, bpos, sb, se, se, mpos, vv, 0))
+    P = np.array(rows, dtype=ROW_DTYPE) if rows else np.zeros(0, dtype=ROW_DTYPE)
     cat = lambda xs, dt: np.concatenate(xs).astype(dt) if xs else np.zeros(0, dt)  # noqa: E731
     return PackedRows(P, cat(hist_parts, np.int32), cat(bias_i, np.int32), cat(bias_v, np.float32),
                       cat(mask, np.int32))
@@ -186,11 +203,13 @@ class SampleOut:
     logprobs: torch.Tensor  # float32 [B]
     flags: torch.Tensor     # int32 view of the uint32 VS_OUT_* bits [B]
     keep: torch.Tensor      # int32 [B]
+    block: Optional[torch.Tensor] = None  # int32 [4, B] holding the four rows above, when allocated together
 
 
 def alloc_out(B: int, dev) -> SampleOut:
-    z = lambda dt: torch.empty(B, dtype=dt, device=dev)  # noqa: E731
-    return SampleOut(z(torch.int32), z(torch.float32), z(torch.int32), z(torch.int32))
+    """The four outputs as rows of one [4, B] int32 block (logprobs viewed as float32), so one copy brings all back."""
+    blk = torch.empty(4, B, dtype=torch.int32, device=dev)
+    return SampleOut(blk[0], blk[1].view(torch.float32), blk[2], blk[3], blk)
 
 
 def sample_rows(logits: torch.Tensor, rows: DeviceRows, out: Optional[SampleOut] = None) -> SampleOut:

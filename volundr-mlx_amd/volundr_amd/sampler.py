@@ -20,6 +20,60 @@ MASK = (1 << 64) - 1
 SAMPLING_EPS = 1e-6
 
 
+class TokenHistory:
+    """The accepted tokens of a request, in order, in a growable int32 buffer (list-like: append, len, iteration,
+    indexing, equality with a list). `array()` is a view of the filled part, which the packing step reads without
+    converting a Python list every step. Ids are checked to lie in [0, 2^31) when appended."""
+
+    __slots__ = ("_buf", "_n")
+
+    def __init__(self, tokens=()):
+        a = np.asarray(list(tokens) if not isinstance(tokens, np.ndarray) else tokens, dtype=np.int64).reshape(-1)
+        if a.size and (a.min() < 0 or a.max() >= 2**31):
+            raise ValueError("token ids must lie in [0, 2^31)")
+        self._buf = np.empty(max(64, 2 * a.size), dtype=np.int32)
+        self._buf[:a.size] = a
+        self._n = int(a.size)
+
+    def append(self, tok):
+        tok = int(tok)
+        if tok < 0 or tok >= 2**31:
+            raise ValueError("token ids must lie in [0, 2^31)")
+        if self._n == self._buf.size:
+            nb = np.empty(2 * self._buf.size, dtype=np.int32)
+            nb[:self._n] = self._buf[:self._n]
+            self._buf = nb
+        self._buf[self._n] = tok
+        self._n += 1
+
+    def array(self) -> np.ndarray:
+        return self._buf[:self._n]
+
+    def __array__(self, dtype=None, copy=None):
+        a = self.array()
+        return a.astype(dtype) if dtype is not None else a.copy()
+
+    def __len__(self):
+        return self._n
+
+    def __iter__(self):
+        return iter(self.array().tolist())
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return self.array()[i].tolist()
+        return int(self.array()[i])
+
+    def __eq__(self, other):
+        try:
+            return list(self) == list(other)
+        except TypeError:
+            return NotImplemented
+
+    def __repr__(self):
+        return f"TokenHistory({self.array().tolist()})"
+
+
 class Budget:
     """Reasoning budget of a request (behaviour of volundr-mlx/sampler.py:18-55), written as a four-state machine.
 
@@ -90,7 +144,7 @@ class Sampler:
         seed = sp.seed if sp.seed is not None else time.time_ns() ^ ((request_id * 0x9E3779B97F4A7C15) & MASK)
         self.rng = (int(seed) | 1) & MASK
         self.counts = {}
-        self.history: list = []  # the accepted tokens, in order (the multiset behind `counts`)
+        self.history = TokenHistory()  # the accepted tokens, in order (the multiset behind `counts`)
         self.produced = 0
         self.budget = None
         self.last_logprob = None
@@ -144,12 +198,11 @@ class Sampler:
             x = torch.as_tensor(np.asarray(x, dtype=np.float32)).cuda()
         rng0 = self.rng
         u = self.uniform() if not self.sp.greedy else 0.0
-        out = _sample_checked(x.reshape(1, -1), [self.sp], [u], [self.history], [self.produced], [list(extra)])
-        flags = int(out.flags[0].item()) & 0xFFFFFFFF
-        if flags & OUT_NOFINITE:  # sampler.py:131-132 returns before drawing (:154): the generator is not advanced
-            self.rng = rng0
-        self.last_logprob = float(out.logprobs[0].item())
-        return int(out.ids[0].item())
+        _, host = _sample_checked(x.reshape(1, -1), [self.sp], [u], [self.history], [self.produced], [list(extra)])
+        if int(host[2, 0].view(np.uint32)) & OUT_NOFINITE:  # sampler.py:131-132 returns before drawing (:154)
+            self.rng = rng0  # the generator is not advanced
+        self.last_logprob = float(host[1, 0].view(np.float32))
+        return int(host[0, 0])
 
 
 def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
@@ -158,20 +211,21 @@ def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
     it is repeated once with a cooperative launch, which makes every workgroup resident together; a second timeout
     raises VsError."""
     out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
-    if not any((int(f) & 0xFFFFFFFF) & OUT_TIMEOUT for f in out.flags.cpu().tolist()):
-        return out
+    host = out.block.cpu().numpy()  # ids, logprobs (as int32 bits), flags, keep: one copy
+    if not (host[2].view(np.uint32) & OUT_TIMEOUT).any():
+        return out, host
     L = _lib.load()
     ops.reset_workspace(logits.device)
     L.vs_set_cooperative(1)
     try:
         out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
-        flags = out.flags.cpu().tolist()
+        host = out.block.cpu().numpy()
     finally:
         L.vs_set_cooperative(0)
-    if any((int(f) & 0xFFFFFFFF) & OUT_TIMEOUT for f in flags):
+    if (host[2].view(np.uint32) & OUT_TIMEOUT).any():
         ops.reset_workspace(logits.device)
         raise VsError("vs_sample_batch: an inter-workgroup wait timed out, also under a cooperative launch")
-    return out
+    return out, host
 
 
 def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Optional[Sequence[int]] = None):
@@ -199,13 +253,18 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
         extras.append(list(extra))
         avv.append(s.vv if argmax_only else None)
     if todo:
-        sub = logits[[rows[i] for i in todo]]
-        out = _sample_checked(sub, sps, us, hists, prods, extras, argmax_vv=avv)
-        ids = out.ids.cpu().tolist()
-        lps = out.logprobs.cpu().tolist()
-        fl = out.flags.cpu().tolist()
+        sel = [rows[i] for i in todo]
+        step = sel[1] - sel[0] if len(sel) > 1 else 1
+        if step > 0 and sel == list(range(sel[0], sel[-1] + 1, step)):
+            sub = logits[sel[0]:sel[-1] + 1:step]  # evenly spaced rows: a strided view, no gather copy
+        else:
+            sub = logits[sel]
+        _, host = _sample_checked(sub, sps, us, hists, prods, extras, argmax_vv=avv)
+        ids = host[0].tolist()
+        lps = host[1].view(np.float32).tolist()
+        fl = host[2].view(np.uint32).tolist()
         for k, i in enumerate(todo):
-            if (fl[k] & 0xFFFFFFFF) & OUT_NOFINITE:
+            if fl[k] & OUT_NOFINITE:
                 samplers[i].rng = rng0[k]  # no draw consumed (sampler.py:131-132)
             samplers[i].last_logprob = lps[k]
             samplers[i].accept(ids[k])

@@ -18,6 +18,7 @@ import torch
 from . import _lib
 from ._lib import STATE_DTYPE, check
 from .ops import _DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, pack_rows, workspace
+from .sampler import TokenHistory
 
 
 class DeviceSamplers:
@@ -124,7 +125,7 @@ class DeviceSamplers:
             off, n = int(st[r]["hist_off"]), int(st[r]["hist_len"])
             h = [int(t) for t in pool[off:off + n]]
             s.rng = int(st[r]["rng"])
-            s.history = h
+            s.history = TokenHistory(h)
             s.counts = {}
             for t in h:
                 s.counts[t] = s.counts.get(t, 0) + 1
