@@ -450,6 +450,15 @@ __device__ __forceinline__ u64 block_kth(const Smem& s, const u64* keys, int n, 
   }
 }
 
+// Logarithms of the logprob formulas in float32 (the result is a float32 logprob; float log and log1p are
+// accurate to a few float ulps, far inside its tolerance), in the forms that keep relative accuracy:
+// log(z) for z >= 1 as log1p(z - 1), and log(p / z) for 0 < p <= z as log1p((p - z) / z) when p >= z / 2 (the
+// difference is exact) or log(p / z) below.
+__device__ __forceinline__ double log_ge1(double z) { return (double)log1pf((float)(z - 1.0)); }
+__device__ __forceinline__ double log_ratio(double p, double z) {
+  return p >= 0.5 * z ? (double)log1pf((float)((p - z) / z)) : (double)logf((float)(p / z));
+}
+
 struct Final {
   int32_t token;
   float lp;
@@ -483,15 +492,13 @@ __device__ __forceinline__ void wave_sample_em(const Smem& s, const u64* a, int 
         ls += pr[q];
       }
     }
-    const double S = wave_sum(ls);  // :143
+    // one scan gives both the total (:143) and each lane's cumulative mass before its first position
+    const double incl = wave_scan(ls);
+    const double S = lane_bcast(incl, WAVE - 1);
     VS_TRX(40);
-    double lp = 0.0;
 #pragma unroll
-    for (int q = 0; q < EM; ++q) {
-      pr[q] = pr[q] / S;
-      lp += pr[q];
-    }
-    const double base = wave_scan(lp) - lp;  // cumulative mass before this lane's first position
+    for (int q = 0; q < EM; ++q) pr[q] = pr[q] / S;
+    const double base = (incl - ls) / S;
     VS_TRX(41);
     int keep = n;
     uint32_t flags = 0;
@@ -530,11 +537,15 @@ __device__ __forceinline__ void wave_sample_em(const Smem& s, const u64* a, int 
       keep = keep < cnt ? keep : cnt;
     }
     VS_TRX(42);
-    double lz = 0.0;
+    double z;  // :153, the cumulative mass through the last kept position (read from the lane that holds it)
+    {
+      const int owner = (keep - 1) / E, qq = keep - 1 - owner * E;
+      double cz = base;
 #pragma unroll
-    for (int q = 0; q < EM; ++q)
-      if (q < E && i0 + q < keep) lz += pr[q];
-    const double z = wave_sum(lz);  // :153
+      for (int q = 0; q < EM; ++q)
+        if (q <= qq && q < E) cz += pr[q];
+      z = lane_bcast(cz, owner);
+    }
     const double uz = P.u * z;      // :154
     double c = base;
     int hit = -1;
@@ -577,7 +588,7 @@ __device__ __forceinline__ void wave_sample_em(const Smem& s, const u64* a, int 
       s.misc[1] = (int)key_index(a[j]);
       s.misc[2] = keep;
       s.misc[3] = (int)flags;
-      s.redf[0] = log(hp / z);
+      s.redf[0] = log_ratio(hp, z);
     }
   }
 }
@@ -2439,7 +2450,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               // The draw range and the top-p bin are in the gathered set by construction (their coarse bins were
               // selected from bounds on z); a miss would be a defect, reported as an invalid row.
               fin.token = (int32_t)key_index(pd.key);
-              fin.lp = (float)((double)d - log(zf));
+              fin.lp = (float)((double)d - log_ge1(zf));
               fin.keep = keep;
               fin.flags = good && pd.key != 0 ? flags : VS_OUT_TIMEOUT;
               VS_TR(A, 8);
@@ -2641,7 +2652,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                       if (fabs(before - tgt_d) < tol || fabs(before + (double)pd.fix - tgt_d) < tol)
                         flags |= VS_OUT_DRAW_BOUNDARY;
                       fin.token = (int32_t)key_index(pd.key);
-                      fin.lp = (float)((double)d - log(zf));
+                      fin.lp = (float)((double)d - log_ge1(zf));
                       fin.keep = keep;
                       fin.flags = flags;
                       VS_TR(A, 8);
@@ -2775,7 +2786,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   if (fabs(before - tgt_d) < tol || fabs(before + (double)pd.fix - tgt_d) < tol)
                     flags |= VS_OUT_DRAW_BOUNDARY;
                   fin.token = (int32_t)key_index(pd.key);
-                  fin.lp = (float)((double)d - log(zf));
+                  fin.lp = (float)((double)d - log_ge1(zf));
                   fin.keep = keep;
                   fin.flags = flags;
                   VS_TR(A, 8);
@@ -2938,7 +2949,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 if (ok) {
                   const float d = key_value(bsel.key) / tt - xs0;
                   fin.token = (int32_t)key_index(bsel.key);
-                  fin.lp = (float)((double)d - log(zf));
+                  fin.lp = (float)((double)d - log_ge1(zf));
                   fin.keep = keep;
                   const double tol = 1e-6 * (double)zfix;
                   if (fabs((double)bsel.fix_before - tgt) < tol ||
