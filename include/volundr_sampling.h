@@ -212,9 +212,11 @@ int vs_set_spin_limit(unsigned polls);
 
 /* Testing flags for later calls of the process (0 restores the default behaviour). VS_DEBUG_FORCE_RADIX: rows of
  * the FULL class (top-k off or above 256) with large kept sets resolve top-p and the draw with the cooperative radix
- * select, the fallback otherwise reached only with min-p or with value bins too full to refine. No counterpart in
+ * select, the fallback otherwise reached only with min-p or with value bins too full to refine.
+ * VS_DEBUG_SPIN_LATER_BARRIERS: the spin limit of vs_set_spin_limit applies only from a row's second barrier on, so
+ * that every workgroup passes the first and some give up at a later one while others pass it. No counterpart in
  * the reference. */
-enum { VS_DEBUG_FORCE_RADIX = 1u };
+enum { VS_DEBUG_FORCE_RADIX = 1u, VS_DEBUG_SPIN_LATER_BARRIERS = 2u };
 int vs_set_debug(unsigned flags);
 
 /* on != 0: later sampling calls of the process launch cooperatively (every workgroup of the grid resident at once,

@@ -104,3 +104,80 @@ def test_device_state_not_committed_for_timed_out_rows(dev):
             assert st1[r]["produced"] == st0[r]["produced"] + 1, r
     out2 = ds.step(x)  # the next step runs normally
     assert not any(f & OUT_TIMEOUT for f in _flags(out2))
+
+
+def _forced_later(fn, debug=0):
+    """fn under a one-poll spin limit that spares each row's first barrier: every workgroup passes it, then at a
+    later barrier the early arrivals give up while the last one passes and goes on alone."""
+    L = _lib.load()
+    L.vs_set_spin_limit(1)
+    L.vs_set_debug(_lib.DEBUG_SPIN_LATER_BARRIERS | debug)
+    try:
+        r = fn()
+        torch.cuda.synchronize()
+    finally:
+        L.vs_set_spin_limit(0)
+        L.vs_set_debug(0)
+    return r
+
+
+def _near_flat_rows(seed, B=2, V=163840):
+    g = np.random.default_rng(seed)
+    x = (g.standard_normal((B, V)) * 0.1).astype(np.float32)
+    sps = [Sampling(temperature=1.0, top_p=0.95), Sampling(temperature=0.8, top_p=0.9)][:B]
+    return x, sps, g.random(B)
+
+
+@pytest.mark.parametrize("case", ["c5", "b1_near_flat", "b2_near_flat", "c5_radix"])
+def test_timeout_after_a_passed_barrier_flags_the_row(dev, case):
+    """A workgroup that gives up at a later row barrier skips the work after it (the gathers that the row's last
+    workgroup resolves, the later radix rounds): the row must come back flagged VS_OUT_TIMEOUT, never as a token
+    resolved from partial data or as an unwritten result, and the workspace must be left clean."""
+    debug = 0
+    if case.startswith("c5"):
+        d = synth.CONFIGS["c5"](seed=4)
+        xn, sps, u, hists = d["logits"], d["params"], d["u"], d["hists"]
+        debug = _lib.DEBUG_FORCE_RADIX if case == "c5_radix" else 0
+    else:
+        xn, sps, u = _near_flat_rows(5, B=1 if case.startswith("b1") else 2)
+        hists = None
+    x = torch.from_numpy(xn).to(dev)
+    rows = ops.pack_rows(sps, u, x.shape[1], hists).to(dev)
+    L = _lib.load()
+    L.vs_set_debug(debug)
+    try:
+        clean = ops.sample_rows(x, rows)
+        ids0, lp0, k0, fl0 = clean.ids.cpu().tolist(), clean.logprobs.cpu().tolist(), clean.keep.cpu().tolist(), _flags(clean)
+    finally:
+        L.vs_set_debug(0)
+    assert not any(f & OUT_TIMEOUT for f in fl0)
+    for rep in range(3):
+        print(f"[timeout] later-barrier forced run, {case} rep {rep}", flush=True)
+        out = ops.alloc_out(x.shape[0], dev)
+        out.ids.fill_(-7)  # a result the kernel did not write shows as -7
+        out.flags.fill_(0)
+        t = _forced_later(lambda: ops.sample_rows(x, rows, out), debug)
+        fl, ids = _flags(t), t.ids.cpu().tolist()
+        lps, keep = t.logprobs.cpu().tolist(), t.keep.cpu().tolist()
+        print(f"[timeout]   flagged rows {sum(bool(f & OUT_TIMEOUT) for f in fl)} of {len(fl)}", flush=True)
+        for r in range(len(fl)):
+            assert ids[r] != -7, f"row {r}: no result written"
+            if not fl[r] & OUT_TIMEOUT:
+                assert (ids[r], lps[r], keep[r]) == (ids0[r], lp0[r], k0[r]), f"row {r}: unflagged wrong result"
+        L.vs_set_debug(debug)
+        try:
+            again = ops.sample_rows(x, rows)  # no reset: the forced run left the workspace zeroed
+            assert again.ids.cpu().tolist() == ids0 and again.logprobs.cpu().tolist() == lp0
+        finally:
+            L.vs_set_debug(0)
+
+
+def test_sampler_retry_after_a_later_barrier_timeout(dev):
+    sp = Sampling(temperature=0.8, top_p=0.9)
+    x = torch.randn(163840, generator=torch.Generator().manual_seed(2)).to(dev)
+    a = Sampler(sp, vocab_valid=163840, request_id=3)
+    b = Sampler(sp, vocab_valid=163840, request_id=3)
+    b.rng = a.rng
+    want = a.sample(x)
+    got = _forced_later(lambda: b.sample(x))
+    assert got == want and b.last_logprob == a.last_logprob and b.rng == a.rng

@@ -67,7 +67,7 @@ struct RowCtl {
   uint32_t mcnt;    // min-p kept count
   u64 mfix;         // min-p kept fixed-point mass
   double mf64;      // min-p kept float64 mass
-  uint32_t err;     // a workgroup of the row timed out
+  uint32_t err;     // bit 0: a workgroup of the row timed out; bit 1: workgroup 0 wrote the row's result
   uint32_t nminkey; // ~ord32 of the smallest finite logit (max-reduced)
   uint32_t g2count; // second gather reservations
   uint32_t gmax;    // largest per-workgroup kept count
@@ -1685,6 +1685,23 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   }
 
   // =================================== FULL class ===================================
+  // A workgroup that gives up at a row barrier skips everything after it. Work done after a barrier that every
+  // workgroup contributes to (the gathers resolved by the row's last workgroup) is then incomplete, so the last
+  // workgroup reports the row as timed out instead of resolving it (the host repeats the call cooperatively).
+  // polls allowed at the row's nb-th barrier (the testing flag exempts the first)
+  auto bar_limit = [&](uint32_t nb) -> uint32_t {
+    return ((A.debug & VS_DEBUG_SPIN_LATER_BARRIERS) && nb < 2) ? (1u << 21) : A.spin_limit;
+  };
+  auto timed_out_final = [&]() {
+    Final f;
+    f.token = -1;
+    f.lp = 0.0f;
+    f.flags = VS_OUT_TIMEOUT;
+    f.keep = 0;
+    write_out(A, row, f, st, rng_next);
+    __syncthreads();
+    cleanup(MAX_ROUNDS);
+  };
   // ---- row statistics: finite count, largest and smallest finite logit, np.argmax key ----
   uint32_t lane_mk = 0;  // ord32 of this lane's largest finite logit, 0 when it has none
   {
@@ -1742,7 +1759,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   VS_TR(A, 22);
 #endif
   ++nbar;
-  ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+  ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
   VS_TR(A, 3);
   VS_TRC(A, 31);
   Final fin;
@@ -1786,7 +1803,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           HistSlot* hs = hslots + slot;
           if (t < NBIN && s.hc[t]) atomicAdd(&hs->cnt[t], s.hc[t]);
           ++nbar;
-          ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+          ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
           if (!ok) break;
           if (t < NBIN) {
             s.hc[t] = ld_relaxed(&hs->cnt[t]);
@@ -2047,7 +2064,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (!zfix_only) unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
         }
         ++nbar;
-        ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+        ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
         if (ok) {
           const int total = (int)ld_relaxed(&ctl->gcount);
           const int gmax = (int)ld_relaxed(&ctl->gmax);
@@ -2212,6 +2229,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               g0_writes = false;
               VS_TR(A, 6);
               if (!arrive_done()) {
+                VS_TR_FLUSH(A);
+                return;
+              }
+              if (ld_relaxed(&ctl->err) & 1u) {  // a workgroup timed out and gathered nothing
+                timed_out_final();
                 VS_TR_FLUSH(A);
                 return;
               }
@@ -2500,7 +2522,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               VS_TR(A, 16);
               ++nbar;
-              ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+              ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
               VS_TR(A, 18);
               if (ok) {
                 for (int i = t; i < ns * NBIN; i += SNT) {
@@ -2590,6 +2612,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     VS_TR_FLUSH(A);
                     return;
                   }  // the last workgroup of the row resolves the exact positions
+                  if (ld_relaxed(&ctl->err) & 1u) {  // a workgroup timed out and gathered nothing
+                    timed_out_final();
+                    VS_TR_FLUSH(A);
+                    return;
+                  }
                   VS_TR(A, 7);
                   // ---- final: exact key order inside the located fine bins ----
                   const int m = (int)ld_relaxed(&ctl->g2count);
@@ -2819,7 +2846,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               atomicMax(&hr->mk[t], s.hmk[t]);
             }
             ++nbar;
-            ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+            ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
             if (ok) {
               auto load_slot = [&](HistSlot* hs) {
                 if (t < NBIN) {
@@ -2879,7 +2906,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     atomicMax(&hs->mk[t], s.hmk[t]);
                   }
                   ++nbar;
-                  ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+                  ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
                   if (!ok) return r;
                   load_slot(hs);
                 }
@@ -2927,7 +2954,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   unsafeAtomicAdd(&ctl->mf64, mff);
                 }
                 ++nbar;
-                ok = row_barrier(&ctl->bar, nbar * G, A.spin_limit, &s.misc[11]);
+                ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
                 if (ok) {
                   const int cm = (int)ld_relaxed(&ctl->mcnt);
                   const int km = cm > 1 ? cm : 1;
@@ -2968,12 +2995,23 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #undef FOR_XV
 #undef FOR_XV4
   VS_TR(A, 9);
-  // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree.
-  if (g == 0 && g0_writes) write_out(A, row, fin, st, rng_next);
+  // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree. Its
+  // result is complete even when another workgroup timed out at the last barrier (everything it reads was
+  // published before that barrier).
+  if (g == 0 && g0_writes) {
+    write_out(A, row, fin, st, rng_next);
+    if (t == 0) atomicOr(&ctl->err, 2u);
+  }
   if (!ok && t == 0) atomicOr(&ctl->err, 1u);  // a timed-out row clears every histogram slot
   if (arrive_done()) {
-    const bool err = ld_relaxed(&ctl->err) != 0;
-    cleanup(err ? MAX_ROUNDS : slot);
+    const uint32_t err = ld_relaxed(&ctl->err);
+    if ((err & 3u) == 1u) {
+      // a workgroup timed out and nobody wrote the row's result: the others took a gather path and left its
+      // resolution to the last workgroup, which is this timed-out one
+      timed_out_final();
+    } else {
+      cleanup((err & 1u) ? MAX_ROUNDS : slot);
+    }
   }
   VS_TR_FLUSH(A);
 #undef FOR_ELEMS

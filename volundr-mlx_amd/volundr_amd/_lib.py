@@ -25,6 +25,7 @@ OUT_GATHER = 1 << 6
 OUT_HIST_FULL = 1 << 7
 OUT_TIMEOUT = 1 << 31
 DEBUG_FORCE_RADIX = 1
+DEBUG_SPIN_LATER_BARRIERS = 2
 
 # vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([

@@ -38,6 +38,25 @@ def workspace(dev: torch.device, nbytes: int, kind: str = "sample") -> torch.Ten
         return w
 
 
+_stage_lock = threading.Lock()
+_stage: dict = {}
+
+
+def _staging(dev: torch.device, nbytes: int):
+    """A pinned host buffer of >= nbytes for uploads to `dev` (one per device, reused; the caller holds
+    _stage_lock from here until its copy is issued and recorded): waits until the copy that last read it has
+    finished, so the caller may overwrite it. Returns the [buffer, event] entry."""
+    ent = _stage.get(dev.index)
+    if ent is None or ent[0].numel() < nbytes:
+        if ent is not None and ent[1] is not None:
+            ent[1].synchronize()
+        ent = [torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True), None]
+        _stage[dev.index] = ent
+    if ent[1] is not None:
+        ent[1].synchronize()
+    return ent
+
+
 def reset_workspace(dev: torch.device, kind: str = "sample"):
     """Re-zero a workspace of (device, current stream), e.g. after a row reported VS_OUT_TIMEOUT."""
     key = (dev.index, _stream_handle(dev), kind)
@@ -84,10 +103,18 @@ class PackedRows:
         for p in parts:
             offs.append(n)
             n += (p.size + 255) // 256 * 256
-        host = np.zeros(max(n, 256), dtype=np.uint8)
-        for o, p in zip(offs, parts):
-            host[o:o + p.size] = p
-        buf = torch.from_numpy(host).to(dev)
+        n = max(n, 256)
+        dev = torch.device(dev)
+        buf = torch.empty(n, dtype=torch.uint8, device=dev)
+        with _stage_lock:
+            ent = _staging(dev, n)
+            host = ent[0].numpy()
+            for o, p in zip(offs, parts):
+                host[o:o + p.size] = p
+            buf.copy_(ent[0][:n], non_blocking=True)  # from pinned memory: asynchronous, on the current stream
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(dev))
+            ent[1] = ev  # the buffer is overwritten only once this copy has completed
 
         def view(i, dt):
             sz = parts[i].size
