@@ -363,12 +363,12 @@ __device__ __forceinline__ uint32_t ctr_add(uint32_t* p, uint32_t v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Block-wide arrival: all waves' prior device-coherent writes complete, then thread 0 bumps *ctr. Returns the old
-// counter value in every thread (through *lds).
-__device__ __forceinline__ uint32_t block_arrive(uint32_t* ctr, uint32_t* lds) {
+// Block-wide arrival: all waves' prior device-coherent writes complete, then thread 0 adds `add` to *ctr. Returns
+// the old counter value in every thread (through *lds).
+__device__ __forceinline__ uint32_t block_arrive(uint32_t* ctr, uint32_t* lds, uint32_t add = 1u) {
   publish_wait();
   __syncthreads();
-  if (threadIdx.x == 0) *lds = ctr_add(ctr, 1u);
+  if (threadIdx.x == 0) *lds = ctr_add(ctr, add);
   __syncthreads();
   const uint32_t old = *lds;
   __syncthreads();

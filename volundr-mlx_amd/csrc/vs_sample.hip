@@ -59,7 +59,8 @@ enum RowClass { CLS_GREEDY = 0, CLS_TOPK = 1, CLS_FULL = 2 };
 // Per-row control block; all zero between calls.
 struct RowCtl {
   uint32_t bar;     // spin-barrier arrivals
-  uint32_t done;    // workgroups finished
+  uint32_t done;    // workgroups finished (bits 0-15), of them the one that wrote the row's result (bits
+                    // 16-23) and those that timed out at a row barrier (bits 24-31)
   uint32_t nfin;    // finite count of the row
   uint32_t mkey;    // ord32 of the largest finite logit
   u64 amkey;        // np.argmax key of the row
@@ -67,7 +68,7 @@ struct RowCtl {
   uint32_t mcnt;    // min-p kept count
   u64 mfix;         // min-p kept fixed-point mass
   double mf64;      // min-p kept float64 mass
-  uint32_t err;     // bit 0: a workgroup of the row timed out; bit 1: workgroup 0 wrote the row's result
+  uint32_t spare;   // kept zero
   uint32_t nminkey; // ~ord32 of the smallest finite logit (max-reduced)
   uint32_t g2count; // second gather reservations
   uint32_t gmax;    // largest per-workgroup kept count
@@ -1212,8 +1213,14 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 
   // Arrive at the row's done counter; true in the last workgroup of the row.
   auto arrive_done = [&]() -> bool { return block_arrive(&ctl->done, (uint32_t*)&s.misc[8]) == (uint32_t)(G - 1); };
+  // FULL rows: the arrival also reports whether this workgroup wrote the row's result and whether it timed out;
+  // returns the counter before it
+  auto arrive_full = [&](bool wrote, bool timed_out) -> uint32_t {
+    return block_arrive(&ctl->done, (uint32_t*)&s.misc[8], 1u + (wrote ? 1u << 16 : 0u) + (timed_out ? 1u << 24 : 0u));
+  };
   auto cleanup = [&](int nrounds) {
     // Only the last workgroup of the row gets here: restore the all-zero state of the row's workspace.
+#pragma nounroll
     for (int r = 0; r < nrounds; ++r) {
       HistSlot* hs = hslots + r;
       if (t < NBIN) {
@@ -2228,14 +2235,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               g0_writes = false;
               VS_TR(A, 6);
-              if (!arrive_done()) {
-                VS_TR_FLUSH(A);
-                return;
-              }
-              if (ld_relaxed(&ctl->err) & 1u) {  // a workgroup timed out and gathered nothing
-                timed_out_final();
-                VS_TR_FLUSH(A);
-                return;
+              {
+                const uint32_t old = arrive_full(false, false);
+                if ((old & 0xFFFFu) != (uint32_t)(G - 1)) {
+                  VS_TR_FLUSH(A);
+                  return;
+                }
+                if (old >> 24) {  // a workgroup timed out and gathered nothing
+                  timed_out_final();
+                  VS_TR_FLUSH(A);
+                  return;
+                }
               }
               VS_TR(A, 7);
               // ---- final (last workgroup of the row): the gathered keys go to the chunk area, are histogrammed by
@@ -2608,14 +2618,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   for (int i = t; i < nloc; i += SNT) st_dev(&gather[s.misc[17] + i], s.keys[i]);
                   g0_writes = false;
                   VS_TR(A, 6);
-                  if (!arrive_done()) {
-                    VS_TR_FLUSH(A);
-                    return;
-                  }  // the last workgroup of the row resolves the exact positions
-                  if (ld_relaxed(&ctl->err) & 1u) {  // a workgroup timed out and gathered nothing
-                    timed_out_final();
-                    VS_TR_FLUSH(A);
-                    return;
+                  {  // the last workgroup of the row resolves the exact positions
+                    const uint32_t old = arrive_full(false, false);
+                    if ((old & 0xFFFFu) != (uint32_t)(G - 1)) {
+                      VS_TR_FLUSH(A);
+                      return;
+                    }
+                    if (old >> 24) {  // a workgroup timed out and gathered nothing
+                      timed_out_final();
+                      VS_TR_FLUSH(A);
+                      return;
+                    }
                   }
                   VS_TR(A, 7);
                   // ---- final: exact key order inside the located fine bins ----
@@ -2998,19 +3011,17 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   // In the small-gather case only workgroup 0 computed `fin`; in the radix and no-finite cases all agree. Its
   // result is complete even when another workgroup timed out at the last barrier (everything it reads was
   // published before that barrier).
-  if (g == 0 && g0_writes) {
-    write_out(A, row, fin, st, rng_next);
-    if (t == 0) atomicOr(&ctl->err, 2u);
-  }
-  if (!ok && t == 0) atomicOr(&ctl->err, 1u);  // a timed-out row clears every histogram slot
-  if (arrive_done()) {
-    const uint32_t err = ld_relaxed(&ctl->err);
-    if ((err & 3u) == 1u) {
+  const bool wrote = g == 0 && g0_writes;
+  if (wrote) write_out(A, row, fin, st, rng_next);
+  const uint32_t old = arrive_full(wrote, !ok);
+  if ((old & 0xFFFFu) == (uint32_t)(G - 1)) {
+    const bool any_timeout = !ok || (old >> 24) != 0;
+    if (any_timeout && !wrote && ((old >> 16) & 0xFFu) == 0) {
       // a workgroup timed out and nobody wrote the row's result: the others took a gather path and left its
       // resolution to the last workgroup, which is this timed-out one
       timed_out_final();
     } else {
-      cleanup((err & 1u) ? MAX_ROUNDS : slot);
+      cleanup(any_timeout ? MAX_ROUNDS : slot);  // a timed-out row clears every histogram slot
     }
   }
   VS_TR_FLUSH(A);
