@@ -327,6 +327,23 @@ def test_deterministic(dev):
     assert torch.equal(a.ids, b.ids) and torch.equal(a.keep, b.keep)
 
 
+@pytest.mark.parametrize("B", [1, 2, 16])
+def test_repeated_calls_identical(dev, B):
+    """Every workgroup order the hardware picks gives the same bits: FULL rows through the value-bin and gather
+    paths (B = 1 uses 64 workgroups per row, B = 16 uses 16), repeated 25 times against the first call."""
+    g = np.random.default_rng(40 + B)
+    x = torch.from_numpy((g.standard_normal((B, 163840)) * np.where(np.arange(B) % 2, 1.0, 0.1)[:, None])
+                         .astype(np.float32)).to(dev)
+    ps = [Sampling(temperature=0.8 if r % 3 else 1.0, top_p=(0.9, 0.95, 1.0)[r % 3]) for r in range(B)]
+    u = g.random(B)
+    first = sample_batch(x, ps, u)
+    want = (first.ids.cpu(), first.logprobs.cpu(), first.keep.cpu(), first.flags.cpu())
+    for rep in range(25):
+        o = sample_batch(x, ps, u)
+        got = (o.ids.cpu(), o.logprobs.cpu(), o.keep.cpu(), o.flags.cpu())
+        assert all(torch.equal(a, b) for a, b in zip(got, want)), f"call {rep + 2} differs"
+
+
 @pytest.mark.parametrize("name", ["c1", "c3", "c5"])
 def test_configs_full_size(dev, name):
     d = synth.CONFIGS[name](seed=0)
