@@ -128,7 +128,22 @@ def _near_flat_rows(seed, B=2, V=163840):
     return x, sps, g.random(B)
 
 
-@pytest.mark.parametrize("case", ["c5", "b1_near_flat", "b2_near_flat", "c5_radix"])
+def _other_paths(case, V=163840):
+    g = np.random.default_rng(11)
+    if case == "topk_radix":  # top-k above the list class: a cooperative radix select over row barriers
+        x = (g.standard_normal((2, V)) * 0.1).astype(np.float32)
+        sps = [Sampling(top_k=3000, top_p=0.9), Sampling(top_k=1000)]
+    elif case == "min_p":  # min-p on a large kept set: the radix path
+        x = (g.standard_normal((2, V)) * 0.5).astype(np.float32)
+        sps = [Sampling(min_p=0.2), Sampling(min_p=0.5, top_p=0.9)]
+    else:  # heavy-tailed rows whose kept sets are small: gathered before the second barrier
+        x = (g.standard_t(3, (2, V)) * 3.0).astype(np.float32)
+        sps = [Sampling(top_p=0.9), Sampling(temperature=0.7)]
+    return x, sps, g.random(2)
+
+
+@pytest.mark.parametrize("case", ["c5", "b1_near_flat", "b2_near_flat", "c5_radix", "topk_radix", "min_p",
+                                  "small_kept"])
 def test_timeout_after_a_passed_barrier_flags_the_row(dev, case):
     """A workgroup that gives up at a later row barrier skips the work after it (the gathers that the row's last
     workgroup resolves, the later radix rounds): the row must come back flagged VS_OUT_TIMEOUT, never as a token
@@ -138,8 +153,11 @@ def test_timeout_after_a_passed_barrier_flags_the_row(dev, case):
         d = synth.CONFIGS["c5"](seed=4)
         xn, sps, u, hists = d["logits"], d["params"], d["u"], d["hists"]
         debug = _lib.DEBUG_FORCE_RADIX if case == "c5_radix" else 0
-    else:
+    elif "near_flat" in case:
         xn, sps, u = _near_flat_rows(5, B=1 if case.startswith("b1") else 2)
+        hists = None
+    else:
+        xn, sps, u = _other_paths(case)
         hists = None
     x = torch.from_numpy(xn).to(dev)
     rows = ops.pack_rows(sps, u, x.shape[1], hists).to(dev)
