@@ -199,3 +199,36 @@ def test_sampler_retry_after_a_later_barrier_timeout(dev):
     want = a.sample(x)
     got = _forced_later(lambda: b.sample(x))
     assert got == want and b.last_logprob == a.last_logprob and b.rng == a.rng
+
+
+def test_device_state_after_a_later_barrier_timeout(dev):
+    """The state entry point under later-barrier timeouts (C5 rows: value bins and gathers): a flagged row commits
+    nothing, an unflagged row commits exactly the token an unforced step commits."""
+    d = synth.CONFIGS["c5"](seed=6)
+    B, V = d["logits"].shape
+    x = torch.from_numpy(d["logits"]).to(dev)
+
+    def fresh():
+        ss = []
+        for r, sp in enumerate(d["params"]):
+            s = Sampler(sp, vocab_valid=V, request_id=r)
+            s.rng = 0x7654321 ^ r
+            ss.append(s)
+        return DeviceSamplers(ss, V, hist_cap=64, device=dev)
+
+    ref = fresh()
+    want = ref.step(x).ids.cpu().tolist()
+    st_want = ref.host_state().copy()
+    ds = fresh()
+    st0 = ds.host_state().copy()
+    out = _forced_later(lambda: ds.step(x))
+    fl, ids = _flags(out), out.ids.cpu().tolist()
+    st1 = ds.host_state()
+    print(f"[timeout] state rows flagged {sum(bool(f & OUT_TIMEOUT) for f in fl)} of {B}", flush=True)
+    for r in range(B):
+        if fl[r] & OUT_TIMEOUT:
+            assert st1[r]["produced"] == st0[r]["produced"] and st1[r]["rng"] == st0[r]["rng"], r
+            assert st1[r]["hist_len"] == st0[r]["hist_len"], r
+        else:
+            assert ids[r] == want[r], r
+            assert st1[r]["rng"] == st_want[r]["rng"] and st1[r]["hist_len"] == st_want[r]["hist_len"], r
