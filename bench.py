@@ -325,7 +325,10 @@ def boundary_rows(d, out):
 
 
 def cpu_baseline(d, budget_s=10.0):
-    """The oracle (NumPy restatement of sampler.py) row by row, single-threaded, for about budget_s seconds."""
+    """The reference's algorithm on the host, single-threaded, for about budget_s seconds: sampler.py:100-156 as
+    written there (np.argpartition for top-k rows, lexsort, float64 exp / cumsum / searchsorted; the restatement
+    oracle.sampler_ref.sample_plain), row by row as scheduler.py:424 calls it, with each request's counts dict built
+    outside the timed loop (the reference keeps it across steps)."""
     from oracle import sampler_ref as S
 
     B = d["logits"].shape[0]
@@ -334,14 +337,16 @@ def cpu_baseline(d, budget_s=10.0):
     t0 = time.perf_counter()
     while True:
         for i in range(B):
-            S.sample(d["logits"][i], d["params"][i], float(d["u"][i]), counts[i])
+            S.sample_plain(d["logits"][i], d["params"][i], float(d["u"][i]), counts[i])
         n += 1
         if time.perf_counter() - t0 > budget_s:
             break
     dt = (time.perf_counter() - t0) / n
     return {"value": round(dt * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"{n} passes over the {B} rows of the same synthetic batch (counts built outside the timed "
-                      f"loop), NumPy oracle of sampler.py:100-156, os.cpu_count()={os.cpu_count()}",
+            "sample": f"{n} passes over the {B} rows of the same synthetic batch: sampler.py:100-156 restated "
+                      f"with the reference's own NumPy calls (argpartition top-k, lexsort, exp, cumsum, "
+                      f"searchsorted), counts dicts built outside the timed loop; 1 thread, "
+                      f"os.cpu_count()={os.cpu_count()}",
             "tokens_per_s": round(B / dt, 1)}
 
 

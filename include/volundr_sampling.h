@@ -104,11 +104,12 @@ int vs_sample_batch(const void* logits, int dtype, int B, int V, int64_t ld, con
 size_t vs_sample_workspace_bytes(int B, int V);
 
 /* vs_sample_batch without a workspace argument and without any allocation: the kernels use a fixed device array
- * of vs_sample_noalloc_scratch_bytes() bytes (about 22.4 MB) in the library, one per device, kept until the process
- * ends. It covers every batch size (batches above 64 rows run as consecutive launches that reuse it); a shape whose
- * workspace would exceed it fails with VS_EWORKSPACE. The first call on a device looks the array up and zeroes it
- * (a fill kernel on `stream`); every call leaves it zeroed. All calls on one device share the array: calls that
- * overlap on one device (different streams, or threads without ordering) race and give wrong results.
+ * of vs_sample_noalloc_scratch_bytes() bytes (about 5.6 MB: 16 rows of the sampling workspace) in the library, one
+ * per device, kept until the process ends. It covers every batch size and vocabulary the library accepts (batches
+ * above 16 rows run as consecutive launches that reuse it). The array is zero when the library is loaded and every
+ * call leaves it zeroed (rows that report VS_OUT_TIMEOUT included), so no call clears it and the first call does no
+ * extra work. All calls on one device share the array: calls that overlap on one device (different streams, or
+ * threads without ordering) race and give wrong results.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). */
 int vs_sample_batch_noalloc(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
@@ -203,26 +204,29 @@ int vs_draft_propose(const void* logits, int dtype, int n, int S, int V, int64_t
 
 size_t vs_draft_workspace_bytes(int n, int S, int V);
 
-/* Polls an inter-workgroup wait of vs_sample_batch / vs_sample_batch_state makes before it gives up and flags its
- * row VS_OUT_TIMEOUT (0 restores the default, ~2M polls). A testing hook: a tiny limit forces the timeout path, whose
- * rows report VS_OUT_TIMEOUT, commit no request state and leave the workspace zeroed. Applies to later plain
- * launches of the process (cooperative launches keep the default). No counterpart in the reference (its sampler is
- * single-threaded host code). */
+/* The inter-workgroup waits of vs_sample_batch / vs_sample_batch_state (row barriers of rows with top-k off or above
+ * 256) give up after 200 us (5 ms under a cooperative launch), measured on the GPU's 100 MHz real-time counter, and
+ * flag their row VS_OUT_TIMEOUT. A testing hook: a non-zero `polls` also bounds each wait of later plain launches of
+ * the process by that many polls (0 restores the time bound alone), so a tiny limit forces the timeout path, whose
+ * rows report VS_OUT_TIMEOUT, commit no request state and leave the workspace zeroed. No counterpart in the
+ * reference (its sampler is single-threaded host code). */
 int vs_set_spin_limit(unsigned polls);
 
 /* Testing flags for later calls of the process (0 restores the default behaviour). VS_DEBUG_FORCE_RADIX: rows of
  * the FULL class (top-k off or above 256) with large kept sets resolve top-p and the draw with the cooperative radix
  * select, the fallback otherwise reached only with min-p or with value bins too full to refine.
  * VS_DEBUG_SPIN_LATER_BARRIERS: the spin limit of vs_set_spin_limit applies only from a row's second barrier on, so
- * that every workgroup passes the first and some give up at a later one while others pass it. No counterpart in
- * the reference. */
-enum { VS_DEBUG_FORCE_RADIX = 1u, VS_DEBUG_SPIN_LATER_BARRIERS = 2u };
+ * that every workgroup passes the first and some give up at a later one while others pass it.
+ * VS_DEBUG_WAIT_CLOCK: every row barrier is treated as unreachable, so each wait ends at its time bound (measures
+ * the bound; every such row reports VS_OUT_TIMEOUT). No counterpart in the reference. */
+enum { VS_DEBUG_FORCE_RADIX = 1u, VS_DEBUG_SPIN_LATER_BARRIERS = 2u, VS_DEBUG_WAIT_CLOCK = 4u };
 int vs_set_debug(unsigned flags);
 
-/* on != 0: later sampling calls of the process launch cooperatively (every workgroup of the grid resident at once,
- * so a row barrier cannot starve when other streams hold CUs; ~18 us more per call); 0: plain launches (the
- * default, unless the environment sets VS_COOPERATIVE=1). The Python layer uses it to retry a call whose rows
- * reported VS_OUT_TIMEOUT. No counterpart in the reference. */
+/* on != 0: the calling thread's later sampling calls launch cooperatively (every workgroup of the grid resident at
+ * once, so a row barrier cannot starve when other streams hold CUs; ~18 us more per call); 0: plain launches (the
+ * default, unless the environment sets VS_COOPERATIVE=1, which makes every call of the process cooperative). The
+ * setting is per thread. Returns the calling thread's previous setting (0 or 1), so a caller can restore it. The
+ * Python layer uses it to retry a call whose rows reported VS_OUT_TIMEOUT. No counterpart in the reference. */
 int vs_set_cooperative(int on);
 
 /* Launch `reps` empty kernels of `blocks` workgroups of `threads` threads with `lds_bytes` of dynamic LDS back to
@@ -236,7 +240,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 6. */
+/* Library ABI version (increments on any signature or struct change): 7. */
 int vs_version(void);
 
 #ifdef __cplusplus

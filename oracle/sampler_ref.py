@@ -177,6 +177,42 @@ def sample(x, sp, u: float, counts: Optional[dict] = None, produced: int = 0, ex
     return Result(int(idx[j]), lp, keep, draw_b, topp_b, tie)
 
 
+def sample_plain(x, sp, u: float, counts: Optional[dict] = None, produced: int = 0, extra=()) -> int:
+    """Sampler.sample (sampler.py:100-156) as the reference computes it, for timing only (bench.py's CPU baseline):
+    np.argpartition for the top-k cut (:136) instead of the stable sort of `sample`, and no boundary diagnostics.
+    Returns the token; equals `sample(...).token` except where values tie at the k-th position
+    (tests/test_oracle.py checks this)."""
+    x = preprocess(x, sp, counts or {}, produced, extra)              # :102-126
+    if sp.greedy:                                                     # :127-128
+        return int(np.argmax(x))
+    t = np.float32(sp.temperature)                                    # :129
+    idx = np.nonzero(np.isfinite(x))[0]                               # :130
+    if idx.size == 0:                                                 # :131-132
+        return int(np.argmax(x))
+    k = max(min(sp.top_k if sp.top_k else idx.size, idx.size), 1)   # :133-134
+    if k < idx.size:                                                  # :135-136
+        idx = idx[np.argpartition(-x[idx], k - 1)[:k]]
+    elif idx.size > 4096:                                             # :137-139
+        m = x[idx].max()
+        idx = idx[x[idx] / t >= m / t - 40.0]
+    idx = idx[np.lexsort((idx, -x[idx]))]                             # :140
+    xs = (x[idx] / t).astype(np.float32)                              # :141
+    pr = np.exp((xs - xs[0]).astype(np.float64))                      # :142
+    pr /= pr.sum()                                                    # :143
+    keep = pr.size                                                    # :144
+    if sp.top_p < 1.0:                                                # :145-148
+        hit = np.nonzero(np.cumsum(pr) >= sp.top_p)[0]
+        if hit.size:
+            keep = int(hit[0]) + 1
+    if sp.min_p > 0.0:                                                # :149-152
+        below = np.nonzero(pr < pr[0] * sp.min_p)[0]
+        cnt = int(below[0]) if below.size else pr.size
+        keep = min(keep, max(cnt, 1))
+    z = pr[:keep].sum()                                               # :153
+    j = int(np.searchsorted(np.cumsum(pr[:keep]), u * z, side="left"))  # :154-155
+    return int(idx[min(j, keep - 1)])                                 # :156
+
+
 def sample_batch(X, params, u, hists=None, produced=None):
     """Row-by-row application of `sample` (the way scheduler.py:416-425 calls the sampler per batch row)."""
     out = []

@@ -9,7 +9,8 @@ Reference arithmetic:
     form of volundr-mlx/spec/check_verify.py:27-30, evaluated here in float64.
 `drafts` is inp[:, 1:], shape [B, T-1].
 
-Pinning: tests/test_oracle.py checks argmax against a Python loop (strict `>` scan keeps the first maximum), the
+Pinning: tests/test_oracle.py checks emitted on hand cases and against the identity emitted == tok[:nacc+1] (the
+accepted drafts equal the argmax prefix), argmax against a Python loop (strict `>` scan keeps the first maximum), the
 accept length against the hand cases all-match -> T-1, first-mismatch -> 0, and a planted exact tie -> the lower
 index, and the logprob against math.fsum of exp on small rows. NaN handling of mx.argmax is unpinned: this oracle
 (like np.argmax) ranks NaN above every number.

@@ -133,3 +133,35 @@ def test_device_samplers_vocab_valid(dev):
     for r in range(B):
         assert int(st[r]["rng"]) == oracle[r].rng and ds.history(r) == oracle[r].gen
     assert oracle[0].gen == [7] * 6 and oracle[2].gen[0] == PAD_HOT
+
+
+@pytest.mark.parametrize("vv", [V // 3, 12289, 1])
+def test_argmax_vv_far_below_v(dev, vv):
+    """Argmax-only rows whose vocab_valid lies far below V, so that whole workgroups of the row hold no valid
+    position: NaN, +inf and the global maximum planted past vocab_valid must not leak in; the result is
+    np.argmax(x[:vv]) (sampler.py:96), for one row alone and for rows of a batch with other classes."""
+    from volundr_amd import ops
+
+    rng = np.random.default_rng(vv)
+    B = 3
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    for r in range(B):
+        x[r, vv:][rng.integers(0, V - vv, 5)] = np.nan
+        x[r, V - 1] = np.inf
+        x[r, (vv + V) // 2] = 50.0
+    x[1, :vv] = -np.inf if vv == 1 else x[1, :vv]     # vv = 1: a single -inf entry, argmax 0
+    x[2, vv - 1] = 30.0                               # the valid maximum at the last valid position
+    sps = [Sampling(temperature=0.0), Sampling(top_k=1), Sampling(temperature=0.0)]
+    print(f"[argmax vv] V={V} vv={vv}", flush=True)
+    xt = torch.from_numpy(x).to(dev)
+    rows = ops.pack_rows(sps, np.zeros(B), V, argmax_vv=[vv] * B).to(dev)
+    o = ops.sample_rows(xt, rows)
+    torch.cuda.synchronize()
+    want = [int(np.argmax(x[r, :vv])) for r in range(B)]
+    assert o.ids.cpu().tolist() == want
+    # one argmax-only row inside a batch whose other row samples the full vocabulary
+    sps2 = [Sampling(temperature=0.0), Sampling(top_k=20, temperature=0.9)]
+    rows2 = ops.pack_rows(sps2, np.array([0.0, 0.3]), V, argmax_vv=[vv, None]).to(dev)
+    o2 = ops.sample_rows(xt[:2], rows2)
+    torch.cuda.synchronize()
+    assert int(o2.ids[0].item()) == want[0]

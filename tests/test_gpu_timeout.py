@@ -232,3 +232,37 @@ def test_device_state_after_a_later_barrier_timeout(dev):
         else:
             assert ids[r] == want[r], r
             assert st1[r]["rng"] == st_want[r]["rng"] and st1[r]["hist_len"] == st_want[r]["hist_len"], r
+
+
+@pytest.mark.parametrize("coop", [0, 1])
+def test_wait_time_bound(dev, coop):
+    """The row barriers give up after a bound in wall time (the GPU's 100 MHz real-time counter): 200 us under a
+    plain launch, 5 ms under a cooperative one. The testing flag VS_DEBUG_WAIT_CLOCK makes every barrier
+    unreachable, so each FULL row waits out the bound at its first barrier and reports VS_OUT_TIMEOUT; the call's
+    duration measures the bound. The workspace is left clean for the next ordinary call."""
+    d = synth.CONFIGS["c5"](seed=4)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    rows = ops.pack_rows(d["params"], d["u"], x.shape[1], d["hists"]).to(dev)
+    clean = ops.sample_rows(x, rows)
+    ids0 = clean.ids.cpu().tolist()
+    L = _lib.load()
+    prev = L.vs_set_cooperative(coop)
+    L.vs_set_debug(_lib.DEBUG_WAIT_CLOCK)
+    try:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        print(f"[timeout] wait-clock bound, cooperative={coop}", flush=True)
+        e0.record()
+        t = ops.sample_rows(x, rows)
+        e1.record()
+        torch.cuda.synchronize()
+    finally:
+        L.vs_set_debug(0)
+        L.vs_set_cooperative(prev)
+    us = e0.elapsed_time(e1) * 1000.0
+    print(f"[timeout] wait-clock call: {us:.1f} us (cooperative={coop})", flush=True)
+    assert all(f & OUT_TIMEOUT for f in _flags(t))
+    lo, hi = (5000.0, 8000.0) if coop else (200.0, 1000.0)
+    assert lo <= us <= hi, us
+    again = ops.sample_rows(x, rows)
+    assert again.ids.cpu().tolist() == ids0
+

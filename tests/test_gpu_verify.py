@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import verify_ref as VR
-from volundr_amd import synth, verify_greedy
+from volundr_amd import emitted, synth, verify_greedy
 
 pytestmark = pytest.mark.gpu
 
@@ -33,6 +33,13 @@ def test_configs(dev, name):
     d = synth.CONFIGS[name](seed=0, tie_frac=0.2)
     o = check(dev, d["logits_bf16"], d["drafts"], 163840, torch.bfloat16, name)
     assert np.array_equal(o.accept.cpu().numpy(), d["accept"])
+    # the emitted tokens of each request (specdec.py:335-336, scheduler.py:465-470) from the device outputs
+    tok, acc, _ = VR.verify(d["logits_bf16"], d["drafts"], 163840)
+    am, ac = o.argmax.cpu().tolist(), o.accept.cpu().tolist()
+    for b in range(len(ac)):
+        got = emitted(d["drafts"][b].tolist(), am[b], ac[b])
+        assert got == VR.emitted(d["drafts"][b], tok[b], int(acc[b])), (name, b)
+        assert len(got) == ac[b] + 1
 
 
 def test_ties_and_vocab_valid(dev):

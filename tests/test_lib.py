@@ -128,3 +128,16 @@ def test_token_history_is_list_like_and_packs_like_a_list():
     for f in ("hist", "bias_ids", "bias_vals", "mask_ids"):
         assert np.array_equal(getattr(a, f), getattr(b, f))
     assert pack_rows([], [], V=10).params.size == 0
+
+
+def test_cooperative_setting_is_per_thread_and_restorable():
+    import threading
+
+    L = _lib.load()
+    assert L.vs_set_cooperative(1) == 0
+    seen = []
+    th = threading.Thread(target=lambda: seen.append(L.vs_set_cooperative(0)))
+    th.start()
+    th.join()
+    assert seen == [0]  # the other thread's own setting was still the default
+    assert L.vs_set_cooperative(0) == 1  # this thread's setting survived the other thread's call

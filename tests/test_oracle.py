@@ -145,6 +145,21 @@ def test_oracle_matches_brute_force(seed):
 
 
 # ---------------------------------------------------------------- xorshift64* (Vigna 2016)
+@pytest.mark.parametrize("seed", range(10))
+def test_plain_restatement_matches_oracle(seed):
+    """sample_plain (the reference's argpartition form, timed by bench.py's CPU baseline) picks the oracle's token
+    on random rows without ties at the k-th position, for every class of row."""
+    from volundr_amd import synth
+
+    d = synth.c3(seed=seed, V=20000, H=512) if seed % 2 else synth.c5(seed=seed, V=20000, B=4, H=2048)
+    for i in range(d["logits"].shape[0]):
+        c = S.counts_from_history(d["hists"][i])
+        r = S.sample(d["logits"][i], d["params"][i], float(d["u"][i]), c)
+        if r.topk_tie:
+            continue
+        assert S.sample_plain(d["logits"][i], d["params"][i], float(d["u"][i]), c) == r.token
+
+
 def test_xorshift64star_known_sequence():
     # state recurrence x ^= x>>12; x ^= x<<25; x ^= x>>27; output x*0x2545F4914F6CDD1D; seed 1 -> first state
     st = S.seed_state(1)
@@ -199,6 +214,42 @@ def test_verify_python_loop_brute():
                 if x[b, t, i] > x[b, t, best]:
                     best = i
             assert tok[b, t] == best
+
+
+def test_emitted_hand_cases():
+    """specdec.py:335-336 / scheduler.py:465-470: n = nacc + 1, emitted = inp[1:n] + [tok[n-1]], with inp[1:] the
+    drafts. Hand cases for the oracle's and the product's emitted."""
+    from volundr_amd.ops import emitted as em_product
+    drafts = [11, 12, 13, 14]
+    tok = [11, 12, 13, 14, 99]
+    for em in (VR.emitted, em_product):
+        assert em(drafts, tok, 4) == [11, 12, 13, 14, 99]           # all drafts accepted -> drafts + [tok[T-1]]
+        assert em(drafts, [7, 12, 13, 14, 99], 0) == [7]            # first mismatch -> [tok[0]]
+        assert em(drafts, [11, 12, 5, 14, 99], 2) == [11, 12, 5]    # nacc = k -> drafts[:k] + [tok[k]]
+        assert em([], [42], 0) == [42]                              # T = 1: the bonus token only
+        assert em(np.array(drafts, np.int32), np.array(tok, np.int32), 3) == [11, 12, 13, 14]
+
+
+def test_emitted_is_the_argmax_prefix():
+    """What the definition fixes: the nacc accepted drafts equal tok[:nacc], so the emitted tokens are exactly
+    tok[:nacc+1] of the verify argmax; length nacc + 1. Checked on random blocks with planted accept lengths."""
+    from volundr_amd.ops import emitted as em_product
+    rng = np.random.default_rng(7)
+    for trial in range(50):
+        B, T, V = 3, int(rng.integers(1, 18)), 50
+        x = rng.integers(-3, 4, size=(B, T, V)).astype(np.float32)
+        tok, _, _ = VR.verify(x, np.zeros((B, T - 1), np.int32), V)
+        drafts = tok[:, :-1].copy()
+        for b in range(B):
+            L = int(rng.integers(0, T))
+            if L < T - 1:
+                drafts[b, L] = (drafts[b, L] + 1) % V
+        tok, acc, _ = VR.verify(x, drafts, V)
+        for b in range(B):
+            n = int(acc[b])
+            want = [int(t) for t in tok[b, :n + 1]]
+            assert VR.emitted(drafts[b], tok[b], n) == want
+            assert em_product(drafts[b].tolist(), tok[b].tolist(), n) == want
 
 
 def test_bf16_bits_roundtrip():

@@ -42,7 +42,7 @@ def _compare(dev, x, samplings, u, hists, label):
 
 def test_noalloc_matches_workspace_entry(dev):
     L = _lib.load()
-    assert L.vs_sample_noalloc_scratch_bytes() >= L.vs_sample_workspace_bytes(64, 163840)
+    assert L.vs_sample_noalloc_scratch_bytes() == L.vs_sample_workspace_bytes(16, 163840)  # 16 rows, ~5.6 MB
     # first call: the C5 shape (FULL rows: row barriers, histogram slots, gathers all use the array)
     d = synth.c5(seed=1)
     x = torch.from_numpy(d["logits"]).to(dev)
@@ -58,6 +58,26 @@ def test_noalloc_matches_workspace_entry(dev):
     # and the C3 shape once more after the small call
     d = synth.c3(seed=2)
     _compare(dev, torch.from_numpy(d["logits"]).to(dev), d["params"], d["u"], d["hists"], "c3")
+
+
+def test_noalloc_timeout_leaves_the_array_zeroed(dev):
+    """Rows that give up at a row barrier (forced from the host with a one-poll spin limit, so every kernel exits
+    normally) report VS_OUT_TIMEOUT and leave the shared array zeroed: the next ordinary call through the
+    allocation-free entry point equals vs_sample_batch, with no reset (its callers have none)."""
+    L = _lib.load()
+    d = synth.c5(seed=4)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    rows = pack_rows(d["params"], d["u"], x.shape[1], d["hists"]).to(dev)
+    print("[noalloc] forced timeout, c5 seed 4", flush=True)
+    L.vs_set_spin_limit(1)
+    try:
+        t = _call("noalloc", x, rows, alloc_out(x.shape[0], dev), dev)
+        torch.cuda.synchronize()
+    finally:
+        L.vs_set_spin_limit(0)
+    flags = [int(f) & 0xFFFFFFFF for f in t.flags.cpu().tolist()]
+    assert any(f & _lib.OUT_TIMEOUT for f in flags)
+    _compare(dev, x, d["params"], d["u"], d["hists"], "c5 after timeout")
 
 
 def test_noalloc_rejects_bad_arguments(dev):

@@ -12,7 +12,7 @@ namespace vs {
 static thread_local std::string g_err;
 unsigned long long* g_trace = nullptr;
 unsigned g_spin_limit = 0;
-int g_cooperative = 0;
+thread_local int g_cooperative = 0;
 unsigned g_debug = 0;
 
 void set_error(const std::string& msg) { g_err = msg; }
@@ -66,7 +66,7 @@ int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stre
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 6; }
+int vs_version(void) { return 7; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;
@@ -79,8 +79,9 @@ int vs_set_debug(unsigned flags) {
 }
 
 int vs_set_cooperative(int on) {
+  const int prev = vs::g_cooperative;
   vs::g_cooperative = on ? 1 : 0;
-  return VS_OK;
+  return prev;
 }
 
 #ifdef VS_TRACE

@@ -375,18 +375,22 @@ __device__ __forceinline__ uint32_t block_arrive(uint32_t* ctr, uint32_t* lds, u
   return old;
 }
 
-// Wait until *ctr >= target after arriving. Thread 0 spins (bounded by `limit` polls); the whole block calls it.
-// Returns false (for every thread) when the limit was hit, so a wave can never wait forever.
-__device__ __forceinline__ bool row_barrier(uint32_t* ctr, uint32_t target, uint32_t limit, int* flag_lds) {
+// Wait until *ctr >= target after arriving. Thread 0 spins; the whole block calls it. The wait is bounded twice:
+// by `ticks` of the constant 100 MHz real-time counter (s_memrealtime, 10 ns per tick; the normal bound) and by
+// `limit` polls (a testing hook: a tiny limit forces the timeout path). Returns false (for every thread) when a
+// bound was hit, so a wave can never wait forever.
+__device__ __forceinline__ bool row_barrier(uint32_t* ctr, uint32_t target, uint32_t limit, uint64_t ticks,
+                                            int* flag_lds) {
   publish_wait();
   __syncthreads();
   if (threadIdx.x == 0) {
     ctr_add(ctr, 1u);
     uint32_t polls = 0;
     int ok = 1;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (ld_dev(ctr) < target) {
       __builtin_amdgcn_s_sleep(1);
-      if (++polls > limit) {
+      if (++polls > limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {
         ok = 0;
         break;
       }

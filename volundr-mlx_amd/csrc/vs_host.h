@@ -21,8 +21,8 @@ const DevInfo* dev_info();
 
 // Polls of an inter-workgroup wait before it gives up (0: the default). Set by vs_set_spin_limit.
 extern unsigned g_spin_limit;
-// Non-zero: sampling kernels are launched cooperatively (set by vs_set_cooperative).
-extern int g_cooperative;
+// Non-zero: the calling thread launches sampling kernels cooperatively (set by vs_set_cooperative, per thread).
+extern thread_local int g_cooperative;
 // VS_DEBUG_* testing flags (set by vs_set_debug).
 extern unsigned g_debug;
 

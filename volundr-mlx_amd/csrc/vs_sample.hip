@@ -43,6 +43,12 @@ constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
 constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
+// Row-barrier time bounds in ticks of the 100 MHz real-time counter. A row's workgroups arrive within ~10 us of one
+// another on an idle device; under a plain launch a wait that outlasts 200 us means some workgroup of the row is not
+// resident (other streams hold the CUs), and the row gives up so that the host can repeat the call cooperatively.
+// Under a cooperative launch every workgroup is resident, so only slowed waves can delay a barrier: 5 ms.
+constexpr uint64_t WAIT_TICKS = 20000;        // 200 us
+constexpr uint64_t WAIT_TICKS_COOP = 500000;  // 5 ms
 // LDS scalar slots (misc): 0-17 single counters and flags, then arrays
 constexpr int M_SEGC = 24;                         // [SNW] candidates per wave (TOPK)
 constexpr int M_CNTS = M_SEGC + SNW;               // [GMAX] kept count per workgroup (FULL, small kept set)
@@ -114,8 +120,9 @@ struct SampleArgs {
   int lds_ch;  // chunk length the LDS areas are sized for
   int kcap;    // candidate-list capacity per workgroup (a power of two)
   int kmax;    // largest top_k of the TOPK class for this launch
-  uint32_t spin_limit;
+  uint32_t spin_limit;  // polls before a row barrier gives up (testing hook; 0xFFFFFFFF: unbounded by polls)
   uint32_t debug;  // VS_DEBUG_* testing flags (vs_set_debug)
+  uint64_t spin_ticks;  // real-time ticks (10 ns) before a row barrier gives up
   double fix_scale;  // probability -> fixed point (2^fix_shift)
   int fix_shift;
   double zspan_max;     // ln(fix_scale) - ln(1e6): the kept-value span up to which z comes from fixed point
@@ -1697,8 +1704,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   // workgroup reports the row as timed out instead of resolving it (the host repeats the call cooperatively).
   // polls allowed at the row's nb-th barrier (the testing flag exempts the first)
   auto bar_limit = [&](uint32_t nb) -> uint32_t {
-    return ((A.debug & VS_DEBUG_SPIN_LATER_BARRIERS) && nb < 2) ? (1u << 21) : A.spin_limit;
+    return ((A.debug & VS_DEBUG_SPIN_LATER_BARRIERS) && nb < 2) ? 0xFFFFFFFFu : A.spin_limit;
   };
+  // the testing flag VS_DEBUG_WAIT_CLOCK makes every row barrier unreachable, so each wait ends at the time bound
+  auto bar_target = [&](uint32_t target) -> uint32_t { return (A.debug & VS_DEBUG_WAIT_CLOCK) ? 0xFFFFFFFFu : target; };
   auto timed_out_final = [&]() {
     Final f;
     f.token = -1;
@@ -1766,7 +1775,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   VS_TR(A, 22);
 #endif
   ++nbar;
-  ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+  ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
   VS_TR(A, 3);
   VS_TRC(A, 31);
   Final fin;
@@ -1810,7 +1819,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           HistSlot* hs = hslots + slot;
           if (t < NBIN && s.hc[t]) atomicAdd(&hs->cnt[t], s.hc[t]);
           ++nbar;
-          ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+          ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
           if (!ok) break;
           if (t < NBIN) {
             s.hc[t] = ld_relaxed(&hs->cnt[t]);
@@ -2071,7 +2080,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (!zfix_only) unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
         }
         ++nbar;
-        ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+        ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
         if (ok) {
           const int total = (int)ld_relaxed(&ctl->gcount);
           const int gmax = (int)ld_relaxed(&ctl->gmax);
@@ -2532,7 +2541,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
               VS_TR(A, 16);
               ++nbar;
-              ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+              ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
               VS_TR(A, 18);
               if (ok) {
                 for (int i = t; i < ns * NBIN; i += SNT) {
@@ -2859,7 +2868,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               atomicMax(&hr->mk[t], s.hmk[t]);
             }
             ++nbar;
-            ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+            ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
             if (ok) {
               auto load_slot = [&](HistSlot* hs) {
                 if (t < NBIN) {
@@ -2919,7 +2928,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     atomicMax(&hs->mk[t], s.hmk[t]);
                   }
                   ++nbar;
-                  ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+                  ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
                   if (!ok) return r;
                   load_slot(hs);
                 }
@@ -2967,7 +2976,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   unsafeAtomicAdd(&ctl->mf64, mff);
                 }
                 ++nbar;
-                ok = row_barrier(&ctl->bar, nbar * G, bar_limit(nbar), &s.misc[11]);
+                ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
                 if (ok) {
                   const int cm = (int)ld_relaxed(&ctl->mcnt);
                   const int km = cm > 1 ? cm : 1;
@@ -3054,7 +3063,8 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
                          vs_row_state* state, int32_t* pool, const int32_t* hist, const int32_t* bias_ids,
                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
                          uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream,
-                         int list_k = 0, int32_t* list_ids = nullptr, float* list_vals = nullptr) {
+                         int list_k = 0, int32_t* list_ids = nullptr, float* list_vals = nullptr,
+                         int rows_cap = RPL_MAX) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
   if (B == 0) return VS_OK;
   if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
@@ -3070,7 +3080,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   const int VEC = dtype == VS_F32 ? 4 : 8;
   const int unit = SNT * VEC;
   const int chmax = (EPT_MAX / VEC) * unit;
-  const int rows_target = B < RPL_MAX ? B : RPL_MAX;
+  const int rows_target = B < rows_cap ? B : rows_cap;
   const int gmin = (V + chmax - 1) / chmax;
   if (gmin > GMAX) return fail(VS_EINVAL, "vs_sample_batch: V too large for one launch row");
   int G = dv->cus / rows_target;
@@ -3118,7 +3128,8 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   // The testing spin limit applies to plain launches only: a cooperative launch guarantees that every workgroup of
   // a row is resident, so its waits keep the default bound.
   const bool coop = use_cooperative();
-  a.spin_limit = (g_spin_limit && !coop) ? g_spin_limit : 1u << 21;
+  a.spin_limit = (g_spin_limit && !coop) ? g_spin_limit : 0xFFFFFFFFu;
+  a.spin_ticks = coop ? WAIT_TICKS_COOP : WAIT_TICKS;
   a.debug = g_debug;
   a.fix_scale = ldexp(1.0, 63 - bits);
   a.fix_shift = 63 - bits;
@@ -3184,25 +3195,21 @@ extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V
 // =================================================================================================================
 // Allocation-free entry point: the workspace is a file-scope device array instead of a caller buffer
 // =================================================================================================================
-// One workspace of RPL_MAX rows covers every launch (larger batches run in launches of at most RPL_MAX rows that
-// reuse it), so the array has a fixed size of RPL_MAX * ROW_WS bytes (about 22.4 MB) per device, held until the
-// process ends. The kernels leave it zeroed after every call; it is zeroed once per device at its first use.
+// The launches of this entry point hold at most NOALLOC_ROWS rows (larger batches run as consecutive launches that
+// reuse the array; 16 rows is the batch that fills the 256 CUs at the vocabulary sizes of the path), so the array has
+// a fixed size of NOALLOC_ROWS * ROW_WS bytes (about 5.6 MB) per device, held until the process ends. It is
+// zero-initialised when the code object is loaded (static storage), and every call leaves it zeroed, so no call
+// clears it (a clear on the first call would be stream work that a call from another stream could overtake).
 namespace {
-constexpr size_t SCRATCH_BYTES = (size_t)RPL_MAX * ROW_WS;
-static_assert(SCRATCH_BYTES % 16 == 0, "the zero fill writes 16-byte words");
+constexpr int NOALLOC_ROWS = 16;
+constexpr size_t SCRATCH_BYTES = (size_t)NOALLOC_ROWS * ROW_WS;
 static __device__ __align__(256) char scratch[SCRATCH_BYTES];
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64];  // device address of `scratch` per device (the host symbol is only a stand-in)
 
-__global__ __launch_bounds__(256) void scratch_zero_kernel(uint4* p, size_t n16) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
-    p[i] = make_uint4(0u, 0u, 0u, 0u);
-}
-
-// The current device's address of `scratch`; on the first call for a device it is looked up and zeroed (a fill
-// kernel on `stream`, so the first call is stream-ordered like every later one).
-int scratch_ptr(void** out, hipStream_t stream) {
+// The current device's address of `scratch`, looked up once per device.
+int scratch_ptr(void** out) {
   int d = 0;
   hipError_t e = hipGetDevice(&d);
   if (e != hipSuccess) return hip_fail(e, "vs_sample_batch_noalloc: hipGetDevice");
@@ -3212,9 +3219,6 @@ int scratch_ptr(void** out, hipStream_t stream) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) return hip_fail(e, "vs_sample_batch_noalloc: hipGetSymbolAddress(scratch)");
-    hipLaunchKernelGGL(scratch_zero_kernel, dim3(1024), dim3(256), 0, stream, (uint4*)p, SCRATCH_BYTES / 16);
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "vs_sample_batch_noalloc: scratch zero fill");
     g_scratch_ptr[d] = p;
   }
   *out = g_scratch_ptr[d];
@@ -3231,11 +3235,10 @@ extern "C" int vs_sample_batch_noalloc(const void* logits, int dtype, int B, int
                                        vs_stream_t stream) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch_noalloc: B < 0");
   if (B == 0) return VS_OK;
-  if (vs_sample_workspace_bytes(B, V) > SCRATCH_BYTES)
-    return fail(VS_EWORKSPACE, "vs_sample_batch_noalloc: the call needs more than the fixed scratch array");
   void* ws = nullptr;
-  const int rc = scratch_ptr(&ws, (hipStream_t)stream);
+  const int rc = scratch_ptr(&ws);
   if (rc != VS_OK) return rc;
   return sample_launch(logits, dtype, B, V, ld, params, nullptr, nullptr, hist, bias_ids, bias_vals, mask_ids, out_ids,
-                       out_logprob, out_flags, out_keep, ws, SCRATCH_BYTES, stream);
+                       out_logprob, out_flags, out_keep, ws, SCRATCH_BYTES, stream, 0, nullptr, nullptr,
+                       NOALLOC_ROWS);
 }

@@ -26,6 +26,7 @@ OUT_HIST_FULL = 1 << 7
 OUT_TIMEOUT = 1 << 31
 DEBUG_FORCE_RADIX = 1
 DEBUG_SPIN_LATER_BARRIERS = 2
+DEBUG_WAIT_CLOCK = 4
 
 # vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([
@@ -42,7 +43,7 @@ STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4")
                         ("produced", "<i4"), ("min_new_tokens", "<i4")])
 assert STATE_DTYPE.itemsize == 32
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",

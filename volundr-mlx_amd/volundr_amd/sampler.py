@@ -162,8 +162,8 @@ class Sampler:
 
     def accept(self, tok):
         tok = int(tok)
+        self.history.append(tok)  # checks the id first, so a rejected id leaves every field unchanged
         self.counts[tok] = self.counts.get(tok, 0) + 1
-        self.history.append(tok)
         if self.budget is not None:
             self.budget.accept(self.produced, tok)
         self.produced += 1
@@ -216,12 +216,12 @@ def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
         return out, host
     L = _lib.load()
     ops.reset_workspace(logits.device)
-    L.vs_set_cooperative(1)
+    prev = L.vs_set_cooperative(1)  # this thread's setting; other threads keep theirs
     try:
         out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
         host = out.block.cpu().numpy()
     finally:
-        L.vs_set_cooperative(0)
+        L.vs_set_cooperative(prev)
     if (host[2].view(np.uint32) & OUT_TIMEOUT).any():
         ops.reset_workspace(logits.device)
         raise VsError("vs_sample_batch: an inter-workgroup wait timed out, also under a cooperative launch")
