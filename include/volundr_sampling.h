@@ -41,12 +41,15 @@ enum { VS_F32 = 0, VS_BF16 = 1, VS_F16 = 2 };
 enum {
   VS_ROW_GREEDY = 1u, /* Sampling.greedy (session.py:466-467): top_k == 1 or temperature < 1e-6 -> np.argmax of the
                          processed row over the full vocabulary, first maximum (sampler.py:127-128) */
-  VS_ROW_ARGMAX_VV = 2u /* with VS_ROW_GREEDY: a request that needs no logits (Sampling.needs_logits is False,
+  VS_ROW_ARGMAX_VV = 2u, /* with VS_ROW_GREEDY: a request that needs no logits (Sampling.needs_logits is False,
                            session.py:469-474) takes the first-max argmax over [0, vocab_valid) with no edits
                            (sampler.py:96, mx.argmax(logits[:vv])). The host sets it only for rows with no bias,
                            neutral penalties and no suppressed id below vocab_valid; the one condition that can change
                            per step, an active stop mask (produced < min_new_tokens with stop ids), is decided by the
                            kernel: a row whose stop range applies takes the ordinary greedy path over the full row */
+  VS_ROW_FORCE = 4u /* the reasoning budget forces force_token (sampler.py:88-90, Sampler.choose returns it without
+                       sampling): the row's logits are not read and no draw is consumed; the state entry point records
+                       the token as Sampler.accept does */
 };
 
 /* out_flags bits */
@@ -59,6 +62,7 @@ enum {
   VS_OUT_GATHER = 1u << 6,        /* the distribution was resolved in one workgroup after a gather */
   VS_OUT_HIST_FULL = 1u << 7,     /* vs_sample_batch_state: the request's history slots were full, the token was
                                      not recorded (later penalties miss it) */
+  VS_OUT_FORCED = 1u << 8,        /* the row returned its VS_ROW_FORCE token */
   VS_OUT_TIMEOUT = 1u << 31       /* an inter-workgroup wait hit its spin limit: results of this row are invalid */
 };
 
@@ -82,7 +86,7 @@ typedef struct vs_row_params {
   int32_t stop_begin, stop_end; /* stop ids masked while produced < min_new_tokens, sorted: -inf after the
                                    penalties (sampler.py:123-126); the host passes an empty range otherwise */
   int32_t vocab_valid;          /* Sampler.vv (sampler.py:59), read only by VS_ROW_ARGMAX_VV rows; 1 <= vv */
-  uint32_t reserved;            /* zero */
+  int32_t force_token;          /* the token of a VS_ROW_FORCE row (zero otherwise) */
 } vs_row_params;
 
 /* Sampler.sample for B rows of logits (row r starts at element r*ld; ld >= V).
@@ -129,19 +133,23 @@ typedef struct vs_row_state {
   int32_t min_new_tokens; /* the stop range of the row's params applies while produced < min_new_tokens */
 } vs_row_state;
 
-/* vs_sample_batch with the state on the device: for each row r the draw is Sampler.uniform() on state[r].rng,
- * the history is pool[hist_off, hist_off + hist_len), and the stop mask applies while produced < min_new_tokens
- * (params[r].u, hist_begin/hist_end are ignored; the stop range gives the stop ids). After the choice the row's
- * state is advanced as Sampler.accept does (sampler.py:75-79): the token is appended to the history (flag
- * VS_OUT_HIST_FULL when hist_len == hist_cap), produced += 1, and the xorshift64* state moves on when the row drew
- * (not for greedy rows or rows with no finite logit, which return before self.uniform(), sampler.py:127-133).
- * Rows flagged VS_OUT_TIMEOUT leave their state unchanged. Rows of one call must not share history slots.
- * Replaces: Sampler.choose (sampler.py:83-98) for requests without a reasoning budget, with uniform() and accept()
- * on the device. */
+/* vs_sample_batch with the state on the device: row r of the logits belongs to request q = slots[r] (slots NULL:
+ * q = r), whose parameters are params[q] and whose state is state[q]. The draw is Sampler.uniform() on
+ * state[q].rng, the history is pool[hist_off, hist_off + hist_len), and the stop mask applies while
+ * produced < min_new_tokens (params[q].u, hist_begin/hist_end are ignored; the stop range gives the stop ids).
+ * After the choice the request's state is advanced as Sampler.accept does (sampler.py:77-81): the token is appended
+ * to the history (flag VS_OUT_HIST_FULL when hist_len == hist_cap), produced += 1, and the xorshift64* state moves on
+ * when the row drew (not for greedy rows, rows with no finite logit, which return before self.uniform(),
+ * sampler.py:127-133, or VS_ROW_FORCE rows). Outputs are indexed by r. Rows flagged VS_OUT_TIMEOUT leave their
+ * state unchanged. Rows of one call must not share a request or history slots. The params and state tables may
+ * hold more requests than the call has rows (a continuous-batching slot table: requests join and leave between
+ * calls by changing their rows of the tables and the slots array).
+ * Replaces: Sampler.choose (sampler.py:83-98) for a batch of requests (scheduler.py:402-425), with uniform() and
+ * accept() on the device; the reasoning budget's force and bias arrive as VS_ROW_FORCE and bias entries. */
 int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
-                          vs_row_state* state, int32_t* pool, const int32_t* bias_ids, const float* bias_vals,
-                          const int32_t* mask_ids, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
-                          int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream);
+                          vs_row_state* state, int32_t* pool, const int32_t* slots, const int32_t* bias_ids,
+                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
+                          uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream);
 
 /* Greedy speculative verify over logits [B, T, V] (row (b,t) starts at element (b*T + t)*ld).
  *   drafts     : int32 [B, T-1], the draft tokens inp[:, 1:] of the verify input
@@ -240,7 +248,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 7. */
+/* Library ABI version (increments on any signature or struct change): 8. */
 int vs_version(void);
 
 #ifdef __cplusplus

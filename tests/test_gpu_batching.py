@@ -1,0 +1,149 @@
+"""Continuous batching on the device-resident sampler state (DeviceSamplers.admit / retire / step), against the
+oracle driven as the reference's engine drives Sampler.choose: a Sampler is created when a request is admitted
+(volundr-mlx/scheduler.py:148-151) and choose() runs for whichever requests are live at each step
+(scheduler.py:402-425), budget force and bias included (sampler.py:85-92). Requests join and leave over 20 steps;
+rows are stepped in admission order, in a reversed order and as a subset; one request's history outgrows the pool
+(which then grows on the device). Tokens, logprobs, rng states, histories and produced counts are compared."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_ref as S
+from parity import LP_ATOL, LP_RTOL
+from volundr_amd import DeviceSamplers, Sampler
+from volundr_amd._lib import OUT_FORCED
+from volundr_amd.session import Sampling
+
+pytestmark = pytest.mark.gpu
+
+V, VV = 50000, 49900
+THINK, UNTHINK = 1000, 1001
+PAD_HOT = V - 7
+
+
+class OracleRequest:
+    """The oracle's view of one request: rng, the tokens produced (forced ones included), the prompt."""
+
+    def __init__(self, sp, prompt=(), think=(None, None), history=()):
+        self.sp, self.prompt, self.think = sp, list(prompt), think
+        self.rng = S.seed_state(sp.seed)
+        self.pre = list(history)  # tokens accepted before admission (count for the penalties, not for produced)
+        self.gen = []
+
+    def step(self, x):
+        nxt, u = S.xorshift64s_next(self.rng)
+        if self.pre:  # a request with earlier tokens and no budget: its penalties count them too
+            assert not self.sp.reasoning_budget and self.sp.needs_logits(VV, len(self.gen))
+            r = S.sample(x, self.sp, u, S.counts_from_history(self.pre + self.gen), len(self.gen))
+        else:
+            r = S.choose(x, self.sp, VV, u, self.gen, self.prompt, self.think)
+        return r, nxt
+
+    def accept(self, tok, r, nxt):
+        if r.kind == "sample":
+            self.rng = nxt
+        self.gen.append(int(tok))
+
+
+def _logits(rng, n):
+    x = np.clip(rng.standard_normal((n, V)) * 2.0, -9.0, 9.0).astype(np.float32)
+    x[:, PAD_HOT] = 12.0   # the row maximum sits in the padding: argmax-only requests must skip it
+    x[:, 11] = 10.5        # the largest valid logit
+    x[:, UNTHINK] = 9.5    # close behind: the budget's soft bias on it decides
+    return x
+
+
+def _check(label, tok, lp, r):
+    if r.kind == "sample" and (r.draw_boundary or r.topp_boundary) and tok != r.token:
+        return
+    assert tok == r.token, f"{label}: token {tok} != oracle {r.token} ({r.kind})"
+    if r.kind != "force":
+        assert abs(lp - r.logprob) <= LP_RTOL * abs(r.logprob) + LP_ATOL, f"{label}: logprob {lp} vs {r.logprob}"
+    else:
+        assert lp == 0.0
+
+
+REQUESTS = {
+    "A": (Sampling(top_p=0.9, temperature=1.1, presence_penalty=0.4, repetition_penalty=1.2, seed=31), (), None),
+    "B": (Sampling(temperature=0.0, seed=32), (), None),                                        # argmax-only
+    "C": (Sampling(temperature=0.0, reasoning_budget=3, seed=33), (5, THINK), None),            # forced at step 3
+    "D": (Sampling(top_k=20, temperature=0.8, min_new_tokens=3, stop_token_ids=[11], seed=34), (), None),
+    "E": (Sampling(temperature=0.0, reasoning_budget=6, reasoning_budget_soft_bias=0.5, seed=35), (THINK,), None),
+    "F": (Sampling(top_k=50, repetition_penalty=1.3, frequency_penalty=0.1, seed=36), (), "long"),
+    "G": (Sampling(top_p=0.8, logit_bias=[(UNTHINK, 1.5), (3, -2.0)], suppress_tokens=[11], seed=37), (), None),
+}
+# step -> (admit, retire) before that step
+SCHEDULE = {0: ("ABC", ""), 3: ("D", "B"), 6: ("E", ""), 10: ("F", "A"), 14: ("G", "C"), 17: ("", "D")}
+
+
+def test_continuous_batching_against_oracle(dev):
+    rng = np.random.default_rng(123)
+    ds = DeviceSamplers([], V, hist_cap=64, device=dev, capacity=2)  # grows to more slots and a larger pool
+    live, slot_of, host, orc, done = [], {}, {}, {}, {}
+    forced_seen = 0
+    for step in range(20):
+        adm, ret = SCHEDULE.get(step, ("", ""))
+        for name in ret:
+            ds.retire(slot_of[name])  # writes the device state back into the host Sampler
+            done[name] = host[name]
+            live.remove(name)
+        for name in adm:
+            sp, prompt, hist = REQUESTS[name]
+            think = (THINK, UNTHINK) if sp.reasoning_budget else (None, None)
+            s = Sampler(sp, prompt=prompt, think_ids=think, vocab_valid=VV)
+            pre = []
+            if hist == "long":  # accepted before admission (not counted in produced): 100 tokens, pool of 64
+                pre = rng.integers(0, VV, 100).tolist()
+                for t in pre:
+                    s.history.append(t)
+                    s.counts[t] = s.counts.get(t, 0) + 1
+            host[name] = s
+            orc[name] = OracleRequest(sp, prompt, think, pre)
+            slot_of[name] = ds.admit(s)
+            live.append(name)
+        names = list(live)
+        if step in (8, 15):
+            names = names[::-1]                    # rows in any order
+        if step == 12:
+            names = names[:-1]                     # a subset: the last request sits this step out
+        x = _logits(rng, len(names))
+        print(f"[batching] step {step}: {''.join(names)}", flush=True)
+        res = ds.step(torch.from_numpy(x).to(dev), [slot_of[n] for n in names])
+        for i, name in enumerate(names):
+            r, nxt = orc[name].step(x[i])
+            _check(f"step {step} {name}", res.ids[i], res.logprobs[i], r)
+            if r.kind == "force":
+                assert res.flags[i] & OUT_FORCED
+                forced_seen += 1
+            orc[name].accept(res.ids[i], r, nxt)
+    ds.write_back()
+    for name, s in list(host.items()):
+        o = orc[name]
+        assert s.rng == o.rng, f"{name}: rng"
+        assert list(s.history) == o.pre + o.gen, f"{name}: history"
+        assert s.produced == len(o.gen), f"{name}: produced"
+    assert forced_seen == 2                               # C at its third thinking token, E at its sixth
+    assert orc["C"].gen[3] == UNTHINK and orc["E"].gen[6] == UNTHINK
+    assert orc["B"].gen == [11] * 3                       # argmax over [:vv] skips the padding maximum
+    assert ds.cap > 64 and ds.S > 2                       # the pool and the slot table grew
+
+
+def test_admit_retire_reuses_slots(dev):
+    """A retired slot is reused by the next admission, and the new request starts from its own state."""
+    rng = np.random.default_rng(5)
+    sp = Sampling(top_k=10, repetition_penalty=1.5, seed=41)
+    ds = DeviceSamplers([Sampler(sp, vocab_valid=VV)], V, hist_cap=64, device=dev)
+    for _ in range(3):
+        ds.step(torch.from_numpy(_logits(rng, 1)).to(dev))
+    old = ds.samplers[0]
+    ds.retire(0)
+    assert old.produced == 3 and len(old.history) == 3
+    fresh = Sampler(Sampling(top_k=10, repetition_penalty=1.5, seed=41), vocab_valid=VV)
+    q = ds.admit(fresh)
+    assert q == 0
+    x = _logits(rng, 1)
+    res = ds.step(torch.from_numpy(x).to(dev))
+    o = OracleRequest(fresh.sp)
+    r, _ = o.step(x[0])
+    _check("reused slot", res.ids[0], res.logprobs[0], r)
+    assert ds.history(0) == [res.ids[0]]

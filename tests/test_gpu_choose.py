@@ -122,7 +122,7 @@ def test_device_samplers_vocab_valid(dev):
     for step in range(6):
         x = _logits(rng, B)
         print(f"[device vv] step {step}", flush=True)
-        out = ds.step(torch.from_numpy(x).to(dev))
+        out = ds.step(torch.from_numpy(x).to(dev), sync=False)
         ids = out.ids.cpu().numpy()
         lps = out.logprobs.cpu().numpy().astype(np.float64)
         for r in range(B):

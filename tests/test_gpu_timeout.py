@@ -92,7 +92,7 @@ def test_device_state_not_committed_for_timed_out_rows(dev):
     ds = DeviceSamplers(samplers, V, hist_cap=64, device=dev)
     x = torch.from_numpy(d["logits"]).to(dev)
     st0 = ds.host_state().copy()
-    out = _forced(lambda: ds.step(x))
+    out = _forced(lambda: ds.step(x, sync=False))
     fl = _flags(out)
     st1 = ds.host_state()
     assert any(f & OUT_TIMEOUT for f in fl)
@@ -102,7 +102,7 @@ def test_device_state_not_committed_for_timed_out_rows(dev):
             assert st1[r]["hist_len"] == st0[r]["hist_len"], r
         else:
             assert st1[r]["produced"] == st0[r]["produced"] + 1, r
-    out2 = ds.step(x)  # the next step runs normally
+    out2 = ds.step(x, sync=False)  # the next step runs normally
     assert not any(f & OUT_TIMEOUT for f in _flags(out2))
 
 
@@ -217,11 +217,11 @@ def test_device_state_after_a_later_barrier_timeout(dev):
         return DeviceSamplers(ss, V, hist_cap=64, device=dev)
 
     ref = fresh()
-    want = ref.step(x).ids.cpu().tolist()
+    want = ref.step(x).ids
     st_want = ref.host_state().copy()
     ds = fresh()
     st0 = ds.host_state().copy()
-    out = _forced_later(lambda: ds.step(x))
+    out = _forced_later(lambda: ds.step(x, sync=False))
     fl, ids = _flags(out), out.ids.cpu().tolist()
     st1 = ds.host_state()
     print(f"[timeout] state rows flagged {sum(bool(f & OUT_TIMEOUT) for f in fl)} of {B}", flush=True)
@@ -233,6 +233,33 @@ def test_device_state_after_a_later_barrier_timeout(dev):
             assert ids[r] == want[r], r
             assert st1[r]["rng"] == st_want[r]["rng"] and st1[r]["hist_len"] == st_want[r]["hist_len"], r
 
+
+
+@pytest.mark.parametrize("later", [False, True])
+def test_device_state_step_retries_timed_out_rows(dev, later):
+    """DeviceSamplers.step (synchronous) repeats the rows that timed out under a cooperative launch: the tokens,
+    logprobs and every slot's state equal an unforced step's, and no row comes back flagged."""
+    d = synth.CONFIGS["c5"](seed=7)
+    B, V = d["logits"].shape
+    x = torch.from_numpy(d["logits"]).to(dev)
+
+    def fresh():
+        ss = []
+        for r, sp in enumerate(d["params"]):
+            s = Sampler(sp, vocab_valid=V, request_id=r)
+            s.rng = 0x5151 ^ r
+            ss.append(s)
+        return DeviceSamplers(ss, V, hist_cap=64, device=dev)
+
+    ref = fresh()
+    want = ref.step(x)
+    ds = fresh()
+    print(f"[timeout] state step retry, later={later}", flush=True)
+    got = _forced_later(lambda: ds.step(x)) if later else _forced(lambda: ds.step(x))
+    assert got.ids == want.ids and got.logprobs == want.logprobs
+    assert not any(f & OUT_TIMEOUT for f in got.flags)
+    assert np.array_equal(ds.host_state(), ref.host_state())
+    assert ds.history(3) == ref.history(3)
 
 @pytest.mark.parametrize("coop", [0, 1])
 def test_wait_time_bound(dev, coop):

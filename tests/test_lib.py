@@ -36,7 +36,7 @@ def test_errors_without_device_calls():
     assert b"B < 0" in L.vs_last_error()
     assert L.vs_sample_batch(0, 0, 0, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_OK
     assert L.vs_verify_greedy(0, 0, 1, 0, 10, 10, 10, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
-    assert L.vs_sample_batch_state(0, 0, 1, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
+    assert L.vs_sample_batch_state(0, 0, 1, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
     assert b"null state" in L.vs_last_error()
 
 

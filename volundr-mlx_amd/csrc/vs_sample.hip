@@ -132,6 +132,7 @@ struct SampleArgs {
   int32_t* list_ids;    // [B, list_k]
   float* list_vals;     // [B, list_k]
   int32_t* pool;        // history pool of the state entry point
+  const int32_t* slots;  // state entry point: row r uses params[slots[r]] and state[slots[r]] (null: r)
   const int32_t* hist;
   const int32_t* bias_ids;
   const float* bias_vals;
@@ -835,8 +836,8 @@ __device__ __forceinline__ Stats block_stats(int n, uint32_t mx1, uint32_t mx2, 
 __device__ __forceinline__ uint32_t commit_state(const SampleArgs& A, int r, int32_t token, uint32_t flags,
                                                  const vs_row_state& st, uint64_t rng_next) {
   if (!A.state || (flags & VS_OUT_TIMEOUT)) return flags;
-  vs_row_state* S = A.state + r;
-  if (!(flags & (VS_OUT_GREEDY | VS_OUT_NOFINITE))) S->rng = rng_next;
+  vs_row_state* S = A.state + (A.slots ? A.slots[r] : r);
+  if (!(flags & (VS_OUT_GREEDY | VS_OUT_NOFINITE | VS_OUT_FORCED))) S->rng = rng_next;
   if (st.hist_len < st.hist_cap) {
     A.pool[st.hist_off + st.hist_len] = token;
     S->hist_len = st.hist_len + 1;
@@ -1012,17 +1013,30 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int row = l / G, g = l % G;
   const int grow = A.row0 + row;
+  const int srow = A.slots ? A.slots[grow] : grow;  // the request's params and state
   vs_row_params P;
   if (A.params) {
-    P = A.params[grow];
+    P = A.params[srow];
   } else {  // top-list mode: plain logits, top_k = list_k, no edits
-    P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0u};
+    P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   }
   // state entry point: the draw, the history range and the stop mask come from the request's device state
   vs_row_state st = {0, 0, 0, 0, 0, 0};
   uint64_t rng_next = 0;
+  if (A.state) st = A.state[srow];
+  // a token forced by the reasoning budget (sampler.py:88-90): the logits are not read, no draw is consumed
+  if (P.flags & VS_ROW_FORCE) {
+    if (g == 0) {
+      Final f;
+      f.token = P.force_token;
+      f.lp = 0.0f;
+      f.flags = VS_OUT_FORCED;
+      f.keep = 0;
+      write_out(A, row, f, st, 0);
+    }
+    return;
+  }
   if (A.state) {
-    st = A.state[grow];
     rng_next = xorshift64s_step(st.rng);
     P.u = xorshift64s_uniform(rng_next);
     P.hist_begin = st.hist_off;
@@ -3064,7 +3078,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
                          uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream,
                          int list_k = 0, int32_t* list_ids = nullptr, float* list_vals = nullptr,
-                         int rows_cap = RPL_MAX) {
+                         int rows_cap = RPL_MAX, const int32_t* slots = nullptr) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
   if (B == 0) return VS_OK;
   if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
@@ -3140,6 +3154,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.list_vals = list_vals;
   a.state = state;
   a.pool = pool;
+  a.slots = slots;
   a.hist = state ? pool : hist;
   a.bias_ids = bias_ids;
   a.bias_vals = bias_vals;
@@ -3184,12 +3199,13 @@ extern "C" int vs_topk_batch(const void* logits, int dtype, int B, int V, int64_
 
 extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld,
                                      const vs_row_params* params, vs_row_state* state, int32_t* pool,
-                                     const int32_t* bias_ids, const float* bias_vals, const int32_t* mask_ids,
-                                     int32_t* out_ids, float* out_logprob, uint32_t* out_flags, int32_t* out_keep,
-                                     void* ws, size_t ws_bytes, vs_stream_t stream) {
+                                     const int32_t* slots, const int32_t* bias_ids, const float* bias_vals,
+                                     const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
+                                     uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes,
+                                     vs_stream_t stream) {
   if (!state) return fail(VS_EINVAL, "vs_sample_batch_state: null state");
   return sample_launch(logits, dtype, B, V, ld, params, state, pool, nullptr, bias_ids, bias_vals, mask_ids, out_ids,
-                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream);
+                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream, 0, nullptr, nullptr, RPL_MAX, slots);
 }
 
 // =================================================================================================================

@@ -16,6 +16,7 @@ VS_OK, VS_EINVAL, VS_EWORKSPACE, VS_EHIP = 0, -1, -2, -3
 VS_F32, VS_BF16, VS_F16 = 0, 1, 2
 VS_ROW_GREEDY = 1
 VS_ROW_ARGMAX_VV = 2
+VS_ROW_FORCE = 4
 OUT_DRAW_BOUNDARY = 1 << 0
 OUT_TOPP_BOUNDARY = 1 << 1
 OUT_GREEDY = 1 << 3
@@ -23,6 +24,7 @@ OUT_NOFINITE = 1 << 4
 OUT_COOP = 1 << 5
 OUT_GATHER = 1 << 6
 OUT_HIST_FULL = 1 << 7
+OUT_FORCED = 1 << 8
 OUT_TIMEOUT = 1 << 31
 DEBUG_FORCE_RADIX = 1
 DEBUG_SPIN_LATER_BARRIERS = 2
@@ -34,7 +36,7 @@ ROW_DTYPE = np.dtype([
     ("presence_penalty", "<f4"), ("top_k", "<i4"), ("flags", "<u4"),
     ("top_p", "<f8"), ("min_p", "<f8"), ("u", "<f8"), ("hist_begin", "<i8"), ("hist_end", "<i8"),
     ("bias_begin", "<i4"), ("bias_end", "<i4"), ("supp_begin", "<i4"), ("supp_end", "<i4"),
-    ("stop_begin", "<i4"), ("stop_end", "<i4"), ("vocab_valid", "<i4"), ("reserved", "<u4"),
+    ("stop_begin", "<i4"), ("stop_end", "<i4"), ("vocab_valid", "<i4"), ("force_token", "<i4"),
 ])
 assert ROW_DTYPE.itemsize == 96
 
@@ -43,7 +45,7 @@ STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4")
                         ("produced", "<i4"), ("min_new_tokens", "<i4")])
 assert STATE_DTYPE.itemsize == 32
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
@@ -71,7 +73,7 @@ def load():
     L.vs_sample_batch_noalloc.restype = i32
     L.vs_sample_noalloc_scratch_bytes.argtypes = []
     L.vs_sample_noalloc_scratch_bytes.restype = sz
-    L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     L.vs_sample_batch_state.restype = i32
     L.vs_lmhead_verify_greedy.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, sz,
                                           vp]

@@ -1,104 +1,375 @@
-"""Per-request sampler state kept on the device (vs_sample_batch_state, include/volundr_sampling.h).
+"""Per-request sampler state kept on the device, for a continuously changing batch (vs_sample_batch_state,
+include/volundr_sampling.h).
 
 Sampler (volundr-mlx/sampler.py:58-98) keeps three things per request on the host: the xorshift64* state behind
-uniform(), the counts that accept() builds, and produced. DeviceSamplers keeps them in device memory for a fixed
-set of requests, so that a serving loop's step is one kernel launch with nothing uploaded: the kernel draws
-uniform() itself, reads the request's token history from a device pool for the penalties, applies the
-min_new_tokens stop mask from its own produced count, and appends the chosen token (Sampler.accept) before it
-returns. Requests with a reasoning budget stay on the host Sampler (the budget's force/bias decisions are host
-logic, sampler.py:18-55).
+uniform(), the counts that accept() builds, and produced. The reference's engine creates one Sampler per request at
+admission (scheduler.py:148-151) and calls choose() for whichever rows are live at each step (scheduler.py:402-425).
+DeviceSamplers keeps that state in device tables with one slot per live request:
+
+  * admit(sampler) gives the request a slot (its rng, history and produced are uploaded once); retire(slot) frees it
+    and by default writes the state back into the Sampler. Only the rows of the changed slot move over PCIe.
+  * step(logits) runs Sampler.choose for the live requests in `order` (row i of logits belongs to order[i]); or
+    step(logits, slots) for any subset, in any order. The kernel draws uniform() itself, reads the request's token
+    history from the device pool for the penalties, applies the min_new_tokens stop mask from its own produced
+    count and appends the chosen token (Sampler.accept).
+  * The reasoning budget (sampler.py:18-55, 85-92) stays host logic: before each step the host asks the request's
+    Budget for its action, which needs no logits. A forced token goes to the device as a VS_ROW_FORCE row (recorded,
+    no draw), a bias as the slot's bias entries (budget extra before logit_bias). The row is re-uploaded only when
+    the action changes.
+  * Histories never overflow: the host keeps an upper bound of every slot's history length and doubles the pool's
+    per-slot capacity on the device before a step could fill it (Sampler.counts is unbounded, sampler.py:77-78).
+  * A row whose row barrier timed out (VS_OUT_TIMEOUT: other work held the CUs its workgroups needed at once)
+    committed nothing; step() repeats those rows once under a cooperative launch and raises only if that also times
+    out (the recovery of Sampler.sample, sampler._sample_checked).
+
+step(sync=True) copies the results back (one copy) and returns them as host lists, which is what an engine that
+emits tokens needs every step; step(sync=False) returns the device outputs without waiting (no budget rows, and the
+caller checks the flags). The host Sampler objects are refreshed by write_back() / retire().
 """
 from __future__ import annotations
 
-from typing import Optional, Sequence
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
 
 import numpy as np
 import torch
 
 from . import _lib
-from ._lib import STATE_DTYPE, check
-from .ops import _DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, pack_rows, workspace
+from ._lib import OUT_HIST_FULL, OUT_TIMEOUT, ROW_DTYPE, STATE_DTYPE, VS_ROW_FORCE, VsError, check
+from .ops import (_DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, pack_rows,
+                  reset_workspace, workspace)
 from .sampler import TokenHistory
+
+_NO_ACTION = ("none", None)
+
+
+@dataclass
+class StepResult:
+    """Host copies of one synchronous step's outputs (row i = the i-th slot of the step)."""
+    ids: List[int]
+    logprobs: List[float]
+    flags: List[int]
+    keep: List[int]
+    out: SampleOut  # the device outputs of the same step
+
+
+def _dev_copy(dst: torch.Tensor, src: np.ndarray):
+    """Host array -> a slice of a device tensor (a byte tensor takes the array's bytes, a typed one its values)."""
+    if src.size:
+        a = np.ascontiguousarray(src)
+        dst.copy_(torch.from_numpy(a.view(np.uint8).reshape(-1) if dst.dtype == torch.uint8 else a.reshape(-1)))
 
 
 class DeviceSamplers:
-    """Device-resident state of the samplers of B requests, one row each.
+    """Device-resident sampler state of a changing set of requests, one slot each.
 
-    samplers : host Sampler objects (volundr_amd.Sampler); their rng, history and produced seed the device state
+    samplers : host Sampler objects (volundr_amd.Sampler) admitted at construction, in order (slots 0, 1, ...)
     vocab    : the logits row length V the steps will be called with
-    hist_cap : history slots reserved per request (a token accepted beyond it is flagged VS_OUT_HIST_FULL and not
-               counted by later penalties)
+    hist_cap : initial history slots per request (the pool grows on the device when a request could fill it)
+    capacity : initial number of slots (grows when more requests are admitted)
+    grow_history : False keeps the pool's size fixed: a token accepted beyond hist_cap is then flagged
+               VS_OUT_HIST_FULL and not counted by later penalties (a testing configuration)
     """
 
-    def __init__(self, samplers: Sequence, vocab: int, hist_cap: int = 4096, device=None):
-        if not samplers:
-            raise ValueError("at least one sampler is required")
-        for s in samplers:
-            if getattr(s, "budget", None) is not None:
-                raise ValueError("requests with a reasoning budget keep their state on the host Sampler")
+    def __init__(self, samplers: Sequence = (), vocab: int = 0, hist_cap: int = 4096, device=None,
+                 capacity: Optional[int] = None, grow_history: bool = True):
+        if vocab < 1:
+            raise ValueError("vocab must be >= 1")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        self.dev, self.V, self.B, self.cap = dev, int(vocab), len(samplers), int(hist_cap)
-        self.samplers = list(samplers)
-        st = np.zeros(self.B, dtype=STATE_DTYPE)
-        pool = np.zeros(self.B * self.cap, dtype=np.int32)
-        for r, s in enumerate(self.samplers):
-            h = np.asarray(getattr(s, "history", []), dtype=np.int64)
-            if h.size > self.cap:
-                raise ValueError(f"request {r}: history of {h.size} tokens exceeds hist_cap {self.cap}")
-            st[r]["rng"] = np.uint64(s.rng)
-            st[r]["hist_off"] = r * self.cap
-            st[r]["hist_len"] = h.size
-            st[r]["hist_cap"] = self.cap
-            st[r]["produced"] = int(s.produced)
-            st[r]["min_new_tokens"] = int(s.sp.min_new_tokens)
-            pool[r * self.cap:r * self.cap + h.size] = h
-        self.state = torch.from_numpy(st.view(np.uint8).copy()).to(dev)
-        self.pool = torch.from_numpy(pool).to(dev)
-        # requests that need no logits take Sampler.choose's argmax over [:vocab_valid] (sampler.py:95-96) whenever
-        # their stop mask is off; the kernel applies the mask while its own produced < min_new_tokens
-        avv = [s.vv if argmax_only_ok(s.sp, s.vv) else None for s in self.samplers]
-        self.rows = pack_rows([s.sp for s in self.samplers], np.zeros(self.B), self.V, stop_always=True,
-                              argmax_vv=avv).to(dev)
-        self.out = alloc_out(self.B, dev)
-        L = _lib.load()
-        self._ws = workspace(dev, L.vs_sample_workspace_bytes(self.B, self.V))
+        self.dev, self.V = dev, int(vocab)
+        self.grow_history = bool(grow_history)
+        need = max(64, max((len(getattr(s, "history", ())) for s in samplers), default=0) + 64)
+        cap = max(int(hist_cap), 1)
+        if self.grow_history:
+            cap = max(cap, need)
+        self.cap = (cap + 63) // 64 * 64 if self.grow_history else cap
+        self.S = max(int(capacity or 0), len(samplers), 1)
+        self.EB = self.EM = 16  # bias / mask (suppress + stop) entries per slot
+        self.slot_sampler: list = [None] * self.S
+        self.order: List[int] = []  # live slots in admission order
+        self._act: list = [None] * self.S  # the budget action each slot's uploaded row encodes
+        self._edits: list = [None] * self.S  # per slot: (bias ids, bias vals, mask ids, n_supp) as uploaded
+        self._hmax = [0] * self.S  # upper bound of each slot's device history length
+        self._prod = [0] * self.S  # produced, as of the last synchronous step (budget rows need it)
+        self.params_h = np.zeros(self.S, dtype=ROW_DTYPE)
+        self._alloc_tables()
+        self._slots_key = None
+        self._slots_t = None
+        self.out = alloc_out(max(len(samplers), 1), dev)
+        for s in samplers:
+            self.admit(s)
 
-    def step(self, logits: torch.Tensor, out: Optional[SampleOut] = None) -> SampleOut:
-        """Sampler.choose for every request on logits [B, V]: draw, choose, accept, all on the device."""
-        _require_cuda(logits, "logits")
-        if logits.shape != (self.B, self.V) or logits.stride(1) != 1:
-            raise ValueError(f"logits must be [{self.B}, {self.V}] with unit stride along V")
-        if logits.dtype not in _DTYPES:
-            raise ValueError(f"unsupported logits dtype {logits.dtype}")
-        out = out if out is not None else self.out
+    # ------------------------------------------------------------------ tables
+    def _alloc_tables(self):
+        S, dev = self.S, self.dev
+        self.params = torch.zeros(S * ROW_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+        self.state = torch.zeros(S * STATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+        self.pool = torch.zeros(S * self.cap, dtype=torch.int32, device=dev)
+        self.bias_ids = torch.zeros(S * self.EB, dtype=torch.int32, device=dev)
+        self.bias_vals = torch.zeros(S * self.EB, dtype=torch.float32, device=dev)
+        self.mask_ids = torch.zeros(S * self.EM, dtype=torch.int32, device=dev)
+
+    def _grow_slots(self, S2: int):
+        """More slots: every table is re-allocated and the live slots' rows copied on the device."""
+        old = (self.params, self.state, self.pool, self.bias_ids, self.bias_vals, self.mask_ids)
+        S1 = self.S
+        self.S = S2
+        self._alloc_tables()
+        for new, o in zip((self.params, self.state, self.pool, self.bias_ids, self.bias_vals, self.mask_ids), old):
+            new[:o.numel()].copy_(o)
+        ph = np.zeros(S2, dtype=ROW_DTYPE)
+        ph[:S1] = self.params_h
+        self.params_h = ph
+        for lst, fill in ((self.slot_sampler, None), (self._act, None), (self._edits, None), (self._hmax, 0),
+                          (self._prod, 0)):
+            lst.extend([fill] * (S2 - S1))
+
+    def _grow_history(self, need: int):
+        """Per-slot history capacity >= need: a new pool, each slot's history copied on the device, and every
+        slot's hist_off / hist_cap rewritten in place (stream-ordered before the next step)."""
+        cap2 = self.cap
+        while cap2 < need:
+            cap2 *= 2
+        S, cap1 = self.S, self.cap
+        pool2 = torch.zeros(S * cap2, dtype=torch.int32, device=self.dev)
+        pool2.view(S, cap2)[:, :cap1].copy_(self.pool.view(S, cap1))
+        self.pool, self.cap = pool2, cap2
+        st64 = self.state.view(torch.int64).view(S, 4)
+        st64[:, 1].copy_(torch.arange(S, dtype=torch.int64, device=self.dev) * cap2)
+        self.state.view(torch.int32).view(S, 8)[:, 5].fill_(cap2)
+
+    def _grow_edits(self, nb: int, nm: int):
+        EB2, EM2 = self.EB, self.EM
+        while EB2 < nb:
+            EB2 *= 2
+        while EM2 < nm:
+            EM2 *= 2
+        if (EB2, EM2) == (self.EB, self.EM):
+            return
+        self.EB, self.EM = EB2, EM2
+        self.bias_ids = torch.zeros(self.S * EB2, dtype=torch.int32, device=self.dev)
+        self.bias_vals = torch.zeros(self.S * EB2, dtype=torch.float32, device=self.dev)
+        self.mask_ids = torch.zeros(self.S * EM2, dtype=torch.int32, device=self.dev)
+        for q in range(self.S):  # every slot's entries move: re-pack and re-upload the live ones
+            if self.slot_sampler[q] is not None:
+                self._upload_row(q, self._act[q], force_edits=True)
+
+    # ------------------------------------------------------------------ per-slot rows
+    def _upload_row(self, q: int, action, force_edits: bool = False):
+        """Pack slot q's params row for a budget action and upload what changed (params row, its edit entries)."""
+        s = self.slot_sampler[q]
+        sp = s.sp
+        kind, val = action if action is not None else _NO_ACTION
+        extra = list(val) if kind == "bias" else []
+        avv = [s.vv] if (argmax_only_ok(sp, s.vv) and not extra) else None
+        p = pack_rows([sp], [0.0], self.V, None, None, [extra], stop_always=True, argmax_vv=avv)
+        nb, nm = p.bias_ids.size, p.mask_ids.size
+        if nb > self.EB or nm > self.EM:
+            self._act[q] = action
+            self._grow_edits(nb, nm)  # re-uploads every live slot, this one included
+            return
+        row = p.params.copy()
+        r = row[0]
+        nsupp = int(r["supp_end"] - r["supp_begin"])
+        b0, m0 = q * self.EB, q * self.EM
+        r["bias_begin"], r["bias_end"] = b0, b0 + nb
+        r["supp_begin"], r["supp_end"] = m0, m0 + nsupp
+        r["stop_begin"], r["stop_end"] = m0 + nsupp, m0 + nm
+        r["hist_begin"] = r["hist_end"] = 0
+        if kind == "force":
+            r["flags"] = int(r["flags"]) | VS_ROW_FORCE
+            r["force_token"] = int(val)
+        self.params_h[q] = r
+        rb = ROW_DTYPE.itemsize
+        _dev_copy(self.params[q * rb:(q + 1) * rb], row)
+        edits = (p.bias_ids, p.bias_vals, p.mask_ids)
+        prev = self._edits[q]
+        if force_edits or prev is None or any(not np.array_equal(a, b) for a, b in zip(prev, edits)):
+            _dev_copy(self.bias_ids[b0:b0 + nb], p.bias_ids)
+            _dev_copy(self.bias_vals[b0:b0 + nb], p.bias_vals)
+            _dev_copy(self.mask_ids[m0:m0 + nm], p.mask_ids)
+            self._edits[q] = edits
+        self._act[q] = action
+
+    # ------------------------------------------------------------------ membership
+    def admit(self, sampler, slot: Optional[int] = None) -> int:
+        """Give a request a slot: its rng, history, produced and parameters are uploaded once. Returns the slot,
+        which is appended to `order`."""
+        if slot is None:
+            free = [q for q in range(self.S) if self.slot_sampler[q] is None]
+            if not free:
+                self._grow_slots(2 * self.S)
+                free = [q for q in range(self.S) if self.slot_sampler[q] is None]
+            slot = free[0]
+        elif not 0 <= slot < self.S or self.slot_sampler[slot] is not None:
+            raise ValueError(f"slot {slot} is not a free slot")
+        h = np.asarray(getattr(sampler, "history", []), dtype=np.int64).reshape(-1)
+        if h.size + 1 > self.cap:
+            if not self.grow_history:
+                raise ValueError(f"history of {h.size} tokens exceeds hist_cap {self.cap}")
+            self._grow_history(h.size + 64)
+        q = slot
+        self.slot_sampler[q] = sampler
+        st = np.zeros(1, dtype=STATE_DTYPE)
+        st[0]["rng"] = np.uint64(sampler.rng)
+        st[0]["hist_off"] = q * self.cap
+        st[0]["hist_len"] = h.size
+        st[0]["hist_cap"] = self.cap
+        st[0]["produced"] = int(sampler.produced)
+        st[0]["min_new_tokens"] = int(sampler.sp.min_new_tokens)
+        sb = STATE_DTYPE.itemsize
+        _dev_copy(self.state[q * sb:(q + 1) * sb], st)
+        _dev_copy(self.pool[q * self.cap:q * self.cap + h.size], h.astype(np.int32))
+        self._hmax[q] = h.size
+        self._prod[q] = int(sampler.produced)
+        self._edits[q] = None
+        self._upload_row(q, _NO_ACTION)
+        self.order.append(q)
+        return q
+
+    def retire(self, slot: int, write_back: bool = True):
+        """Free a slot (the request left the batch); by default its state is first copied into its Sampler."""
+        if not 0 <= slot < self.S or self.slot_sampler[slot] is None:
+            raise ValueError(f"slot {slot} is not live")
+        if write_back:
+            self._write_back_slots([slot])
+        self.slot_sampler[slot] = None
+        self._act[slot] = self._edits[slot] = None
+        self.order.remove(slot)
+
+    @property
+    def B(self) -> int:
+        return len(self.order)
+
+    @property
+    def samplers(self):
+        return [self.slot_sampler[q] for q in self.order]
+
+    # ------------------------------------------------------------------ steps
+    def _prepare(self, slots: Sequence[int], sync: bool) -> torch.Tensor:
+        """Budget actions, history capacity and the slots array for a step over `slots`."""
+        for q in slots:
+            s = self.slot_sampler[q]
+            if s is None:
+                raise ValueError(f"slot {q} is not live")
+            b = getattr(s, "budget", None)
+            if b is not None:
+                if not sync:
+                    raise ValueError("requests with a reasoning budget need step(sync=True): the host decides the "
+                                     "budget's action from the tokens of the previous step")
+                act = b.act(self._prod[q])
+                if act != self._act[q]:
+                    self._upload_row(q, act)
+        need = max(self._hmax[q] for q in slots) + 1
+        if need > self.cap and self.grow_history:
+            self._grow_history(need + 64)
+        key = tuple(slots)
+        if key != self._slots_key:
+            self._slots_t = torch.tensor(key, dtype=torch.int32).to(self.dev)
+            self._slots_key = key
+        return self._slots_t
+
+    def _launch(self, logits: torch.Tensor, slots_t: torch.Tensor, out: SampleOut):
+        n = logits.shape[0]
         L = _lib.load()
-        ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
-        rows = self.rows
-        rc = L.vs_sample_batch_state(logits.data_ptr(), _DTYPES[logits.dtype], self.B, self.V, logits.stride(0),
-                                     rows.params.data_ptr(), self.state.data_ptr(), self.pool.data_ptr(),
-                                     ptr(rows.bias_ids), ptr(rows.bias_vals), ptr(rows.mask_ids),
-                                     out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(),
-                                     out.keep.data_ptr(), self._ws.data_ptr(), self._ws.numel(),
+        ws = workspace(self.dev, L.vs_sample_workspace_bytes(n, self.V))
+        rc = L.vs_sample_batch_state(logits.data_ptr(), _DTYPES[logits.dtype], n, self.V, logits.stride(0),
+                                     self.params.data_ptr(), self.state.data_ptr(), self.pool.data_ptr(),
+                                     slots_t.data_ptr(), self.bias_ids.data_ptr(), self.bias_vals.data_ptr(),
+                                     self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
+                                     out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(),
                                      _stream_handle(self.dev))
         check(rc, "vs_sample_batch_state")
-        return out
+
+    def _check_logits(self, logits: torch.Tensor, n: int):
+        _require_cuda(logits, "logits")
+        if logits.dim() != 2 or logits.shape != (n, self.V) or logits.stride(1) != 1:
+            raise ValueError(f"logits must be [{n}, {self.V}] with unit stride along V")
+        if logits.dtype not in _DTYPES:
+            raise ValueError(f"unsupported logits dtype {logits.dtype}")
+
+    def step(self, logits: torch.Tensor, slots: Optional[Sequence[int]] = None, sync: bool = True,
+             out: Optional[SampleOut] = None):
+        """Sampler.choose for the requests of `slots` (default: `order`) on logits [n, V], row i for slots[i]:
+        draw, choose, accept, all on the device. sync=True returns a StepResult (host lists; timed-out rows
+        repeated cooperatively; budget bookkeeping done); sync=False returns the device SampleOut at once."""
+        slots = list(self.order if slots is None else slots)
+        n = len(slots)
+        if n == 0:
+            raise ValueError("no live requests to step")
+        if len(set(slots)) != n:
+            raise ValueError("a request can take only one row of a step")
+        self._check_logits(logits, n)
+        slots_t = self._prepare(slots, sync)
+        if out is None:
+            if self.out.ids.shape[0] != n:
+                self.out = alloc_out(n, self.dev)
+            out = self.out
+        self._launch(logits, slots_t, out)
+        for q in slots:
+            self._hmax[q] += 1
+        if not sync:
+            return out
+        host = out.block.cpu().numpy()
+        fl = host[2].view(np.uint32)
+        bad = np.nonzero(fl & OUT_TIMEOUT)[0]
+        if bad.size:
+            self._retry(logits, slots, bad, out, host)
+            fl = host[2].view(np.uint32)
+        if (fl & OUT_HIST_FULL).any() and self.grow_history:
+            raise VsError("vs_sample_batch_state: a history slot was full (the pool should have grown)")
+        ids = host[0].tolist()
+        for i, q in enumerate(slots):
+            b = getattr(self.slot_sampler[q], "budget", None)
+            if b is not None:
+                b.accept(self._prod[q], ids[i])
+            self._prod[q] += 1
+        return StepResult(ids, host[1].view(np.float32).tolist(), fl.tolist(), host[3].tolist(), out)
+
+    def _retry(self, logits, slots, bad, out, host):
+        """Repeat the rows that reported VS_OUT_TIMEOUT (they committed nothing) under a cooperative launch."""
+        L = _lib.load()
+        idx = bad.tolist()
+        sub_slots = [slots[i] for i in idx]
+        key = tuple(sub_slots)
+        sub_t = torch.tensor(key, dtype=torch.int32).to(self.dev)
+        sub_x = logits[torch.tensor(idx, device=self.dev)].contiguous()
+        sub_out = alloc_out(len(idx), self.dev)
+        reset_workspace(self.dev)
+        prev = L.vs_set_cooperative(1)
+        try:
+            self._launch(sub_x, sub_t, sub_out)
+            sub = sub_out.block.cpu().numpy()
+        finally:
+            L.vs_set_cooperative(prev)
+        if (sub[2].view(np.uint32) & OUT_TIMEOUT).any():
+            reset_workspace(self.dev)
+            raise VsError("vs_sample_batch_state: an inter-workgroup wait timed out, also under a cooperative launch")
+        ii = torch.tensor(idx, device=self.dev)
+        out.block[:, ii] = sub_out.block
+        host[:, idx] = sub
 
     def bind(self, logits_slots: Sequence[torch.Tensor]):
-        """A callable f(i) running step() on logits_slots[i] with every argument bound once (for serving loops that
-        reuse the same buffers): one C call, no host checks."""
+        """A callable f(i) running step(logits_slots[i], sync=False) for the current `order`, with every argument
+        bound once (serving loops that reuse the same buffers and membership): one C call, no host checks. Not for
+        requests with a reasoning budget, and the pool does not grow under it: size hist_cap for the calls made."""
+        n = len(self.order)
         for x in logits_slots:
-            _require_cuda(x, "logits")
-            if x.shape != (self.B, self.V) or x.stride(1) != 1 or x.dtype not in _DTYPES:
-                raise ValueError(f"logits slots must be [{self.B}, {self.V}] rows of a supported dtype")
+            self._check_logits(x, n)
+        if any(getattr(self.slot_sampler[q], "budget", None) is not None for q in self.order):
+            raise ValueError("bind() does not serve requests with a reasoning budget; use step()")
+        slots_t = self._prepare(self.order, sync=False)
+        if self.out.ids.shape[0] != n:
+            self.out = alloc_out(n, self.dev)
         fn = _lib.load().vs_sample_batch_state
-        ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
-        rows, out = self.rows, self.out
+        out = self.out
+        ws = workspace(self.dev, _lib.load().vs_sample_workspace_bytes(n, self.V))
         slots = [x.data_ptr() for x in logits_slots]
-        rest = (_DTYPES[logits_slots[0].dtype], self.B, self.V, logits_slots[0].stride(0), rows.params.data_ptr(),
-                self.state.data_ptr(), self.pool.data_ptr(), ptr(rows.bias_ids), ptr(rows.bias_vals),
-                ptr(rows.mask_ids), out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(),
-                out.keep.data_ptr(), self._ws.data_ptr(), self._ws.numel(), _stream_handle(self.dev))
-        keep = list(logits_slots)
+        rest = (_DTYPES[logits_slots[0].dtype], n, self.V, logits_slots[0].stride(0), self.params.data_ptr(),
+                self.state.data_ptr(), self.pool.data_ptr(), slots_t.data_ptr(), self.bias_ids.data_ptr(),
+                self.bias_vals.data_ptr(), self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
+                out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
+        keep = (list(logits_slots), slots_t, ws, self.params, self.state, self.pool, self.bias_ids, self.mask_ids)
 
         def call(i: int = 0) -> SampleOut:
             rc = fn(slots[i], *rest)
@@ -108,25 +379,30 @@ class DeviceSamplers:
 
         return call
 
+    # ------------------------------------------------------------------ host views
     def host_state(self) -> np.ndarray:
-        """The device state as a STATE_DTYPE array (synchronises)."""
+        """The device state of every slot as a STATE_DTYPE array (synchronises)."""
         return self.state.cpu().numpy().view(STATE_DTYPE).copy()
 
-    def history(self, r: int):
-        st = self.host_state()[r]
+    def history(self, slot: int):
+        st = self.host_state()[slot]
         off, n = int(st["hist_off"]), int(st["hist_len"])
         return [int(t) for t in self.pool[off:off + n].cpu().tolist()]
 
-    def write_back(self):
-        """Copy rng, counts/history and produced back into the host Sampler objects (synchronises)."""
+    def _write_back_slots(self, slots):
         st = self.host_state()
         pool = self.pool.cpu().numpy()
-        for r, s in enumerate(self.samplers):
-            off, n = int(st[r]["hist_off"]), int(st[r]["hist_len"])
-            h = [int(t) for t in pool[off:off + n]]
-            s.rng = int(st[r]["rng"])
+        for q in slots:
+            s = self.slot_sampler[q]
+            off, n = int(st[q]["hist_off"]), int(st[q]["hist_len"])
+            h = pool[off:off + n]
+            s.rng = int(st[q]["rng"])
             s.history = TokenHistory(h)
             s.counts = {}
-            for t in h:
+            for t in h.tolist():
                 s.counts[t] = s.counts.get(t, 0) + 1
-            s.produced = int(st[r]["produced"])
+            s.produced = int(st[q]["produced"])
+
+    def write_back(self):
+        """Copy rng, counts/history and produced of every live slot back into its Sampler (synchronises)."""
+        self._write_back_slots(list(self.order))
