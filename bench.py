@@ -171,7 +171,18 @@ def bench_dropin(torch, dev, d, steps):
         for i, s in enumerate(ss):
             s.choose(x[i])
     loop = (time.perf_counter() - t0) * 1e6 / nl
-    return batched, loop
+    # a serving engine holding the requests in a DeviceSamplers table: one synchronous step per batch
+    from volundr_amd import DeviceSamplers
+
+    ds = DeviceSamplers(mk(), Vx, hist_cap=8192, device=dev)
+    for _ in range(3):
+        ds.step(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ds.step(x)
+    served = (time.perf_counter() - t0) * 1e6 / n
+    return batched, loop, served
 
 
 def bench_state(torch, dev, d, steps, warmup, nslots):
@@ -429,10 +440,12 @@ def main():
             others["c3_greedy"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         if sel("c3_dropin"):
             dd = synth.CONFIGS["c3"](seed=0)
-            bt, lp = bench_dropin(torch, dev, dd, a.steps)
+            bt, lp, sv = bench_dropin(torch, dev, dd, a.steps)
             others["c3_dropin"] = {"sample_rows_for_us_per_step": round(bt, 1), "choose_loop_us_per_step": round(lp, 1),
-                                   "workload": "C3 through the drop-in routes, host work included (wall clock): one "
-                                               "sample_rows_for per step, and the per-row Sampler.choose loop"}
+                                   "device_samplers_step_us_per_step": round(sv, 1),
+                                   "workload": "C3 through the drop-in routes, host work included (wall clock, the "
+                                               "token ids back on the host): one sample_rows_for per step, the "
+                                               "per-row Sampler.choose loop, and DeviceSamplers.step (sync)"}
         if sel("c3_state"):
             dd = synth.CONFIGS["c3"](seed=0)
             (oe, ok), (we, wk), ab = bench_state(torch, dev, dd, a.steps, a.warmup, a.slots)

@@ -165,3 +165,48 @@ def test_argmax_vv_far_below_v(dev, vv):
     o2 = ops.sample_rows(xt[:2], rows2)
     torch.cuda.synchronize()
     assert int(o2.ids[0].item()) == want[0]
+
+
+def test_host_state_follows_the_device_pool(dev):
+    """sample_rows_for keeps each request's state in a device pool: the host fields read back what the device
+    advanced (rng, history, counts, produced); a host-side change (accept of a token, a new rng) is taken over by
+    the next device step; a Sampler that is dropped frees its slot."""
+    import gc
+
+    from volundr_amd import sampler as SM
+
+    rng = np.random.default_rng(99)
+    sps = [Sampling(top_k=20, temperature=0.9, repetition_penalty=1.4, seed=61),
+           Sampling(top_p=0.8, presence_penalty=0.7, seed=62)]
+    ss = [Sampler(sp, vocab_valid=VV) for sp in sps]
+    oracle = [OracleRequest(sp) for sp in sps]
+
+    def run(nsteps, label):
+        for step in range(nsteps):
+            x = _logits(rng, len(ss))
+            toks = sample_rows_for(torch.from_numpy(x).to(dev), ss)
+            for r in range(len(ss)):
+                res, nxt = oracle[r].step(x[r])
+                _check(f"{label} step {step} row {r}", toks[r], ss[r].last_logprob, res)
+                oracle[r].accept(toks[r], res, nxt)
+
+    run(3, "first")
+    for r, s in enumerate(ss):  # host reads pull the device state
+        assert s.rng == oracle[r].rng and list(s.history) == oracle[r].gen and s.produced == 3
+        assert sum(s.counts.values()) == 3
+    # host-side changes: an accepted token and a new generator state
+    ss[0].accept(7)
+    oracle[0].gen.append(7)
+    ss[1].rng = oracle[1].rng = 0xDEADBEEF1234567
+    run(3, "after host changes")
+    for r, s in enumerate(ss):
+        assert s.rng == oracle[r].rng and list(s.history) == oracle[r].gen
+    pool = ss[0]._vs[0]
+    live = len(pool.order)
+    s = None  # noqa: F841  (the loop variable held the last sampler)
+    del ss[1]
+    gc.collect()
+    oracle.pop(1)
+    run(1, "after a drop")
+    assert len(pool.order) == live - 1
+    assert SM._pools  # the pool is kept for later calls

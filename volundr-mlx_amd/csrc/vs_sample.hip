@@ -3059,6 +3059,31 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 // =================================================================================================================
 using namespace vs;
 
+// Workgroups of the sampling kernel per CU for a dynamic LDS size, cached per (device, dtype): the query costs more
+// than the rest of a launch's host work, and a serving loop launches one shape over and over.
+static hipError_t occupancy(int dev, int dtype, const void* kfn, size_t lds, int* per_cu) {
+  struct Entry {
+    size_t lds;
+    int per_cu;
+  };
+  static std::mutex mu;
+  static Entry cache[64][3];  // zero lds: not yet queried (every launch has LDS)
+  if (dev < 0 || dev >= 64 || dtype < 0 || dtype > 2)
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, kfn, SNT, lds);
+  std::lock_guard<std::mutex> lk(mu);
+  Entry& c = cache[dev][dtype];
+  if (c.lds != lds) {
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&c.per_cu, kfn, SNT, lds);
+    if (e != hipSuccess) {
+      c.lds = 0;
+      return e;
+    }
+    c.lds = lds;
+  }
+  *per_cu = c.per_cu;
+  return hipSuccess;
+}
+
 static bool use_cooperative() {
   static const bool coop = [] {
     const char* v = getenv("VS_COOPERATIVE");
@@ -3114,7 +3139,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
                     : dtype == VS_BF16 ? (const void*)vs_sample_kernel<VS_BF16>
                                        : (const void*)vs_sample_kernel<VS_F16>;
   int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, SNT, lds);
+  hipError_t e = occupancy(dv->device, dtype, kfn, lds, &per_cu);
   if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: occupancy query");
   const int maxres = per_cu * dv->cus;
   int RB = maxres / G;

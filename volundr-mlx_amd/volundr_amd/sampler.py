@@ -7,14 +7,16 @@ through `ops.sample_batch`. Batched callers (the scheduler's per-row loop, sched
 """
 from __future__ import annotations
 
+import threading
 import time
+import weakref
 from typing import Optional, Sequence
 
 import numpy as np
 import torch
 
 from . import _lib, ops
-from ._lib import OUT_NOFINITE, OUT_TIMEOUT, VsError
+from ._lib import OUT_FORCED, OUT_NOFINITE, OUT_TIMEOUT, VsError
 
 MASK = (1 << 64) - 1
 SAMPLING_EPS = 1e-6
@@ -137,60 +139,92 @@ class Budget:
 
 class Sampler:
     """Per-request sampler (volundr-mlx/sampler.py:58-156). Logits rows are GPU tensors; the arithmetic runs in
-    vs_sample_batch. `last_logprob` holds log p of the last sampled token under the distribution drawn from."""
+    the HIP library. `last_logprob` holds log p of the last sampled token under the distribution drawn from.
+
+    Once `choose` / `sample_rows_for` has served the request, its state (rng, the accepted tokens, produced) lives
+    in a device pool and the kernel advances it there; the host fields are a cache refreshed when read (`rng`,
+    `counts`, `history`, `produced` copy the device state back on first access after a device step). Assigning one of
+    them, `uniform()` and `accept()` change the host state, which the pool then takes over again at the next device
+    step (the state is uploaded once). Mutating `counts` or `history` in place is not seen by the pool."""
 
     def __init__(self, sp, prompt=(), think_ids=(None, None), vocab_valid=248077, request_id=0):
         self.sp, self.vv = sp, vocab_valid
         seed = sp.seed if sp.seed is not None else time.time_ns() ^ ((request_id * 0x9E3779B97F4A7C15) & MASK)
-        self.rng = (int(seed) | 1) & MASK
-        self.counts = {}
-        self.history = TokenHistory()  # the accepted tokens, in order (the multiset behind `counts`)
-        self.produced = 0
+        self._vs = None     # [pool, slot, valid, finalizer] while a device pool holds this request's state
+        self._ahead = False  # the pool has advanced the state past the host copy
+        self._rng = (int(seed) | 1) & MASK
+        self._counts = {}
+        self._history = TokenHistory()  # the accepted tokens, in order (the multiset behind `counts`)
+        self._produced = 0
         self.budget = None
         self.last_logprob = None
         if sp.reasoning_budget and think_ids[0] is not None and think_ids[1] is not None:
             self.budget = Budget(sp.reasoning_budget, sp.reasoning_budget_soft_bias, prompt, *think_ids)
 
+    # ---- host cache of the device-held state
+    def _pull(self):
+        """Copy the state the device pool advanced back into the host fields (synchronises)."""
+        if not self._ahead:
+            return
+        self._ahead = False
+        pool, q = self._vs[0], self._vs[1]
+        rng, off, n, produced = pool.slot_state(q)
+        have = len(self._history)
+        if n > have:
+            for t in pool.pool[off + have:off + n].cpu().tolist():
+                self._history.append(t)
+                self._counts[t] = self._counts.get(t, 0) + 1
+        self._rng, self._produced = rng, produced
+
+    def _host_changed(self):
+        if self._vs is not None:
+            self._vs[2] = False  # the pool re-takes the host state before its next step
+
+    def _field(name):  # noqa: N805
+        attr = "_" + name
+
+        def get(self):
+            self._pull()
+            return getattr(self, attr)
+
+        def put(self, v):
+            self._pull()
+            setattr(self, attr, TokenHistory(v) if name == "history" and not isinstance(v, TokenHistory) else v)
+            self._host_changed()
+
+        return property(get, put)
+
+    rng = _field("rng")
+    counts = _field("counts")
+    history = _field("history")
+    produced = _field("produced")
+    del _field
+
     def uniform(self) -> float:
         """xorshift64* (shifts 12, 25, 27; multiplier 0x2545F4914F6CDD1D), top 53 bits / 2^53 (sampler.py:69-75)."""
-        r = self.rng
+        self._pull()
+        r = self._rng
         r ^= r >> 12
         r ^= (r << 25) & MASK
         r ^= r >> 27
-        self.rng = r
+        self._rng = r
+        self._host_changed()
         return (((r * 0x2545F4914F6CDD1D) & MASK) >> 11) / float(1 << 53)
 
     def accept(self, tok):
+        self._pull()
         tok = int(tok)
-        self.history.append(tok)  # checks the id first, so a rejected id leaves every field unchanged
-        self.counts[tok] = self.counts.get(tok, 0) + 1
+        self._history.append(tok)  # checks the id first, so a rejected id leaves every field unchanged
+        self._counts[tok] = self._counts.get(tok, 0) + 1
         if self.budget is not None:
-            self.budget.accept(self.produced, tok)
-        self.produced += 1
-
-    def _extra(self):
-        """Budget action before sampling (sampler.py:85-92): ("force", tok) or the extra biases."""
-        if self.budget is None:
-            return None, []
-        kind, v = self.budget.act(self.produced)
-        if kind == "force":
-            return v, []
-        return None, (v if kind == "bias" else [])
+            self.budget.accept(self._produced, tok)
+        self._produced += 1
+        self._host_changed()
 
     def choose(self, logits) -> int:
-        """The next token from a logits row (GPU tensor [vocab]); records it (sampler.py:83-98)."""
-        forced, extra = self._extra()
-        if forced is not None:
-            self.accept(forced)
-            return forced
-        if extra or self.sp.needs_logits(self.vv, self.produced):
-            tok = self.sample(logits, extra)
-        else:
-            o = ops.verify_greedy(logits.reshape(1, 1, -1), None, vocab_valid=min(self.vv, logits.shape[-1]))
-            tok = int(o.argmax[0, 0].item())
-            self.last_logprob = float(o.logprobs[0, 0].item())
-        self.accept(tok)
-        return tok
+        """The next token from a logits row (GPU tensor [vocab]); records it (sampler.py:83-98). Runs as a one-row
+        sample_rows_for: the request's state stays on the device between calls."""
+        return sample_rows_for(logits.reshape(1, -1), [self])[0]
 
     def sample(self, x, extra=()) -> int:
         """Sampler.sample (sampler.py:100-156) for one row; x is a GPU tensor [V] (a host array is uploaded)."""
@@ -228,45 +262,76 @@ def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
     return out, host
 
 
+_pools: dict = {}  # (device index, V) -> DeviceSamplers holding the state of the Samplers these routes served
+_pool_lock = threading.Lock()
+
+
+def _release(pool, slot):
+    pool._released.append(slot)  # drained (the slot retired) at the pool's next use
+
+
+def _pool_for(dev: torch.device, V: int):
+    from .state import DeviceSamplers
+
+    key = (dev.index, int(V))
+    p = _pools.get(key)
+    if p is None:
+        p = DeviceSamplers([], V, hist_cap=4096, device=dev, capacity=64)
+        p._released = []
+        _pools[key] = p
+    while p._released:
+        p.retire(p._released.pop(), write_back=False)
+    return p
+
+
+def _slot_in(pool, s) -> int:
+    """The pool slot holding Sampler s's state. A Sampler seen for the first time, or whose host state changed since
+    the pool last stepped it, is (re)admitted: its host state is uploaded once; later steps upload nothing of it."""
+    ent = s._vs
+    if ent is not None and ent[0] is pool and ent[2]:
+        return ent[1]
+    if ent is not None:
+        s._pull()
+        ent[3].detach()
+        ent[0].retire(ent[1], write_back=False)
+        s._vs = None
+    q = pool.admit(weakref.proxy(s))
+    s._vs = [pool, q, True, weakref.finalize(s, _release, pool, q)]
+    return q
+
+
 def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Optional[Sequence[int]] = None):
     """One batched device call for the rows of logits [B, V] that the per-row loop of scheduler.py:416-425 would
     hand to Sampler.choose: returns the chosen token per sampler, updating each sampler's state exactly as
     `choose` does (budget force and bias, sampler.py:85-92; the draw is consumed only by rows that sample; rows that
-    need no logits take the argmax over [:vocab_valid], sampler.py:95-96)."""
-    rows = list(range(len(samplers))) if rows is None else list(rows)
-    toks: list = [None] * len(samplers)
-    todo, sps, us, hists, prods, extras, rng0, avv = [], [], [], [], [], [], [], []
-    for i, s in enumerate(samplers):
-        forced, extra = s._extra()
-        if forced is not None:
-            s.accept(forced)
-            toks[i] = forced
-            continue
-        todo.append(i)
-        sp = s.sp
-        argmax_only = not (extra or sp.needs_logits(s.vv, s.produced))
-        sps.append(sp)
-        rng0.append(s.rng)
-        us.append(s.uniform() if not sp.greedy else 0.0)
-        hists.append([] if argmax_only else s.history)
-        prods.append(s.produced)
-        extras.append(list(extra))
-        avv.append(s.vv if argmax_only else None)
-    if todo:
-        sel = [rows[i] for i in todo]
-        step = sel[1] - sel[0] if len(sel) > 1 else 1
-        if step > 0 and sel == list(range(sel[0], sel[-1] + 1, step)):
-            sub = logits[sel[0]:sel[-1] + 1:step]  # evenly spaced rows: a strided view, no gather copy
+    need no logits take the argmax over [:vocab_valid], sampler.py:95-96).
+
+    The samplers' state lives on the device (a DeviceSamplers pool per device and vocabulary), so a step uploads
+    nothing per request: the kernel draws, applies the penalties from the device history and records the token
+    there; each Sampler's host fields are refreshed from the device when next read."""
+    ops._require_cuda(logits, "logits")
+    if not samplers:
+        return []
+    if rows is None and logits.shape[0] == len(samplers):
+        sub = logits
+    else:
+        rows = list(range(len(samplers))) if rows is None else list(rows)
+        if len(rows) != len(samplers):
+            raise ValueError("one logits row per sampler is required")
+        step = rows[1] - rows[0] if len(rows) > 1 else 1
+        if step > 0 and rows == list(range(rows[0], rows[-1] + 1, step)):
+            sub = logits[rows[0]:rows[-1] + 1:step]  # evenly spaced rows: a strided view, no gather copy
         else:
-            sub = logits[sel]
-        _, host = _sample_checked(sub, sps, us, hists, prods, extras, argmax_vv=avv)
-        ids = host[0].tolist()
-        lps = host[1].view(np.float32).tolist()
-        fl = host[2].view(np.uint32).tolist()
-        for k, i in enumerate(todo):
-            if fl[k] & OUT_NOFINITE:
-                samplers[i].rng = rng0[k]  # no draw consumed (sampler.py:131-132)
-            samplers[i].last_logprob = lps[k]
-            samplers[i].accept(ids[k])
-            toks[i] = ids[k]
-    return toks
+            sub = logits[rows]
+    if sub.stride(-1) != 1:
+        sub = sub.contiguous()
+    with _pool_lock:
+        pool = _pool_for(logits.device, logits.shape[-1])
+        slots = [e[1] if (e := s._vs) is not None and e[0] is pool and e[2] else _slot_in(pool, s) for s in samplers]
+        res = pool.step(sub, slots)
+        lps, fl = res.logprobs, res.flags
+        for i, s in enumerate(samplers):
+            s._ahead = True
+            if not fl[i] & OUT_FORCED:
+                s.last_logprob = lps[i]
+    return res.ids

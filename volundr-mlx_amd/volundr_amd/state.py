@@ -50,7 +50,13 @@ class StepResult:
     logprobs: List[float]
     flags: List[int]
     keep: List[int]
-    out: SampleOut  # the device outputs of the same step
+    out: SampleOut  # the kernel's outputs (pinned host memory, rewritten by the next step of as many rows)
+
+
+def _alloc_out_host(n: int, dev: torch.device) -> SampleOut:
+    """alloc_out in pinned host memory, which the kernel writes directly (the device addresses host memory)."""
+    blk = torch.empty((4, n), dtype=torch.int32, pin_memory=dev.type == "cuda")
+    return SampleOut(blk[0], blk[1].view(torch.float32), blk[2], blk[3], blk)
 
 
 def _dev_copy(dst: torch.Tensor, src: np.ndarray):
@@ -89,12 +95,16 @@ class DeviceSamplers:
         self.order: List[int] = []  # live slots in admission order
         self._act: list = [None] * self.S  # the budget action each slot's uploaded row encodes
         self._edits: list = [None] * self.S  # per slot: (bias ids, bias vals, mask ids, n_supp) as uploaded
-        self._hmax = [0] * self.S  # upper bound of each slot's device history length
+        self._hmax = np.zeros(self.S, dtype=np.int64)  # upper bound of each slot's device history length
+        self._budget = set()  # live slots whose request has a reasoning budget
         self._prod = [0] * self.S  # produced, as of the last synchronous step (budget rows need it)
         self.params_h = np.zeros(self.S, dtype=ROW_DTYPE)
         self._alloc_tables()
-        self._slots_key = None
-        self._slots_t = None
+        self._slots_key = None  # the slots of the last step ...
+        self._key_steps = 0     # ... the steps taken with them since _hmax was last brought up to date
+        self._key_base = 0      # ... and their largest _hmax at that time
+        self._keys: dict = {}   # slots tuple -> (index array, device int32 tensor, budget rows)
+        self._host_out: dict = {}  # n -> SampleOut in pinned host memory that synchronous steps write into
         self.out = alloc_out(max(len(samplers), 1), dev)
         for s in samplers:
             self.admit(s)
@@ -120,9 +130,9 @@ class DeviceSamplers:
         ph = np.zeros(S2, dtype=ROW_DTYPE)
         ph[:S1] = self.params_h
         self.params_h = ph
-        for lst, fill in ((self.slot_sampler, None), (self._act, None), (self._edits, None), (self._hmax, 0),
-                          (self._prod, 0)):
+        for lst, fill in ((self.slot_sampler, None), (self._act, None), (self._edits, None), (self._prod, 0)):
             lst.extend([fill] * (S2 - S1))
+        self._hmax = np.concatenate([self._hmax, np.zeros(S2 - S1, dtype=np.int64)])
 
     def _grow_history(self, need: int):
         """Per-slot history capacity >= need: a new pool, each slot's history copied on the device, and every
@@ -220,10 +230,13 @@ class DeviceSamplers:
         sb = STATE_DTYPE.itemsize
         _dev_copy(self.state[q * sb:(q + 1) * sb], st)
         _dev_copy(self.pool[q * self.cap:q * self.cap + h.size], h.astype(np.int32))
+        self._flush()
         self._hmax[q] = h.size
         self._prod[q] = int(sampler.produced)
         self._edits[q] = None
         self._upload_row(q, _NO_ACTION)
+        if getattr(sampler, "budget", None) is not None:
+            self._budget.add(q)
         self.order.append(q)
         return q
 
@@ -235,7 +248,10 @@ class DeviceSamplers:
             self._write_back_slots([slot])
         self.slot_sampler[slot] = None
         self._act[slot] = self._edits[slot] = None
+        self._budget.discard(slot)
         self.order.remove(slot)
+        self._flush()
+        self._keys.clear()  # cached slot sets may name this slot
 
     @property
     def B(self) -> int:
@@ -246,28 +262,43 @@ class DeviceSamplers:
         return [self.slot_sampler[q] for q in self.order]
 
     # ------------------------------------------------------------------ steps
-    def _prepare(self, slots: Sequence[int], sync: bool) -> torch.Tensor:
-        """Budget actions, history capacity and the slots array for a step over `slots`."""
-        for q in slots:
-            s = self.slot_sampler[q]
-            if s is None:
-                raise ValueError(f"slot {q} is not live")
-            b = getattr(s, "budget", None)
-            if b is not None:
-                if not sync:
-                    raise ValueError("requests with a reasoning budget need step(sync=True): the host decides the "
-                                     "budget's action from the tokens of the previous step")
-                act = b.act(self._prod[q])
-                if act != self._act[q]:
-                    self._upload_row(q, act)
-        need = max(self._hmax[q] for q in slots) + 1
-        if need > self.cap and self.grow_history:
-            self._grow_history(need + 64)
+    def _flush(self):
+        """Bring the per-slot history bounds up to date with the steps taken since the slot set last changed."""
+        if self._slots_key is not None and self._key_steps:
+            self._hmax[self._keys[self._slots_key][0]] += self._key_steps
+        self._slots_key, self._key_steps = None, 0
+
+    def _prepare(self, slots: Sequence[int], sync: bool):
+        """Budget actions, history capacity and the slots array for a step over `slots`. Returns the slots as a
+        device int32 tensor."""
         key = tuple(slots)
         if key != self._slots_key:
-            self._slots_t = torch.tensor(key, dtype=torch.int32).to(self.dev)
-            self._slots_key = key
-        return self._slots_t
+            self._flush()
+            ent = self._keys.get(key)
+            if ent is None:
+                for q in key:
+                    if not 0 <= q < self.S or self.slot_sampler[q] is None:
+                        raise ValueError(f"slot {q} is not live")
+                if len(set(key)) != len(key):
+                    raise ValueError("a request can take only one row of a step")
+                if len(self._keys) >= 256:
+                    self._keys.clear()
+                ent = (np.asarray(key, dtype=np.int64), torch.tensor(key, dtype=torch.int32).to(self.dev),
+                       [(i, q) for i, q in enumerate(key) if q in self._budget])
+                self._keys[key] = ent
+            self._slots_key, self._key_base = key, int(self._hmax[ent[0]].max())
+        ent = self._keys[key]
+        if ent[2] and not sync:
+            raise ValueError("requests with a reasoning budget need step(sync=True): the host decides the budget's "
+                             "action from the tokens of the previous step")
+        for _, q in ent[2]:
+            act = self.slot_sampler[q].budget.act(self._prod[q])
+            if act != self._act[q]:
+                self._upload_row(q, act)
+        need = self._key_base + self._key_steps + 1
+        if need > self.cap and self.grow_history:
+            self._grow_history(need + 64)
+        return ent[1]
 
     def _launch(self, logits: torch.Tensor, slots_t: torch.Tensor, out: SampleOut):
         n = logits.shape[0]
@@ -293,61 +324,66 @@ class DeviceSamplers:
         """Sampler.choose for the requests of `slots` (default: `order`) on logits [n, V], row i for slots[i]:
         draw, choose, accept, all on the device. sync=True returns a StepResult (host lists; timed-out rows
         repeated cooperatively; budget bookkeeping done); sync=False returns the device SampleOut at once."""
-        slots = list(self.order if slots is None else slots)
+        slots = self.order if slots is None else slots
         n = len(slots)
         if n == 0:
             raise ValueError("no live requests to step")
-        if len(set(slots)) != n:
-            raise ValueError("a request can take only one row of a step")
         self._check_logits(logits, n)
         slots_t = self._prepare(slots, sync)
         if out is None:
-            if self.out.ids.shape[0] != n:
-                self.out = alloc_out(n, self.dev)
-            out = self.out
+            if sync:  # results land in pinned host memory: no copy, only the stream's completion is awaited
+                out = self._host_out.get(n)
+                if out is None:
+                    out = self._host_out[n] = _alloc_out_host(n, self.dev)
+            else:
+                if self.out.ids.shape[0] != n:
+                    self.out = alloc_out(n, self.dev)
+                out = self.out
         self._launch(logits, slots_t, out)
-        for q in slots:
-            self._hmax[q] += 1
+        self._key_steps += 1
         if not sync:
             return out
-        host = out.block.cpu().numpy()
+        if out.block.is_cuda:
+            hb = torch.empty((4, n), dtype=torch.int32)
+            hb.copy_(out.block)
+        else:
+            hb = out.block
+            if self.dev.type == "cuda":
+                torch.cuda.current_stream(self.dev).synchronize()
+        host = hb.numpy()
         fl = host[2].view(np.uint32)
-        bad = np.nonzero(fl & OUT_TIMEOUT)[0]
-        if bad.size:
-            self._retry(logits, slots, bad, out, host)
+        anyf = int(np.bitwise_or.reduce(fl))
+        if anyf & OUT_TIMEOUT:
+            self._retry(logits, list(slots), np.nonzero(fl & OUT_TIMEOUT)[0], out)
             fl = host[2].view(np.uint32)
-        if (fl & OUT_HIST_FULL).any() and self.grow_history:
+            anyf = int(np.bitwise_or.reduce(fl))
+        if anyf & OUT_HIST_FULL and self.grow_history:
             raise VsError("vs_sample_batch_state: a history slot was full (the pool should have grown)")
         ids = host[0].tolist()
-        for i, q in enumerate(slots):
-            b = getattr(self.slot_sampler[q], "budget", None)
-            if b is not None:
-                b.accept(self._prod[q], ids[i])
+        for i, q in self._keys[self._slots_key][2]:
+            self.slot_sampler[q].budget.accept(self._prod[q], ids[i])
             self._prod[q] += 1
         return StepResult(ids, host[1].view(np.float32).tolist(), fl.tolist(), host[3].tolist(), out)
 
-    def _retry(self, logits, slots, bad, out, host):
-        """Repeat the rows that reported VS_OUT_TIMEOUT (they committed nothing) under a cooperative launch."""
+    def _retry(self, logits, slots, bad, out):
+        """Repeat the rows that reported VS_OUT_TIMEOUT (they committed nothing) under a cooperative launch; their
+        results replace the flagged ones in `out`."""
         L = _lib.load()
         idx = bad.tolist()
-        sub_slots = [slots[i] for i in idx]
-        key = tuple(sub_slots)
-        sub_t = torch.tensor(key, dtype=torch.int32).to(self.dev)
+        sub_t = torch.tensor([slots[i] for i in idx], dtype=torch.int32).to(self.dev)
         sub_x = logits[torch.tensor(idx, device=self.dev)].contiguous()
         sub_out = alloc_out(len(idx), self.dev)
         reset_workspace(self.dev)
         prev = L.vs_set_cooperative(1)
         try:
             self._launch(sub_x, sub_t, sub_out)
-            sub = sub_out.block.cpu().numpy()
+            sub = sub_out.block.cpu()
         finally:
             L.vs_set_cooperative(prev)
-        if (sub[2].view(np.uint32) & OUT_TIMEOUT).any():
+        if (sub[2].numpy().view(np.uint32) & OUT_TIMEOUT).any():
             reset_workspace(self.dev)
             raise VsError("vs_sample_batch_state: an inter-workgroup wait timed out, also under a cooperative launch")
-        ii = torch.tensor(idx, device=self.dev)
-        out.block[:, ii] = sub_out.block
-        host[:, idx] = sub
+        out.block[:, torch.tensor(idx, device=out.block.device)] = sub.to(out.block.device)
 
     def bind(self, logits_slots: Sequence[torch.Tensor]):
         """A callable f(i) running step(logits_slots[i], sync=False) for the current `order`, with every argument
@@ -383,6 +419,12 @@ class DeviceSamplers:
     def host_state(self) -> np.ndarray:
         """The device state of every slot as a STATE_DTYPE array (synchronises)."""
         return self.state.cpu().numpy().view(STATE_DTYPE).copy()
+
+    def slot_state(self, slot: int):
+        """(rng, hist_off, hist_len, produced) of one slot, read from the device (synchronises)."""
+        sb = STATE_DTYPE.itemsize
+        st = self.state[slot * sb:(slot + 1) * sb].cpu().numpy().view(STATE_DTYPE)[0]
+        return int(st["rng"]), int(st["hist_off"]), int(st["hist_len"]), int(st["produced"])
 
     def history(self, slot: int):
         st = self.host_state()[slot]
