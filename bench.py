@@ -15,6 +15,8 @@ The other configurations (C1, C2, C4, C5) are reported under "other_configs" wit
 is C3 through vs_sample_batch_state (the per-request sampler state on the device; each step also accepts),
 "c3_dropin" C3 through sample_rows_for and the Sampler.choose loop (host work included, wall clock),
 "c3_greedy" C3's logits and histories with every row greedy (temperature 0);
+"c3_raw" / "c5_raw" the same rows with the raw token histories as the penalty input (the default, --hist-form pairs,
+passes each request's sorted (id, count) table, the form of Sampler.counts, built outside the timed region);
 "draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary;
 "lmhead_verify_*" is the bf16 lm_head with greedy verify fused in (vs_lmhead_verify_greedy), beside the unfused
 torch matmul + vs_verify_greedy.
@@ -36,17 +38,29 @@ WORKLOADS = {
     "c1": "C1: B=1 V=163840 fp32, top-k 20 (BASELINE configs[0])",
     "c2": "C2: greedy verify [1,17,163840] bf16 + drafts [1,16] (BASELINE configs[1])",
     "c3": "C3: B=16 V=163840 fp32 mixed-parameter sampling, histories 16x4096 (BASELINE configs[2])",
+    "c3_raw": "C3 with each history passed as its 4096 raw token ids instead of the (id, count) table",
     "c4": "C4: greedy verify [4,17,163840] bf16 + drafts [4,16] (BASELINE configs[3])",
     "c5": "C5: B=16 V=163840 fp32 near-flat, top-p 0.95, histories 16x32768 (BASELINE configs[4])",
+    "c5_raw": "C5 with each history passed as its 32768 raw token ids instead of the (id, count) table",
 }
+HIST_FORM = ("; penalty state passed as each request's sorted (id, count) table, the form of Sampler.counts "
+             "(sampler.py:77-78, 113-122), built from the history outside the timed region")
 PEAK_GBPS = 8000.0
 V = 163840
 
 
 def algo_bytes_sample(d, B):
-    """Logits read once + histories read once + per-row params + outputs (ids, logprob, flags, keep)."""
+    """Logits read once + the penalty state read once (raw histories: 4 bytes per token; (id, count) tables: 8 bytes
+    per distinct id) + per-row params + outputs (ids, logprob, flags, keep)."""
+    import numpy as np
+
     x = d["logits"]
-    h = 0 if d["hists"] is None else d["hists"].size * 4
+    if d["hists"] is None:
+        h = 0
+    elif d.get("hist_pairs"):
+        h = sum(8 * int(np.unique(r).size) for r in d["hists"])
+    else:
+        h = d["hists"].size * 4
     return x.size * 4 + h + B * 96 + B * 16
 
 
@@ -112,7 +126,7 @@ def prepared_slots(torch, dev, d, nslots):
     from volundr_amd import ops
 
     x = torch.from_numpy(d["logits"]).to(dev)
-    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"])
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"], hist_pairs=d.get("hist_pairs", False))
     preps = [ops.PreparedSample([x if i == 0 else x.clone()], rows.to(dev)) for i in range(nslots)]
     return (lambda i: preps[i](0)), preps
 
@@ -380,6 +394,8 @@ def main():
     ap.add_argument("--slots", type=int, default=32, help="rotating logits buffers (cold-HBM measurement)")
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--hist-form", choices=("pairs", "raw"), default="pairs",
+                    help="penalty input: sorted (id, count) tables (Sampler.counts) or the raw token histories")
     ap.add_argument("--no-others", action="store_true")
     ap.add_argument("--others", default="", help="comma-separated subset of other_configs to run (default: all)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -404,6 +420,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": n * 4, "steps": a.steps}))
         return
     d = synth.CONFIGS[a.config](seed=0)
+    d["hist_pairs"] = a.hist_form == "pairs"
     verify = "logits_bf16" in d
     if verify:
         (e2e, kern), (e2e_w, kern_w), algo, ntok = bench_verify(torch, dev, d, a.steps, a.warmup, a.slots)
@@ -426,16 +443,25 @@ def main():
             if name == a.config or not sel(name):
                 continue
             dd = synth.CONFIGS[name](seed=0)
+            dd["hist_pairs"] = a.hist_form == "pairs"
             (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others[name] = entry(oe, ok, we, ab, dd["logits"].shape[0])
             if not a.no_cpu:
                 others[name].update(boundary_rows(dd, oout))
+        for name in ("c3", "c5"):  # the same rows with the raw token histories as the penalty input
+            if a.hist_form != "pairs" or not sel(name + "_raw"):
+                continue
+            dd = synth.CONFIGS[name](seed=0)
+            (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
+            others[name + "_raw"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
+            others[name + "_raw"]["workload"] = WORKLOADS[name + "_raw"]
         if sel("c3_greedy"):
             # C3's logits and histories with every row greedy (temperature 0, same penalties): the argmax class
             from volundr_amd.session import Sampling
             dd = synth.CONFIGS["c3"](seed=0)
             dd["params"] = [Sampling(temperature=0.0, repetition_penalty=p.repetition_penalty,
                                      presence_penalty=p.presence_penalty) for p in dd["params"]]
+            dd["hist_pairs"] = a.hist_form == "pairs"
             (oe, ok), (we, wk), ab, oout = bench_sample(torch, dev, dd, a.steps, a.warmup, a.slots)
             others["c3_greedy"] = entry(oe, ok, we, ab, dd["logits"].shape[0])
         if sel("c3_dropin"):
@@ -486,7 +512,8 @@ def main():
         "metric": METRIC, "value": round(e2e, 2), "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(e2e / 1000.0, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if verify else "f32", "data": "synthetic",
-        "config": {"workload": WORKLOADS[a.config], "B": B, "V": V,
+        "config": {"workload": WORKLOADS[a.config] + (HIST_FORM if d.get("hist_pairs") and d.get("hists") is not None
+                                                      else ""), "B": B, "V": V,
                    "history_len": None if verify or d["hists"] is None else int(d["hists"].shape[1]),
                    "logit_slots": a.slots},
         "tokens_per_s": round(ntok / (e2e * 1e-6), 1),

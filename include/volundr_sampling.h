@@ -47,6 +47,11 @@ enum {
                            neutral penalties and no suppressed id below vocab_valid; the one condition that can change
                            per step, an active stop mask (produced < min_new_tokens with stop ids), is decided by the
                            kernel: a row whose stop range applies takes the ordinary greedy path over the full row */
+  VS_ROW_HIST_PAIRS = 8u, /* vs_sample_batch: the row's hist range holds the penalty counts as a table of (id, count)
+                            int32 pairs, ids ascending and unique (Sampler.counts, sampler.py:77-78, as :113-122 reads
+                            it), hist_begin even, instead of the raw token history; each workgroup then reads only
+                            the entries of its vocabulary range. Ignored by vs_sample_batch_state (its pool holds
+                            raw ids) */
   VS_ROW_FORCE = 4u /* the reasoning budget forces force_token (sampler.py:88-90, Sampler.choose returns it without
                        sampling): the row's logits are not read and no draw is consumed; the state entry point records
                        the token as Sampler.accept does */

@@ -12,11 +12,11 @@ from volundr_amd.session import Sampling
 pytestmark = pytest.mark.gpu
 
 
-def run(dev, x, params, u, hists=None, produced=None, dtype=torch.float32, label="", max_excused=None):
+def run(dev, x, params, u, hists=None, produced=None, dtype=torch.float32, label="", max_excused=None, pairs=False):
     xt = torch.from_numpy(x).to(dev).to(dtype)
     xr = xt.float().cpu().numpy()  # the oracle sees exactly the widened values the kernel reads
-    print(f"[{label}] B={x.shape[0]} V={x.shape[1]} dtype={dtype}", flush=True)
-    out = sample_batch(xt, params, u, hists, produced)
+    print(f"[{label}] B={x.shape[0]} V={x.shape[1]} dtype={dtype} pairs={pairs}", flush=True)
+    out = sample_batch(xt, params, u, hists, produced, hist_pairs=pairs)
     torch.cuda.synchronize()
     refs = [S.sample(xr[i], params[i], float(u[i]), S.counts_from_history(hists[i]) if hists is not None else {},
                      0 if produced is None else produced[i]) for i in range(x.shape[0])]
@@ -344,11 +344,55 @@ def test_repeated_calls_identical(dev, B):
         assert all(torch.equal(a, b) for a, b in zip(got, want)), f"call {rep + 2} differs"
 
 
-@pytest.mark.parametrize("name", ["c1", "c3", "c5"])
-def test_configs_full_size(dev, name):
+@pytest.mark.parametrize("name,pairs", [("c1", False), ("c3", False), ("c5", False), ("c3", True), ("c5", True)])
+def test_configs_full_size(dev, name, pairs):
     d = synth.CONFIGS[name](seed=0)
-    out, refs, nb = run(dev, d["logits"], d["params"], d["u"], d["hists"], label=name, max_excused=1)
+    out, refs, nb = run(dev, d["logits"], d["params"], d["u"], d["hists"], label=name, max_excused=1, pairs=pairs)
     print(f"{name}: {len(refs)} rows, {nb} CDF-boundary rows", flush=True)
+
+
+@pytest.mark.parametrize("V", [5003, 40000, 163840])
+def test_hist_pairs_equal_raw_histories(dev, V):
+    """Penalty counts as a sorted (id, count) table (VS_ROW_HIST_PAIRS) give bit-identical results to the raw
+    histories they count, and match the oracle: random rows with every penalty kind, ids at and above V, tables of
+    one entry, tables whose ids all lie in one workgroup's range, Zipf-dense and uniform histories."""
+    rng = np.random.default_rng(V)
+    B = 16
+    x = (rng.standard_normal((B, V)) * rng.choice([0.2, 1.0, 3.0], size=(B, 1))).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    ps = [Sampling(temperature=p.temperature, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p,
+                   repetition_penalty=float(rng.choice([1.1, 1.3, 0.8])), presence_penalty=0.3,
+                   frequency_penalty=float(rng.choice([0.0, 0.1]))) for p in ps]
+    hists = []
+    for r in range(B):
+        kind = r % 5
+        if kind == 0:
+            h = rng.integers(0, V, size=int(rng.integers(1, 4000)))
+        elif kind == 1:
+            h = (rng.zipf(1.1, size=3000) - 1) % V
+        elif kind == 2:
+            h = np.array([int(rng.integers(0, V))] * 3)      # one entry, count 3
+        elif kind == 3:
+            h = rng.integers(V // 2, V // 2 + 300, size=500)  # one workgroup's range
+        else:
+            h = np.concatenate([rng.integers(0, V, 200), np.array([V, V + 5, V + 5])])  # ids at and above V
+        hists.append(h)
+    u = rng.random(B)
+    a, refs, _ = run(dev, x, ps, u, hists, label=f"raw V{V}")
+    b, _, _ = run(dev, x, ps, u, hists, label=f"pairs V{V}", pairs=True)
+    for f in ("ids", "logprobs", "keep", "flags"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_hist_pairs_long_table(dev):
+    """A table of more entries than two probe rounds resolve (V = 248320, ~200k distinct ids): the search narrows
+    over further rounds."""
+    rng = np.random.default_rng(3)
+    B, V = 2, 248320
+    x = (rng.standard_normal((B, V)) * 0.5).astype(np.float32)
+    ps = [Sampling(top_p=0.9, repetition_penalty=1.5, frequency_penalty=0.05), Sampling(top_k=30, repetition_penalty=1.2)]
+    hists = [rng.integers(0, V, size=400000), rng.integers(0, V, size=300000)]
+    run(dev, x, ps, rng.random(B), hists, label="long pairs", pairs=True, max_excused=1)
 
 
 def test_sampler_shim_sequence(dev):

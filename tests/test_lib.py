@@ -141,3 +141,24 @@ def test_cooperative_setting_is_per_thread_and_restorable():
     th.join()
     assert seen == [0]  # the other thread's own setting was still the default
     assert L.vs_set_cooperative(0) == 1  # this thread's setting survived the other thread's call
+
+
+def test_pack_rows_hist_pairs():
+    """The (id, count) table form: ids ascending and unique, counts from the raw history or a counts dict (the same
+    table either way), the flag set, the range at an even word."""
+    from volundr_amd._lib import VS_ROW_HIST_PAIRS
+
+    hist = [5, 3, 5, 9, 3, 5, 200]
+    counts = {}
+    for t in hist:
+        counts[t] = counts.get(t, 0) + 1
+    sps = [Sampling(repetition_penalty=1.2), Sampling(repetition_penalty=1.2)]
+    a = pack_rows(sps, [0.1, 0.2], 100, [[1, 2, 3], hist], hist_pairs=True)
+    b = pack_rows(sps, [0.1, 0.2], 100, [{1: 1, 2: 1, 3: 1}, counts])
+    for p in (a, b):
+        r = p.params[1]
+        assert int(r["flags"]) & VS_ROW_HIST_PAIRS and int(r["hist_begin"]) % 2 == 0
+        assert p.hist[r["hist_begin"]:r["hist_end"]].tolist() == [3, 2, 5, 3, 9, 1, 200, 1]
+    assert np.array_equal(a.hist, b.hist) and np.array_equal(a.params, b.params)
+    c = pack_rows(sps[:1], [0.1], 100, [[]], hist_pairs=True)
+    assert not int(c.params[0]["flags"]) & VS_ROW_HIST_PAIRS and c.params[0]["hist_end"] == c.params[0]["hist_begin"]

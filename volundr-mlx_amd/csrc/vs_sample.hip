@@ -996,6 +996,34 @@ __device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, i
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Penalty counts given as a table (VS_ROW_HIST_PAIRS): n (id, count) pairs sorted by id with unique ids, the form of
+// Sampler.counts (sampler.py:77-78, iterated at :113-122). A workgroup needs the entries with ids in [lo, hi) only.
+// Thread t loads the id at entry pos(t) = t * n / SNT ahead (with the logits); the block counts the probes below lo
+// (c0) and below hi (c1). Every entry with an id in [lo, hi) then lies in [pos(c0 - 1) + 1, pos(c1)) (pos(-1) = -1,
+// pos(SNT) = n): at most 2 n / SNT entries beyond the wanted ones, which the range test of the edit skips.
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int64_t probe_at(int64_t n, int j) { return ((int64_t)j * n) / SNT; }
+
+__device__ __forceinline__ void pair_range(int64_t n, int32_t probe, int lo, int hi, int* red, int64_t* r0,
+                                           int64_t* r1) {
+  const int w = threadIdx.x / WAVE;
+  const int n0 = __popcll(__ballot(probe < lo)), n1 = __popcll(__ballot(probe < hi));
+  if (lane_id() == 0) {
+    red[w] = n0;
+    red[SNW + w] = n1;
+  }
+  __syncthreads();
+  int c0 = 0, c1 = 0;
+#pragma unroll
+  for (int i = 0; i < SNW; ++i) {
+    c0 += red[i];
+    c1 += red[SNW + i];
+  }
+  *r0 = c0 == 0 ? 0 : probe_at(n, c0 - 1) + 1;
+  *r1 = c1 == SNT ? n : probe_at(n, c1);
+}
+
 template <int DT>
 __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   typedef DTraits<DT> TR;
@@ -1083,10 +1111,16 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   }
   // ---- while the logits are in flight: the first batch of the history ids, and the count array cleared ----
   const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
-  const bool has_pen = A.has_hist && P.hist_end > P.hist_begin && (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
+  const bool pairs = (P.flags & VS_ROW_HIST_PAIRS) && !A.state;  // the state pool always holds raw ids
+  const int64_t npairs = (P.hist_end - P.hist_begin) >> 1;
+  const bool has_pen = A.has_hist && (pairs ? npairs > 0 : P.hist_end > P.hist_begin) &&
+                       (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
   HistWin hw;
   int4 hpre[HD][HB];
-  if (has_pen) {
+  int32_t probe = 0;  // pairs: the id at entry t * npairs / SNT, loaded with the logits
+  if (has_pen && pairs) {
+    probe = A.hist[P.hist_begin + 2 * probe_at(npairs, t)];
+  } else if (has_pen) {
     hw = hist_window(P.hist_begin, P.hist_end);
     if (hw.nv > 0) {
 #pragma unroll
@@ -1135,7 +1169,38 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     }
     __syncthreads();
   }
-  if (has_pen) {  // :113-122 over the multiset of generated tokens
+  if (has_pen && pairs) {  // :113-122 over the (id, count) table: each entry edits its own logit
+    int64_t p0, p1;
+    pair_range(npairs, probe, lo, hi, s.redi, &p0, &p1);
+    VS_TR(A, 24);
+    const int2* hp = (const int2*)(A.hist + P.hist_begin);  // hist_begin is even
+    constexpr int PU = 4;  // entries per lane in flight
+    for (int64_t p = p0 + t; p < p1; p += (int64_t)PU * SNT) {
+      int2 e[PU];
+#pragma unroll
+      for (int u = 0; u < PU; ++u) {
+        const int64_t q = p + (int64_t)u * SNT;
+        e[u] = hp[q < p1 ? q : p];
+      }
+#pragma unroll
+      for (int u = 0; u < PU; ++u) {
+        const int id = e[u].x;
+        const int32_t c = e[u].y;
+        // the bracket's entries outside [lo, hi) (and repeats past its end) are skipped
+        if (p + (int64_t)u * SNT < p1 && (unsigned)(id - lo) < (unsigned)(hi - lo)) {
+          float y = s.xv[id - lo];
+          if (rep != 1.0f) {
+            const float dv = y / rep, ml = y * rep;
+            y = y > 0.0f ? dv : ml;
+          }
+          const float fc = fpen * (float)c;
+          const float sub = fc + (c > 0 ? ppen : 0.0f);
+          s.xv[id - lo] = y - sub;
+        }
+      }
+    }
+    __syncthreads();
+  } else if (has_pen) {  // :113-122 over the multiset of generated tokens
     hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
     __syncthreads();
     VS_TR(A, 24);

@@ -17,6 +17,7 @@ VS_F32, VS_BF16, VS_F16 = 0, 1, 2
 VS_ROW_GREEDY = 1
 VS_ROW_ARGMAX_VV = 2
 VS_ROW_FORCE = 4
+VS_ROW_HIST_PAIRS = 8
 OUT_DRAW_BOUNDARY = 1 << 0
 OUT_TOPP_BOUNDARY = 1 << 1
 OUT_GREEDY = 1 << 3

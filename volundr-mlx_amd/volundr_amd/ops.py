@@ -14,7 +14,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import ROW_DTYPE, VS_BF16, VS_F16, VS_F32, VS_ROW_ARGMAX_VV, VS_ROW_GREEDY, check
+from ._lib import ROW_DTYPE, VS_BF16, VS_F16, VS_F32, VS_ROW_ARGMAX_VV, VS_ROW_GREEDY, VS_ROW_HIST_PAIRS, check
 
 _DTYPES = {torch.float32: VS_F32, torch.bfloat16: VS_BF16, torch.float16: VS_F16}
 _ws_lock = threading.Lock()
@@ -141,8 +141,27 @@ def argmax_only_ok(sp, vocab_valid: int) -> bool:
             and sp.presence_penalty == 0.0 and not any(t < vocab_valid for t in sp.suppress_tokens))
 
 
+def _pairs_of(hr) -> np.ndarray:
+    """Penalty counts as int32 (id, count) pairs, ids ascending: from a counts dict (Sampler.counts) or a history."""
+    if isinstance(hr, dict):
+        if not hr:
+            return np.zeros(0, np.int32)
+        ids = np.fromiter(hr.keys(), dtype=np.int64, count=len(hr))
+        cnt = np.fromiter(hr.values(), dtype=np.int64, count=len(hr))
+        o = np.argsort(ids, kind="stable")
+        ids, cnt = ids[o], cnt[o]
+    else:
+        h = hr.array() if hasattr(hr, "array") else np.asarray([] if hr is None else hr, dtype=np.int64).reshape(-1)
+        if h.size == 0:
+            return np.zeros(0, np.int32)
+        ids, cnt = np.unique(h, return_counts=True)
+    if ids.size and (ids.min() < 0 or ids.max() >= 2**31 or cnt.max() >= 2**31):
+        raise ValueError("counts must hold ids in [0, 2^31) and counts below 2^31")
+    return np.stack([ids, cnt], axis=1).astype(np.int32).reshape(-1)
+
+
 def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, extras=None,
-              stop_always: bool = False, argmax_vv=None) -> PackedRows:
+              stop_always: bool = False, argmax_vv=None, hist_pairs: bool = False) -> PackedRows:
     """Pack the per-row parameters the way Sampler.sample reads them (volundr-mlx/sampler.py:100-156).
 
     samplings : Sampling-like objects (session.Sampling); u : B uniform draws in [0, 1)
@@ -154,6 +173,8 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
     argmax_vv : per-row vocab_valid or None: a row given one is a request that needs no logits while its stop mask
                 is off, and then takes mx.argmax(logits[:vv]) as Sampler.choose does (sampler.py:95-96); its
                 Sampling must pass argmax_only_ok and it must carry no extras
+    hist_pairs : pass each row's penalty counts as a sorted (id, count) table (VS_ROW_HIST_PAIRS) instead of the raw
+                history; a history may then also be given as a counts dict (Sampler.counts)
     """
     B = len(samplings)
     u = np.asarray(u, dtype=np.float64).reshape(-1)
@@ -178,7 +199,14 @@ def pack_rows(samplings: Sequence, u, V: int, histories=None, produced=None, ext
             flags |= VS_ROW_ARGMAX_VV
             vv = min(vvr, V)
         hr = None if histories is None else histories[r]
-        if hasattr(hr, "array"):
+        if hist_pairs or isinstance(hr, dict):
+            h = _pairs_of(hr)
+            if hpos % 2:  # pairs start at an even word
+                hist_parts.append(np.zeros(1, np.int32))
+                hpos += 1
+            if h.size:
+                flags |= VS_ROW_HIST_PAIRS
+        elif hasattr(hr, "array"):
             h = hr.array()  # TokenHistory: int32, ids checked on append
         else:
             h = np.asarray([] if hr is None else hr, dtype=np.int64).reshape(-1)
@@ -264,11 +292,12 @@ def sample_rows(logits: torch.Tensor, rows: DeviceRows, out: Optional[SampleOut]
 
 
 def sample_batch(logits: torch.Tensor, samplings: Sequence, u, histories=None, produced=None,
-                 extras=None, argmax_vv=None) -> SampleOut:
+                 extras=None, argmax_vv=None, hist_pairs: bool = False) -> SampleOut:
     """Sampler.sample (sampler.py:100-156) for every row of logits [B, V], with the uniform draws supplied (rows
     given an argmax_vv take Sampler.choose's argmax over [:vv] instead, see pack_rows)."""
     _require_cuda(logits, "logits")
-    rows = pack_rows(samplings, u, logits.shape[-1], histories, produced, extras, argmax_vv=argmax_vv).to(logits.device)
+    rows = pack_rows(samplings, u, logits.shape[-1], histories, produced, extras, argmax_vv=argmax_vv,
+                     hist_pairs=hist_pairs).to(logits.device)
     return sample_rows(logits, rows)
 
 
