@@ -310,6 +310,64 @@ def bench_lmhead(torch, dev, steps, warmup, B=1, T=17):
     return (med(fb), med(fb)), (med(ub), med(ub)), algo
 
 
+def bench_lmhead_sample(torch, dev, steps, warmup, R=16):
+    """lm_head + Sampler.sample for R decode rows with top-k (and a greedy row), fused (vs_lmhead_sample: the GEMM
+    keeps each workgroup's candidates, a second launch draws) against torch's bf16 matmul writing the logits followed
+    by vs_sample_batch reading them. Same head as bench_lmhead; the row parameters of C3's top-k rows (k 20 / 50,
+    top-p, temperature) with no penalties."""
+    import numpy as np
+
+    from volundr_amd import ops
+    from volundr_amd.session import Sampling
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    h = torch.randn(R, LMH_K, generator=g, device=dev).to(torch.bfloat16)
+    W = (torch.randn(LMH_N, LMH_K, generator=g, device=dev) / 16).to(torch.bfloat16)
+    rng = np.random.default_rng(8)
+    sps = [Sampling(temperature=float(rng.uniform(0.6, 1.2)), top_k=int(rng.choice([20, 50])),
+                    top_p=float(rng.choice([0.8, 0.95, 1.0]))) for _ in range(R - 1)] + [Sampling(temperature=0.0)]
+    u = rng.random(R)
+    rows = ops.pack_rows(sps, u, LMH_N, None).to(dev)
+    out = ops.alloc_out(R, dev)
+    L = ops._lib.load()
+    ws = ops.workspace(dev, L.vs_lmhead_sample_workspace_bytes(R), "lmsample")
+    st = ops._stream_handle(dev)
+
+    def fused(i):
+        L.vs_lmhead_sample(h.data_ptr(), LMH_K, W.data_ptr(), LMH_K, LMH_N, LMH_K, R, rows.params.data_ptr(),
+                           out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(), out.keep.data_ptr(),
+                           ws.data_ptr(), ws.numel(), st)
+
+    lg = torch.empty(R, LMH_N, dtype=torch.bfloat16, device=dev)
+    out2 = ops.alloc_out(R, dev)
+
+    def unfused(i):
+        torch.matmul(h, W.T, out=lg)
+        ops.sample_rows(lg, rows, out2)
+
+    for _ in range(max(warmup // 10, 3)):
+        fused(0)
+        unfused(0)
+    torch.cuda.synchronize()
+
+    def block(fn, n=10):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / n
+
+    fb, ub = [], []
+    for _ in range(max(steps // 50, 3)):
+        fb.append(block(fused))
+        ub.append(block(unfused))
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+    algo = LMH_N * LMH_K * 2 + R * LMH_K * 2 + R * 96 + R * 16
+    return med(fb), med(ub), algo
+
+
 def launch_floor(torch, dev, steps):
     """Microseconds per launch of an empty kernel issued back to back through the library's C ABI, for a
     one-workgroup grid and for full-chip grids of 512-thread workgroups: one launch per Python call (the way the
@@ -499,6 +557,15 @@ def main():
                                        "both the median of alternating 10-call blocks")
             others[key]["unfused_us_per_step"] = round(ue, 2)
             others[key]["frac_of_8tbs"] = round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)
+        if sel("lmhead_sample_b16"):
+            fe, ue, ab = bench_lmhead_sample(torch, dev, a.steps, a.warmup)
+            others["lmhead_sample_b16"] = entry(fe, fe, fe, ab, 16)
+            others["lmhead_sample_b16"].update({
+                "workload": "bf16 lm_head 5120 -> 248320 + Sampler.sample for 16 decode rows (15 top-k 20/50 rows "
+                            "with temperature and top-p, 1 greedy): vs_lmhead_sample (candidates kept in the GEMM "
+                            "epilogue, no logits in HBM, 2 launches); 'unfused_us_per_step' = torch bf16 matmul + "
+                            "vs_sample_batch; both the median of alternating 10-call blocks",
+                "unfused_us_per_step": round(ue, 2), "frac_of_8tbs": round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)})
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
     parity = None if (a.no_cpu or verify) else boundary_rows(d, sout)
     floor = launch_floor(torch, dev, a.steps)

@@ -68,6 +68,8 @@ enum {
   VS_OUT_HIST_FULL = 1u << 7,     /* vs_sample_batch_state: the request's history slots were full, the token was
                                      not recorded (later penalties miss it) */
   VS_OUT_FORCED = 1u << 8,        /* the row returned its VS_ROW_FORCE token */
+  VS_OUT_UNSUPPORTED = 1u << 9,   /* vs_lmhead_sample: the row needs its logits (edits, or top_k off or above 64);
+                                     no result was computed */
   VS_OUT_TIMEOUT = 1u << 31       /* an inter-workgroup wait hit its spin limit: results of this row are invalid */
 };
 
@@ -184,6 +186,25 @@ int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W, int64_t l
                             vs_stream_t stream);
 
 size_t vs_lmhead_workspace_bytes(int B, int T);
+
+/* The bf16 lm_head with Sampler.sample fused after it, for R <= 16 decode rows: logits = bf16(h @ W^T) are reduced
+ * in the GEMM's epilogue (per workgroup: each top-k row's largest keys, the first-max key, max, sum-exp and finite
+ * count) and never written; a second launch merges them per row and draws as vs_sample_batch does.
+ *   h, ldh, W, ldw, N, K : as vs_lmhead_verify_greedy (h [R, ldh], W [N, ldw] bf16, K a multiple of 256)
+ *   params : device array [R] of vs_row_params (u supplied). Served rows: greedy (VS_ROW_GREEDY, with
+ *            VS_ROW_ARGMAX_VV the argmax over [0, vocab_valid)) and top-k rows with 1 <= top_k <= 64, temperature,
+ *            top_p and min_p, with no logit edits. A row with bias or suppressed ids, an active stop range, penalties
+ *            over a history, VS_ROW_FORCE or top_k off / above 64 is not computed: out_flags = VS_OUT_UNSUPPORTED
+ *            (such a batch takes the head and vs_sample_batch).
+ *   outputs: as vs_sample_batch (out_ids, out_logprob required; out_flags, out_keep may be NULL)
+ *   ws     : device workspace of at least vs_lmhead_sample_workspace_bytes(R) bytes (no zeroing needed)
+ * Replaces: volundr-mlx/volundr.py:958-968 (lm_head, bf16) feeding Sampler.sample (sampler.py:100-156) through the
+ * decode step's per-row loop (scheduler.py:382-392, 416-425). */
+int vs_lmhead_sample(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K, int R,
+                     const vs_row_params* params, int32_t* out_ids, float* out_logprob, uint32_t* out_flags,
+                     int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream);
+
+size_t vs_lmhead_sample_workspace_bytes(int R);
 
 /* The k largest logits of each of B rows, value descending, ties to the lower id (rows with fewer than k finite
  * logits pad with id -1 and value -inf). 1 <= k <= 256 (less when V needs many workgroups per row; the call fails

@@ -21,6 +21,7 @@
 //    per-lane partials.
 #include "vs_common.h"
 #include "vs_host.h"
+#include "vs_lmsample.h"
 
 #pragma clang fp contract(off)
 
@@ -65,9 +66,184 @@ struct LHArgs {
   float* out_lp;          // [R] or null
   uint16_t* out_logits;   // [R, ldo] bf16 or null
   int64_t ldo;
-  char* ws;  // [LWS_HEAD bytes: the arrival counters] then the workgroup partials (LParts)
+  char* ws;  // [LWS_HEAD bytes: the arrival counters] then the workgroup partials (LParts); sampling: LSParts
+  const vs_row_params* params;  // sampling epilogue: one row per position
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
+
+// Sampling epilogue. Each round, a top-k position's values go to LDS as 16-bit ordered values (the bf16 logit's
+// ord32 >> 16: equal values compare equal, zero = not finite) at fixed slots; after the last round one wave per
+// position selects its largest ones. ls_ord16 / ls_key64 convert between the two.
+constexpr int LS_VROUNDS = 4;  // rounds a workgroup may run (its tiles <= LS_VROUNDS * LNW * NTW)
+__device__ __forceinline__ uint32_t ls_ord16(float x) { return is_finite(x) ? ord32(x) >> 16 : 0u; }
+__device__ __forceinline__ u64 ls_key64(uint32_t v, uint32_t id) {
+  const uint32_t o = (v << 16) | ((v & 0x8000u) ? 0u : 0xFFFFu);  // a bf16 value's ord32 (see ord32)
+  return ((u64)o << 32) | (u64)(0xFFFFFFFFu - id);
+}
+
+// The kept keys of one position, written to list[0, LS_KMAX) (zero padded) with the largest to *head: every key
+// whose value reaches the k-th largest (a superset of the k largest when values tie), reduced to exactly the k
+// largest (ties to the lower id) only when they would not fit. vbuf holds the position's values, 4 per word (nw
+// words); `id` maps a slot to its vocabulary row. One wave; counts are ballots or lane sums.
+//  1. L = the k-th largest lane maximum (a lower bound of the k-th largest value: >= k lanes reach it), by a
+//     bisection with one compare per lane;
+//  2. the values >= L (usually k to 2k) become keys in the position's own LDS row (already read);
+//  3. the kept keys are selected among those few (ls_keep). Only when more than LS_CAND values reach L does the
+//     selection run over all the values.
+constexpr int LS_CAND = 512;
+template <int C>
+__device__ __forceinline__ void ls_keep(const u64* cb, int n, int k, u64* list, u64* head) {
+  constexpr int PER = C / WAVE;
+  const int ln = lane_id();
+  u64 kk[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = ln + WAVE * u;
+    kk[u] = i < n ? cb[i] : (u64)0;
+  }
+  auto count_ge = [&](u64 c) -> int {  // keys >= c (c > 0: zeros never count)
+    int m = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) m += (int)__popcll(__ballot(kk[u] >= c));
+    return m;
+  };
+  u64 T = 1;
+  if (n > k) {
+    uint32_t H = 0;
+    for (int b = 15; b >= 0; --b) {
+      const uint32_t c = H | (1u << b);
+      H = count_ge((u64)c << 48) >= k ? c : H;
+    }
+    T = (u64)H << 48;
+    if (count_ge(T) > LS_KMAX) {  // ties beyond the slots: the k-th largest key itself
+      for (int b = 47; b >= 0; --b) {
+        const u64 c = T | ((u64)1 << b);
+        T = count_ge(c) >= k ? c : T;
+      }
+    }
+  }
+  int m = 0;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) m += kk[u] >= T ? 1 : 0;
+  const int incl = wave_scan(m);
+  const int tot = __builtin_amdgcn_readlane(incl, WAVE - 1);
+  int p = incl - m;
+  u64 best = 0;
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (kk[u] >= T) {
+      list[p++] = kk[u];
+      best = kk[u] > best ? kk[u] : best;
+    }
+  for (int i = tot + ln; i < LS_KMAX; i += WAVE) list[i] = 0;
+  best = wave_max(best);
+  if (ln == 0) *head = best;
+}
+
+template <int NW, typename IdOf>
+__device__ __forceinline__ void ls_select(uint16_t* vbuf, int nw, int k, IdOf id, u64* list, u64* head) {
+  const int ln = lane_id();
+  uint32_t v[NW][4];
+  uint32_t lm = 0;
+#pragma unroll
+  for (int u = 0; u < NW; ++u) {
+    const int w = ln + WAVE * u;
+    const uint2 d = w < nw ? *(const uint2*)(vbuf + 4 * w) : make_uint2(0u, 0u);
+    v[u][0] = d.x & 0xFFFFu;
+    v[u][1] = d.x >> 16;
+    v[u][2] = d.y & 0xFFFFu;
+    v[u][3] = d.y >> 16;
+    lm = max3u(lm, max3u(v[u][0], v[u][1], 0u), max3u(v[u][2], v[u][3], 0u));
+  }
+  uint32_t L = 1;
+  if ((int)__popcll(__ballot(lm != 0)) >= k) {
+    L = 0;
+    for (int b = 15; b >= 0; --b) {
+      const uint32_t c = L | (1u << b);
+      L = (int)__popcll(__ballot(lm >= c)) >= k ? c : L;
+    }
+  }
+  int m = 0;
+#pragma unroll
+  for (int u = 0; u < NW; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m += v[u][e] >= L ? 1 : 0;
+  const int incl = wave_scan(m);
+  const int tot = __builtin_amdgcn_readlane(incl, WAVE - 1);
+  if (tot <= LS_CAND) {
+    u64* cb = (u64*)vbuf;  // the row has been read into registers: its space holds the candidate keys
+    int p = incl - m;
+#pragma unroll
+    for (int u = 0; u < NW; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (v[u][e] >= L) cb[p++] = ls_key64(v[u][e], id(4 * (ln + WAVE * u) + e));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (tot <= 2 * WAVE)
+      ls_keep<2 * WAVE>(cb, tot, k, list, head);  // the usual case: two candidates per lane
+    else
+      ls_keep<LS_CAND>(cb, tot, k, list, head);
+    return;
+  }
+  // Many values reach L (one lane held most of the largest): the selection runs over all of them. H = the largest
+  // 16-bit value with >= k values at or above it; ties at H beyond the slots keep their lowest ids.
+  auto count_ge = [&](uint32_t c) -> int {  // values >= c (c >= 1: zeros never count)
+    int cnt = 0;
+#pragma unroll
+    for (int u = 0; u < NW; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cnt += v[u][e] >= c ? 1 : 0;
+    return wave_sum(cnt);
+  };
+  uint32_t H = 0;
+  for (int b = 15; b >= 0; --b) {
+    const uint32_t c = H | (1u << b);
+    H = count_ge(c) >= k ? c : H;
+  }
+  uint32_t idmax = 0xFFFFFFFFu;
+  if (count_ge(H) > LS_KMAX) {
+    const int need = k - count_ge(H + 1);  // ties to keep (>= 1)
+    auto ties_below = [&](uint32_t c) -> int {  // ties with id < c
+      int cnt = 0;
+#pragma unroll
+      for (int u = 0; u < NW; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cnt += (v[u][e] == H && id(4 * (ln + WAVE * u) + e) < c) ? 1 : 0;
+      return wave_sum(cnt);
+    };
+    idmax = 0;  // the largest c with fewer than `need` ties below it: the need-th smallest tie id
+    for (int b = 30; b >= 0; --b) {
+      const uint32_t c = idmax | (1u << b);
+      idmax = ties_below(c) < need ? c : idmax;
+    }
+  }
+  m = 0;
+#pragma unroll
+  for (int u = 0; u < NW; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      m += (v[u][e] > H || (v[u][e] == H && (idmax == 0xFFFFFFFFu || id(4 * (ln + WAVE * u) + e) <= idmax))) ? 1 : 0;
+  const int incl2 = wave_scan(m);
+  const int tot2 = __builtin_amdgcn_readlane(incl2, WAVE - 1);
+  int p = incl2 - m;
+  u64 best = 0;
+#pragma unroll
+  for (int u = 0; u < NW; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t slot = 4 * (ln + WAVE * u) + e;
+      if (v[u][e] > H || (v[u][e] == H && (idmax == 0xFFFFFFFFu || id(slot) <= idmax))) {
+        const u64 key = ls_key64(v[u][e], id(slot));
+        list[p++] = key;
+        best = key > best ? key : best;
+      }
+    }
+  for (int i = tot2 + ln; i < LS_KMAX; i += WAVE) list[i] = 0;
+  best = wave_max(best);
+  if (ln == 0) *head = best;
+}
 
 // (m, s) pairs: s = sum exp(x - m) over finite x, accumulated in float64; the rescale factor exp(m - mm) <= 1 is a
 // float32 expf (relative error ~1e-7, far inside the logprob tolerance; a float64 exp per merge step made the
@@ -81,11 +257,22 @@ __device__ __forceinline__ void lse_merge(float& m, double& s, float m2, double 
   s = r;
 }
 
-// KC: k per LDS chunk (512 where K allows and two chunks of RP rows fit the LDS: fewer barriers; else 256)
-template <int NTT, int NTW, int KC>
+// SAMPLE: the sampling epilogue (one tile of <= 16 positions): besides the (first-max key, max, sum-exp) partials,
+// every position of a top-k row keeps its workgroup's largest keys, and the partials go to LSParts for
+// vs_lmhead_sample_merge_kernel instead of an in-launch merge.
+template <int NTT, int NTW, int KC, bool SAMPLE>
 __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))) void vs_lmhead_verify_kernel(
     LHArgs A) {
+  static_assert(!SAMPLE || NTT == 1, "the sampling epilogue serves one tile of positions");
+  static_assert(LS_KMAX == WAVE, "a wave writes a position's kept keys");
   constexpr int RP = 16 * NTT;  // positions padded to whole MFMA tiles
+  // sampling: per position, every round's values (LNW waves x 4 lanes x NTW x 4 per round) as 16-bit ordered values;
+  // rows padded by 8 bytes, so that the 16 positions a wave writes at once fall in different LDS banks
+  constexpr int LS_RV = LNW * 4 * NTW * 4;
+  constexpr int LS_VSTR = LS_VROUNDS * LS_RV + 4;
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[SAMPLE ? 16 : 1][SAMPLE ? LS_VSTR : 1];
+  __shared__ int scls[16], svlim[16];
+  __shared__ uint32_t rn[SAMPLE ? LNW : 1][SAMPLE ? RP : 1];
   constexpr int SPC = KC / KS;
   constexpr int HSTR = KC + 8;
   __shared__ __attribute__((aligned(16))) uint16_t hs[2][RP][HSTR];
@@ -107,8 +294,19 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   // accept lengths start at T-1 (every draft accepted); the merge lowers them to the first mismatch. A coherent
   // store: the merging workgroup may run on another XCD, and workgroup 0 arrives (after waiting for this store)
   // before the merge starts.
-  if (wg == 0)
+  if (!SAMPLE && wg == 0)
     for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
+  if constexpr (SAMPLE) {
+    if (t < 16) {
+      int vl = 0, c = LS_UNSUPPORTED;
+      if (t < R) c = ls_class(A.params[t], A.N, &vl);
+      scls[t] = c;
+      svlim[t] = vl;
+    }
+  }
+  uint32_t nfc[NTT];  // finite values of the lane's positions (sampling)
+#pragma unroll
+  for (int tt = 0; tt < NTT; ++tt) nfc[tt] = 0;
 
   // padded positions R..RP-1 read as zeros in both buffers
   {
@@ -277,6 +475,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
       const int pos = tt * 16 + m16;
+      const int vlim = SAMPLE ? svlim[m16] : A.vv;  // sampling: the row's own range ([0, vv) or the whole row)
       float xs[NTW][4];
       float best = -__builtin_inff();
       uint32_t mag = 0;
@@ -285,7 +484,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int v = tile[j] * 16 + kg * 4 + q;
-          const bool in = (tile[j] < t1) & (v < A.vv);
+          const bool in = (tile[j] < t1) & (v < vlim);
           const float x = (float)(__bf16)acc[j][tt][q];
           xs[j][q] = in ? x : -__builtin_inff();
           mag = in ? max3u(mag, __float_as_uint(x) & 0x7FFFFFFFu, 0u) : mag;
@@ -356,6 +555,22 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
           ps[tt] += (double)sacc;
         }
       }
+      if constexpr (SAMPLE) {
+        // the finite count, and for a top-k row this round's values (sampler.py:130-136 keeps finite logits only)
+        const int kc = scls[m16];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) nfc[tt] += is_finite(xs[j][q]) ? 1u : 0u;
+        if (kc >= 1) {
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            const uint2 d = make_uint2(ls_ord16(xs[j][0]) | (ls_ord16(xs[j][1]) << 16),
+                                       ls_ord16(xs[j][2]) | (ls_ord16(xs[j][3]) << 16));
+            *(uint2*)&vbuf[m16][r * LS_RV + ((wv * 4 + kg) * NTW + j) * 4] = d;
+          }
+        }
+      }
     }
   }
 #undef LH_HLOAD
@@ -371,6 +586,11 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       const double os = sh == 16 ? lane_xor<16>(ps[tt]) : lane_xor<32>(ps[tt]);
       pk[tt] = ok > pk[tt] ? ok : pk[tt];
       lse_merge(pm[tt], ps[tt], om, os);
+    }
+    if constexpr (SAMPLE) {
+      nfc[tt] += lane_xor<16>(nfc[tt]);
+      nfc[tt] += lane_xor<32>(nfc[tt]);
+      if (kg == 0) rn[wv][tt * 16 + m16] = nfc[tt];
     }
     if (kg == 0) {
       rk[wv][tt * 16 + m16] = pk[tt];
@@ -388,10 +608,51 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       k = rk[w][t] > k ? rk[w][t] : k;
       lse_merge(m, s, rm[w][t], rs[w][t]);
     }
-    const size_t ix = (size_t)t * LPMAX + wg;
-    st_dev(&parts.amkey[ix], k);
-    st_dev(&parts.mf[ix], m);
-    st_dev(&parts.se[ix], s);
+    if constexpr (SAMPLE) {
+      // the merge runs as a later launch: plain stores
+      const LSParts q = ls_parts(A.ws, R);
+      uint32_t nf = 0;
+#pragma unroll
+      for (int w = 0; w < LNW; ++w) nf += rn[w][t];
+      const size_t ix = (size_t)t * LS_PMAX + wg;
+      q.amkey[ix] = k;
+      q.mf[ix] = m;
+      q.se[ix] = s;
+      q.nfin[ix] = nf;
+    } else {
+      const size_t ix = (size_t)t * LPMAX + wg;
+      st_dev(&parts.amkey[ix], k);
+      st_dev(&parts.mf[ix], m);
+      st_dev(&parts.se[ix], s);
+    }
+  }
+  if constexpr (SAMPLE) {
+    // each wave selects the kept keys of its positions (w, w + 8) from every round's values (the barrier above
+    // ordered the rounds' LDS writes): the list and its largest key
+    VS_TR(A, 12);
+    const LSParts q = ls_parts(A.ws, R);
+    const int nw = rounds * LS_RV / 4;
+    // slot -> vocabulary row: slot = r * LS_RV + ((w * 4 + g) * NTW + j) * 4 + e holds row tile * 16 + g * 4 + e of
+    // tile t0 + r * LNW * NTW + j * LNW + w
+    auto id_of = [&](uint32_t slot) -> uint32_t {
+      const uint32_t rr = slot / LS_RV, rem = slot % LS_RV;
+      const uint32_t e = rem & 3, jj = (rem >> 2) % NTW, wk = (rem >> 2) / NTW;
+      const uint32_t tl = (uint32_t)t0 + rr * LNW * NTW + jj * LNW + (wk >> 2);
+      return tl * 16 + (wk & 3) * 4 + e;
+    };
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const int pos = wv + pp * LNW;
+      const int kc = pos < R ? scls[pos] : 0;
+      if (kc >= 1)
+        ls_select<LS_VROUNDS * LS_RV / 4 / WAVE>(vbuf[pos], nw, kc, id_of,
+                                                 q.lists + ((size_t)pos * LS_PMAX + wg) * LS_KMAX,
+                                                 q.heads + (size_t)pos * LS_PMAX + wg);
+      VS_TR(A, 14 + pp);
+    }
+    VS_TR(A, 13);
+    VS_TR_FLUSH(A);
+    return;
   }
   VS_TR(A, 20);
   if (!A.merge_in) {
@@ -583,7 +844,7 @@ constexpr int LMERGE_IN = 32;
 
 template <int NTT, int NTW, int KC>
 static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
-  hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW, KC>), dim3(P), dim3(LNT), 0, stream, a);
+  hipLaunchKernelGGL((vs_lmhead_verify_kernel<NTT, NTW, KC, false>), dim3(P), dim3(LNT), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "vs_lmhead_verify_greedy: launch");
   if (!a.merge_in) {
@@ -593,9 +854,64 @@ static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
   return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_verify_greedy: merge launch");
 }
 
+template <int KC>
+static int lmhead_sample_launch(const LHArgs& a, int P, hipStream_t stream) {
+  hipLaunchKernelGGL((vs_lmhead_verify_kernel<1, 4, KC, true>), dim3(P), dim3(LNT), 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_sample: launch");
+}
+
 }  // namespace vs
 
 using namespace vs;
+
+extern "C" size_t vs_lmhead_sample_workspace_bytes(int R) { return ls_workspace_bytes(R < 1 ? 1 : R); }
+
+extern "C" int vs_lmhead_sample(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K, int R,
+                                const vs_row_params* params, int32_t* out_ids, float* out_logprob,
+                                uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes,
+                                vs_stream_t stream) {
+  if (R < 0 || R > LS_RMAX) return fail(VS_EINVAL, "vs_lmhead_sample: need 0 <= R <= 16 rows");
+  if (R == 0) return VS_OK;
+  if (N < 1) return fail(VS_EINVAL, "vs_lmhead_sample: N < 1");
+  if (K < 256 || K % 256 != 0) return fail(VS_EINVAL, "vs_lmhead_sample: K must be a positive multiple of 256");
+  if (ldh < K || ldw < K || ldh % 8 != 0 || ldw % 8 != 0)
+    return fail(VS_EINVAL, "vs_lmhead_sample: row strides must be >= K and multiples of 8");
+  if (!h || !W || !params || !out_ids || !out_logprob || !ws)
+    return fail(VS_EINVAL, "vs_lmhead_sample: null pointer argument");
+  if ((uintptr_t)h % 16 != 0 || (uintptr_t)W % 16 != 0)
+    return fail(VS_EINVAL, "vs_lmhead_sample: h and W must be 16-byte aligned");
+  if ((int64_t)LNW * 8 * 16 * ldw * 2 >= ((int64_t)1 << 32))
+    return fail(VS_EINVAL, "vs_lmhead_sample: weight rows too long (ldw)");
+  if (ws_bytes < vs_lmhead_sample_workspace_bytes(R)) return fail(VS_EWORKSPACE, "vs_lmhead_sample: workspace too small");
+  const DevInfo* dv = dev_info();
+  if (!dv) return fail(VS_EHIP, "vs_lmhead_sample: no HIP device");
+  LHArgs a = {};
+  a.h = (const uint16_t*)h;
+  a.ldh = ldh;
+  a.W = (const uint16_t*)W;
+  a.ldw = ldw;
+  a.N = N;
+  a.vv = N;
+  a.K = K;
+  a.B = R;
+  a.T = 1;
+  a.R = R;
+  a.ntiles = (N + 15) / 16;
+  a.merge_in = 0;
+  a.ws = (char*)ws;
+  a.params = params;
+  a.trace = g_trace;
+  int P = dv->cus;
+  if (P > a.ntiles) P = a.ntiles;
+  if (P > LS_PMAX) P = LS_PMAX;
+  if ((a.ntiles + P - 1) / P > LS_VROUNDS * LNW * 4)
+    return fail(VS_EINVAL, "vs_lmhead_sample: N too large for the workgroups' value buffers");
+  const int rc = K % 512 == 0 ? lmhead_sample_launch<512>(a, P, (hipStream_t)stream)
+                              : lmhead_sample_launch<256>(a, P, (hipStream_t)stream);
+  if (rc != VS_OK) return rc;
+  return ls_merge_launch(params, R, N, P, (char*)ws, out_ids, out_logprob, out_flags, out_keep, (hipStream_t)stream);
+}
 
 extern "C" size_t vs_lmhead_workspace_bytes(int B, int T) {
   const size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;

@@ -18,6 +18,7 @@
 // No full-vocabulary sort happens anywhere.
 #include "vs_common.h"
 #include "vs_host.h"
+#include "vs_lmsample.h"
 
 #include <mutex>
 
@@ -3115,6 +3116,185 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   VS_TR_FLUSH(A);
 #undef FOR_ELEMS
 #undef ELEM
+}
+
+// =================================================================================================================
+// Merge of the fused head-and-sample kernel (vs_lmhead.hip): one workgroup per row reads the head workgroups'
+// partials and candidate lists (LSParts) and finishes Sampler.sample (sampler.py:127-156) as the TOPK and GREEDY
+// classes of vs_sample_kernel do.
+// =================================================================================================================
+constexpr int LSM_SEL = LS_KMAX * LS_KMAX;  // survivors at most: the keff lists whose heads reach the bound
+
+struct LSMArgs {
+  const vs_row_params* params;
+  int R, N, P;
+  char* ws;
+  int32_t* out_ids;
+  float* out_lp;
+  uint32_t* out_flags;
+  int32_t* out_keep;
+  unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
+};
+
+__global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) {
+  __shared__ u64 sel[LSM_SEL];
+  __shared__ u64 tk[LS_KMAX];
+  __shared__ u64 red64[NRED];
+  __shared__ double redf[NRED];
+  __shared__ int misc[NMISC];
+  __shared__ u64 bound;
+  __shared__ int qlist[LS_KMAX + 1];  // the qualifying lists, then their number
+  const int pos = blockIdx.x, t = threadIdx.x, ln = lane_id();
+  VS_TR_DECL(A);
+  VS_TR(A, 0);
+  const vs_row_params P = A.params[pos];
+  int vlim;
+  const int cls = ls_class(P, A.N, &vlim);
+  auto out = [&](int32_t tok, float lp, uint32_t fl, int32_t keep) {
+    VS_TR(A, 6);
+    VS_TR_FLUSH(A);
+    if (t == 0) {
+      A.out_ids[pos] = tok;
+      A.out_lp[pos] = lp;
+      if (A.out_flags) A.out_flags[pos] = fl;
+      if (A.out_keep) A.out_keep[pos] = keep;
+    }
+  };
+  if (cls == LS_UNSUPPORTED) {
+    out(-1, 0.0f, VS_OUT_UNSUPPORTED, 0);
+    return;
+  }
+  const LSParts q = ls_parts(A.ws, A.R);
+  const size_t base = (size_t)pos * LS_PMAX;
+  // The workgroups' partials (one per thread) and, for a top-k row, the list heads (wave 0, HPL per lane), all
+  // loaded at once.
+  static_assert(LS_PMAX <= SNT, "one partial per thread");
+  constexpr int HPL = LS_PMAX / WAVE;
+  const bool in = t < A.P;
+  u64 hv[HPL];
+  if (cls >= 1 && t < WAVE) {
+#pragma unroll
+    for (int u = 0; u < HPL; ++u) {
+      const int g = ln + WAVE * u;
+      hv[u] = q.heads[base + (g < A.P ? g : 0)];
+      hv[u] = g < A.P ? hv[u] : (u64)0;
+    }
+  }
+  const u64 k0 = q.amkey[base + (in ? t : 0)];
+  const float m0 = q.mf[base + (in ? t : 0)];
+  const double s0 = q.se[base + (in ? t : 0)];
+  const uint32_t n0 = q.nfin[base + (in ? t : 0)];
+  const u64 am = block_max<SNT>(in ? k0 : (u64)0, red64);
+  const float M = block_max<SNT>(in ? m0 : -__builtin_inff(), (float*)redf);
+  const int n = block_sum<SNT>(in ? (int)n0 : 0, misc);
+  const float L2E = 1.44269504088896340736f;
+  const double S = block_sum<SNT>((in && s0 > 0.0 && is_finite(M)) ? s0 * (double)__builtin_amdgcn_exp2f((m0 - M) * L2E)
+                                                                   : 0.0,
+                                  redf);
+  VS_TR(A, 1);
+  if (cls == LS_GREEDY) {  // sampler.py:127-128 (or :95-96 over [0, vv)): first maximum, log-softmax there
+    const float xj = am_is_nan(am) ? __builtin_nanf("") : key_value(am);
+    out((int32_t)key_index(am),
+        (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f,
+        VS_OUT_GREEDY, 0);
+    return;
+  }
+  if (n == 0) {  // sampler.py:131-132: np.argmax of a row without finite logits
+    out((int32_t)key_index(am), 0.0f, VS_OUT_NOFINITE, 0);
+    return;
+  }
+  const int keff = cls < n ? cls : n;  // sampler.py:133-134
+  // The bound T: the keff-th largest list head (heads are keys of the row, so its keff-th largest key reaches it),
+  // to its 16-bit value prefix; exact only when more than LS_KMAX heads share that prefix. Only the lists whose heads
+  // reach T can hold keys >= T (<= LS_KMAX lists of LS_KMAX keys); their indices go to LDS.
+  if (t < WAVE) {
+    auto count_ge = [&](u64 c) -> int {
+      int m = 0;
+#pragma unroll
+      for (int u = 0; u < HPL; ++u) m += (int)__popcll(__ballot(hv[u] >= c));
+      return m;
+    };
+    u64 T = 1;
+    if (count_ge(1) >= keff) {
+      uint32_t H = 0;
+      for (int b = 15; b >= 0; --b) {
+        const uint32_t c = H | (1u << b);
+        H = count_ge((u64)c << 48) >= keff ? c : H;
+      }
+      T = (u64)H << 48;
+      if (count_ge(T) > LS_KMAX) {
+        for (int b = 47; b >= 0; --b) {
+          const u64 c = T | ((u64)1 << b);
+          T = count_ge(c) >= keff ? c : T;
+        }
+      }
+    }
+    int nq = 0;
+#pragma unroll
+    for (int u = 0; u < HPL; ++u) {
+      const bool qual = hv[u] >= T;
+      const unsigned long long mb = __ballot(qual);
+      const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mb, 0u));
+      if (qual && nq + below < LS_KMAX) qlist[nq + below] = ln + WAVE * u;
+      nq += (int)__popcll(mb);
+    }
+    if (t == 0) {
+      bound = T;
+      qlist[LS_KMAX] = nq < LS_KMAX ? nq : LS_KMAX;
+      misc[0] = 0;
+    }
+  }
+  __syncthreads();
+  VS_TR(A, 2);
+  const u64 Mb = bound;
+  const int nq = qlist[LS_KMAX];
+  // the qualifying lists' slots, all loaded at once (LS_KMAX * LS_KMAX / SNT per thread)
+  constexpr int QPT = LS_KMAX * LS_KMAX / SNT;
+  u64 lv[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = u * SNT + t;
+    const int li = i / LS_KMAX < nq ? i / LS_KMAX : 0;
+    lv[u] = q.lists[(base + qlist[li]) * LS_KMAX + (i % LS_KMAX)];
+    lv[u] = i / LS_KMAX < nq ? lv[u] : (u64)0;
+  }
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) c += (lv[u] != 0 && lv[u] >= Mb) ? 1 : 0;
+  int p = wave_alloc(c, &misc[0]);
+#pragma unroll
+  for (int u = 0; u < QPT; ++u)
+    if (lv[u] != 0 && lv[u] >= Mb) sel[p++] = lv[u];
+  __syncthreads();
+  int Sv = misc[0];
+  Sv = Sv < LSM_SEL ? Sv : LSM_SEL;
+  VS_TR(A, 3);
+  VS_TRV(A, 10, Sv);
+  rank_sort(sel, Sv, tk, keff);  // sampler.py:140 on the survivors
+  VS_TR(A, 4);
+  Smem s = {};
+  s.misc = misc;
+  s.redf = redf;
+  const Final f = wave_sample(s, tk, keff, P);
+  out(f.token, f.lp, f.flags, f.keep);
+}
+
+int ls_merge_launch(const vs_row_params* params, int R, int N, int P, char* ws, int32_t* out_ids, float* out_lp,
+                    uint32_t* out_flags, int32_t* out_keep, hipStream_t stream) {
+  LSMArgs a;
+  a.params = params;
+  a.R = R;
+  a.N = N;
+  a.P = P;
+  a.ws = ws;
+  a.out_ids = out_ids;
+  a.out_lp = out_lp;
+  a.out_flags = out_flags;
+  a.out_keep = out_keep;
+  a.trace = g_trace;
+  hipLaunchKernelGGL(vs_lmhead_sample_merge_kernel, dim3(R), dim3(SNT), 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_lmhead_sample: merge launch");
 }
 
 }  // namespace vs

@@ -26,6 +26,7 @@ OUT_COOP = 1 << 5
 OUT_GATHER = 1 << 6
 OUT_HIST_FULL = 1 << 7
 OUT_FORCED = 1 << 8
+OUT_UNSUPPORTED = 1 << 9
 OUT_TIMEOUT = 1 << 31
 DEBUG_FORCE_RADIX = 1
 DEBUG_SPIN_LATER_BARRIERS = 2
@@ -49,7 +50,8 @@ assert STATE_DTYPE.itemsize == 32
 ABI_VERSION = 8
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
-           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
+           "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_lmhead_sample",
+           "vs_lmhead_sample_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
            "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_set_cooperative", "vs_set_debug")
 
 _lib = None
@@ -79,6 +81,10 @@ def load():
     L.vs_lmhead_verify_greedy.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, sz,
                                           vp]
     L.vs_lmhead_verify_greedy.restype = i32
+    L.vs_lmhead_sample.argtypes = [vp, i64, vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp]
+    L.vs_lmhead_sample.restype = i32
+    L.vs_lmhead_sample_workspace_bytes.argtypes = [i32]
+    L.vs_lmhead_sample_workspace_bytes.restype = sz
     L.vs_lmhead_workspace_bytes.argtypes = [i32, i32]
     L.vs_lmhead_workspace_bytes.restype = sz
     L.vs_launch_floor.argtypes = [i32, i32, sz, i32, vp]

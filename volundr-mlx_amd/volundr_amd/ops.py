@@ -563,3 +563,57 @@ def lmhead_verify_greedy(h: torch.Tensor, W: torch.Tensor, drafts: Optional[torc
                                     out.logprobs.data_ptr(), logits.data_ptr() if logits is not None else 0, N,
                                     ws.data_ptr(), ws.numel(), _stream_handle(dev)), "vs_lmhead_verify_greedy")
     return (out, logits) if return_logits else out
+
+
+LMHEAD_SAMPLE_KMAX = 64  # largest top_k the fused head-and-sample path serves
+LMHEAD_SAMPLE_RMAX = 16  # rows per call
+
+
+def lmhead_sample_ok(sp, V: int, history=None, produced: int = 0, extra=()) -> bool:
+    """True when vs_lmhead_sample serves this row without its logits: no logit edits (bias, suppressed ids, an
+    active stop range, penalties over a non-empty history) and either greedy or 1 <= top_k <= 64."""
+    if extra or sp.logit_bias or any(_wrap_id(t, V) is not None for t in sp.suppress_tokens):
+        return False
+    if produced < sp.min_new_tokens and sp.min_new_tokens > 0 and sp.stop_token_ids and \
+            any(_wrap_id(t, V) is not None for t in sp.stop_token_ids):
+        return False
+    if history is not None and len(history) and (sp.repetition_penalty != 1.0 or sp.frequency_penalty != 0.0
+                                                  or sp.presence_penalty != 0.0):
+        return False
+    return sp.greedy or (sp.top_k is not None and 1 <= sp.top_k <= LMHEAD_SAMPLE_KMAX)
+
+
+def lmhead_sample(h: torch.Tensor, W: torch.Tensor, samplings: Sequence, u, histories=None, produced=None,
+                  argmax_vv=None, out: Optional[SampleOut] = None) -> SampleOut:
+    """lm_head (bf16, volundr.py:958-968) + Sampler.sample (sampler.py:100-156) for R <= 16 decode rows in two launches
+    with no logits in HBM: h bf16 [R, K] final hidden states, W bf16 [N, K]. Rows that need their logits (see
+    lmhead_sample_ok) make the whole call take the unfused path (the bf16 matmul, then sample_batch)."""
+    _require_cuda(h, "h")
+    _require_cuda(W, "W")
+    if h.dtype != torch.bfloat16 or W.dtype != torch.bfloat16:
+        raise ValueError("h and W must be bf16")
+    if h.dim() != 2 or W.dim() != 2 or h.shape[1] != W.shape[1]:
+        raise ValueError("h must be [R, K] and W [N, K]")
+    R, K = h.shape
+    N = W.shape[0]
+    if h.stride(1) != 1 or W.stride(1) != 1:
+        raise ValueError("h and W need unit stride along K")
+    if len(samplings) != R:
+        raise ValueError("one Sampling per row")
+    dev = h.device
+    prods = [0] * R if produced is None else list(produced)
+    ok = R <= LMHEAD_SAMPLE_RMAX and all(
+        lmhead_sample_ok(sp, N, None if histories is None else histories[r], prods[r])
+        for r, sp in enumerate(samplings))
+    if not ok:
+        logits = h @ W.t()
+        rows = pack_rows(samplings, u, N, histories, produced, argmax_vv=argmax_vv).to(dev)
+        return sample_rows(logits, rows, out)
+    rows = pack_rows(samplings, u, N, histories, produced, argmax_vv=argmax_vv).to(dev)
+    out = out if out is not None else alloc_out(R, dev)
+    L = _lib.load()
+    ws = workspace(dev, L.vs_lmhead_sample_workspace_bytes(R), "lmsample")
+    check(L.vs_lmhead_sample(h.data_ptr(), h.stride(0), W.data_ptr(), W.stride(0), N, K, R, rows.params.data_ptr(),
+                             out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(), out.keep.data_ptr(),
+                             ws.data_ptr(), ws.numel(), _stream_handle(dev)), "vs_lmhead_sample")
+    return out
