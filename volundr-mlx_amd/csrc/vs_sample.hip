@@ -3147,7 +3147,26 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
   const int pos = blockIdx.x, t = threadIdx.x, ln = lane_id();
   VS_TR_DECL(A);
   VS_TR(A, 0);
+  // Every load of the row at once, before its class is known: the parameters, the workgroups' partials (one per
+  // thread) and the list heads (wave 0, HPL per lane; unused unless the row is a top-k row).
   const vs_row_params P = A.params[pos];
+  const LSParts q = ls_parts(A.ws, A.R);
+  const size_t base = (size_t)pos * LS_PMAX;
+  static_assert(LS_PMAX <= SNT, "one partial per thread");
+  constexpr int HPL = LS_PMAX / WAVE;
+  const bool in = t < A.P;
+  u64 hv[HPL];
+  if (t < WAVE) {
+#pragma unroll
+    for (int u = 0; u < HPL; ++u) {
+      const int g = ln + WAVE * u;
+      hv[u] = q.heads[base + (g < A.P ? g : 0)];
+    }
+  }
+  const u64 k0 = q.amkey[base + (in ? t : 0)];
+  const float m0 = q.mf[base + (in ? t : 0)];
+  const double s0 = q.se[base + (in ? t : 0)];
+  const uint32_t n0 = q.nfin[base + (in ? t : 0)];
   int vlim;
   const int cls = ls_class(P, A.N, &vlim);
   auto out = [&](int32_t tok, float lp, uint32_t fl, int32_t keep) {
@@ -3164,26 +3183,10 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
     out(-1, 0.0f, VS_OUT_UNSUPPORTED, 0);
     return;
   }
-  const LSParts q = ls_parts(A.ws, A.R);
-  const size_t base = (size_t)pos * LS_PMAX;
-  // The workgroups' partials (one per thread) and, for a top-k row, the list heads (wave 0, HPL per lane), all
-  // loaded at once.
-  static_assert(LS_PMAX <= SNT, "one partial per thread");
-  constexpr int HPL = LS_PMAX / WAVE;
-  const bool in = t < A.P;
-  u64 hv[HPL];
-  if (cls >= 1 && t < WAVE) {
+  if (t < WAVE) {
 #pragma unroll
-    for (int u = 0; u < HPL; ++u) {
-      const int g = ln + WAVE * u;
-      hv[u] = q.heads[base + (g < A.P ? g : 0)];
-      hv[u] = g < A.P ? hv[u] : (u64)0;
-    }
+    for (int u = 0; u < HPL; ++u) hv[u] = ln + WAVE * u < A.P ? hv[u] : (u64)0;
   }
-  const u64 k0 = q.amkey[base + (in ? t : 0)];
-  const float m0 = q.mf[base + (in ? t : 0)];
-  const double s0 = q.se[base + (in ? t : 0)];
-  const uint32_t n0 = q.nfin[base + (in ? t : 0)];
   const u64 am = block_max<SNT>(in ? k0 : (u64)0, red64);
   const float M = block_max<SNT>(in ? m0 : -__builtin_inff(), (float*)redf);
   const int n = block_sum<SNT>(in ? (int)n0 : 0, misc);
@@ -3216,10 +3219,17 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
     };
     u64 T = 1;
     if (count_ge(1) >= keff) {
+      // the value prefix on the heads' high words (32-bit compares)
+      uint32_t hh[HPL];
+#pragma unroll
+      for (int u = 0; u < HPL; ++u) hh[u] = (uint32_t)(hv[u] >> 32);
       uint32_t H = 0;
       for (int b = 15; b >= 0; --b) {
         const uint32_t c = H | (1u << b);
-        H = count_ge((u64)c << 48) >= keff ? c : H;
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < HPL; ++u) cnt += (int)__popcll(__ballot(hh[u] >= (c << 16)));
+        H = cnt >= keff ? c : H;
       }
       T = (u64)H << 48;
       if (count_ge(T) > LS_KMAX) {
