@@ -19,7 +19,9 @@ is C3 through vs_sample_batch_state (the per-request sampler state on the device
 passes each request's sorted (id, count) table, the form of Sampler.counts, built outside the timed region);
 "draft_propose" is the DFlash2 drafter's top-16 + candidate walk (vs_draft_propose) at the drafter's vocabulary;
 "lmhead_verify_*" is the bf16 lm_head with greedy verify fused in (vs_lmhead_verify_greedy), beside the unfused
-torch matmul + vs_verify_greedy.
+torch matmul + vs_verify_greedy; "lmhead_sample_b16" the head with top-k sampling fused in (vs_lmhead_sample) beside
+the matmul + vs_sample_batch; "read_ceiling" one streaming read of a buffer of the head weight's size
+(vs_stream_read), the rate the head kernels stream against.
 """
 import argparse
 import json
@@ -368,6 +370,40 @@ def bench_lmhead_sample(torch, dev, steps, warmup, R=16):
     return med(fb), med(ub), algo
 
 
+def read_ceiling(torch, dev, steps):
+    """The streaming ceiling of the head kernels: vs_stream_read over a buffer of the lm_head weight's size (2.54 GB),
+    one 512-thread workgroup per CU (the head kernel's grid) and four per CU; GB/s of the median of 10-call blocks."""
+    from volundr_amd import _lib
+
+    L = _lib.load()
+    nbytes = LMH_N * LMH_K * 2
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    out = torch.zeros(4096, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {"bytes": nbytes}
+    for mult in (1, 4):
+        call = lambda i: _lib.check(L.vs_stream_read(buf.data_ptr(), nbytes, cus * mult, out.data_ptr(), stream),  # noqa
+                                    "vs_stream_read")
+        for _ in range(3):
+            call(0)
+        torch.cuda.synchronize()
+        blocks = []
+        for _ in range(max(steps // 100, 5)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(10):
+                call(i)
+            e1.record()
+            torch.cuda.synchronize()
+            blocks.append(e0.elapsed_time(e1) * 100.0)  # us per call
+        us = sorted(blocks)[len(blocks) // 2]
+        res[f"{mult}_per_cu"] = {"us": round(us, 1), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                 "frac_of_8tbs": round(nbytes / (us * 1e-6) / 1e12 / 8.0, 4)}
+    del buf
+    return res
+
+
 def launch_floor(torch, dev, steps):
     """Microseconds per launch of an empty kernel issued back to back through the library's C ABI, for a
     one-workgroup grid and for full-chip grids of 512-thread workgroups: one launch per Python call (the way the
@@ -566,6 +602,10 @@ def main():
                             "epilogue, no logits in HBM, 2 launches); 'unfused_us_per_step' = torch bf16 matmul + "
                             "vs_sample_batch; both the median of alternating 10-call blocks",
                 "unfused_us_per_step": round(ue, 2), "frac_of_8tbs": round(ab / (fe * 1e-6) / 1e12 / 8.0, 4)})
+        if sel("read_ceiling"):
+            others["read_ceiling"] = read_ceiling(torch, dev, a.steps)
+            others["read_ceiling"]["workload"] = ("vs_stream_read: one streaming read of a buffer the size of the "
+                                                  "lm_head weight (the ceiling the fused head kernels stream against)")
     cpu = None if (a.no_cpu or verify) else cpu_baseline(d)
     parity = None if (a.no_cpu or verify) else boundary_rows(d, sout)
     floor = launch_floor(torch, dev, a.steps)

@@ -268,6 +268,12 @@ int vs_set_cooperative(int on);
  * takes the caller's per-call host overhead out of the figure). No counterpart in the reference. */
 int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stream_t stream);
 
+/* Read `bytes` (a multiple of 16, 16-byte aligned) once with `blocks` 512-thread workgroups, each over a contiguous
+ * share, eight 16-byte loads per lane in flight: a measurement hook (the streaming rate a kernel that reads its
+ * bytes once, such as the lm_head weight stream, can reach). `out` (device, >= blocks words) is written only on an
+ * impossible value. No counterpart in the reference. */
+int vs_stream_read(const void* p, size_t bytes, int blocks, uint32_t* out, vs_stream_t stream);
+
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 

@@ -51,9 +51,39 @@ namespace {
 // An empty kernel: the launch-floor measurement of vs_launch_floor (what a launch of a given shape costs with no
 // work in it, back to back on one stream).
 __global__ void vs_empty_kernel(int) {}
+
+// Streaming read: workgroup b reads its contiguous share of n16 16-byte words, eight loads per lane in flight, and
+// folds them into one word (written only on an impossible value, so the loads stay live). The rate a kernel whose
+// bytes stream in once, such as the lm_head weight of vs_lmhead_verify_greedy, can reach on the device.
+__global__ __launch_bounds__(512) void vs_stream_read_kernel(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
+  const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < n16 ? b0 + per : n16;
+  uint32_t acc = 0;
+  for (size_t i = b0 + threadIdx.x; i < b1; i += (size_t)512 * 8) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const size_t j = i + (size_t)u * 512;
+      v[u] = p[j < b1 ? j : i];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
+}
 }  // namespace
 
 extern "C" {
+
+int vs_stream_read(const void* p, size_t bytes, int blocks, uint32_t* out, vs_stream_t stream) {
+  if (!p || !out || blocks < 1 || bytes % 16 != 0 || (uintptr_t)p % 16 != 0)
+    return vs::fail(VS_EINVAL, "vs_stream_read: need a 16-byte aligned buffer of whole 16-byte words and blocks >= 1");
+  hipLaunchKernelGGL(vs_stream_read_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, (const uint4*)p,
+                     bytes / 16, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return vs::hip_fail(e, "vs_stream_read: launch");
+  return VS_OK;
+}
 
 int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stream_t stream) {
   if (blocks < 1 || threads < 1 || threads > 1024 || reps < 1) return vs::fail(VS_EINVAL, "vs_launch_floor: bad shape");

@@ -52,7 +52,7 @@ EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_byte
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_lmhead_sample",
            "vs_lmhead_sample_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
-           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_set_cooperative", "vs_set_debug")
+           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_stream_read", "vs_set_cooperative", "vs_set_debug")
 
 _lib = None
 
@@ -81,6 +81,8 @@ def load():
     L.vs_lmhead_verify_greedy.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, sz,
                                           vp]
     L.vs_lmhead_verify_greedy.restype = i32
+    L.vs_stream_read.argtypes = [vp, sz, i32, vp, vp]
+    L.vs_stream_read.restype = i32
     L.vs_lmhead_sample.argtypes = [vp, i64, vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp]
     L.vs_lmhead_sample.restype = i32
     L.vs_lmhead_sample_workspace_bytes.argtypes = [i32]
