@@ -130,20 +130,27 @@ int vs_sample_batch_noalloc(const void* logits, int dtype, int B, int V, int64_t
 
 size_t vs_sample_noalloc_scratch_bytes(void);
 
-/* Per-request sampler state kept on the device (Sampler, sampler.py:58-81). 32 bytes, 8-byte aligned. */
+/* Per-request sampler state kept on the device (Sampler, sampler.py:58-81). 48 bytes, 8-byte aligned.
+ * The penalty counts (Sampler.counts) are a table of (id, count) pairs sorted by id in a table pool, holding the
+ * history up to hist_base, plus the history tokens recorded since (pool[hist_off + hist_base, hist_off + hist_len)),
+ * which vs_state_fold merges into the table. */
 typedef struct vs_row_state {
   uint64_t rng;           /* xorshift64* state (Sampler.rng); the host seeds it as Sampler.__init__ does */
   int64_t hist_off;       /* first slot of this request's token history in the pool */
-  int32_t hist_len;       /* tokens recorded so far (the multiset behind Sampler.counts) */
+  int32_t hist_len;       /* tokens recorded so far (the history, in order) */
   int32_t hist_cap;       /* slots reserved from hist_off */
   int32_t produced;       /* Sampler.produced */
   int32_t min_new_tokens; /* the stop range of the row's params applies while produced < min_new_tokens */
+  int64_t tab_off;        /* first int32 of the (id, count) table in the table pool (even) */
+  int32_t tab_len;        /* its entries: the counts of history tokens [0, hist_base) */
+  int32_t hist_base;      /* history tokens already counted in the table */
 } vs_row_state;
 
 /* vs_sample_batch with the state on the device: row r of the logits belongs to request q = slots[r] (slots NULL:
  * q = r), whose parameters are params[q] and whose state is state[q]. The draw is Sampler.uniform() on
- * state[q].rng, the history is pool[hist_off, hist_off + hist_len), and the stop mask applies while
- * produced < min_new_tokens (params[q].u, hist_begin/hist_end are ignored; the stop range gives the stop ids).
+ * state[q].rng; the penalty counts are the table tabs[tab_off, tab_off + 2 tab_len) plus the history tokens
+ * pool[hist_off + hist_base, hist_off + hist_len) (tabs may be NULL when every tab_len is 0); the stop mask applies
+ * while produced < min_new_tokens (params[q].u, hist_begin/hist_end are ignored; the stop range gives the stop ids).
  * After the choice the request's state is advanced as Sampler.accept does (sampler.py:77-81): the token is appended
  * to the history (flag VS_OUT_HIST_FULL when hist_len == hist_cap), produced += 1, and the xorshift64* state moves on
  * when the row drew (not for greedy rows, rows with no finite logit, which return before self.uniform(),
@@ -154,9 +161,19 @@ typedef struct vs_row_state {
  * Replaces: Sampler.choose (sampler.py:83-98) for a batch of requests (scheduler.py:402-425), with uniform() and
  * accept() on the device; the reasoning budget's force and bias arrive as VS_ROW_FORCE and bias entries. */
 int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld, const vs_row_params* params,
-                          vs_row_state* state, int32_t* pool, const int32_t* slots, const int32_t* bias_ids,
-                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
-                          uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream);
+                          vs_row_state* state, int32_t* pool, const int32_t* tabs, const int32_t* slots,
+                          const int32_t* bias_ids, const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids,
+                          float* out_logprob, uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes,
+                          vs_stream_t stream);
+
+/* Merge the history tokens recorded since each listed request's last merge (pool[hist_off + hist_base, hist_off +
+ * hist_len), at most 512 of them) into its (id, count) table: the merged table is written to the other half of the
+ * request's table region (a region of 4 * tab_cap int32 at a multiple of 4 * tab_cap; tab_cap >= the number of
+ * distinct ids the request can hold), tab_off / tab_len / hist_base are updated. Stream-ordered with the sampling
+ * calls that read the tables. No counterpart in the reference (Sampler.counts is a dict updated per token,
+ * sampler.py:77-78). */
+int vs_state_fold(vs_row_state* state, const int32_t* pool, int32_t* tabs, int64_t tab_cap, const int32_t* slots, int n,
+                  vs_stream_t stream);
 
 /* Greedy speculative verify over logits [B, T, V] (row (b,t) starts at element (b*T + t)*ld).
  *   drafts     : int32 [B, T-1], the draft tokens inp[:, 1:] of the verify input
@@ -280,7 +297,7 @@ int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 8. */
+/* Library ABI version (increments on any signature or struct change): 9. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -147,3 +147,48 @@ def test_admit_retire_reuses_slots(dev):
     r, _ = o.step(x[0])
     _check("reused slot", res.ids[0], res.logprobs[0], r)
     assert ds.history(0) == [res.ids[0]]
+
+
+def test_long_run_folds_the_tables(dev):
+    """700 steps of penalised sampling: each slot's (id, count) table takes in its recent tokens every 256 or so
+    (vs_state_fold); every step must equal the oracle over the whole history, and the tables must hold exactly the
+    counts of the history they cover."""
+    from volundr_amd._lib import STATE_DTYPE
+
+    Vs = 3000
+    rng = np.random.default_rng(31)
+    sps = [Sampling(top_k=30, repetition_penalty=1.3, frequency_penalty=0.05, presence_penalty=0.2, seed=71),
+           Sampling(top_p=0.9, temperature=1.2, repetition_penalty=1.1, seed=72),
+           Sampling(temperature=0.0, repetition_penalty=2.0, frequency_penalty=0.5, seed=73)]
+    ss = [Sampler(sp, vocab_valid=Vs) for sp in sps]
+    pre = rng.integers(0, Vs, 300).tolist()
+    for t in pre:  # an earlier history for the first request: its table is built at admission
+        ss[0].history.append(t)
+        ss[0].counts[t] = ss[0].counts.get(t, 0) + 1
+    hists = [list(pre), [], []]
+    refs = []
+    for r, sp in enumerate(sps):
+        refs.append([S.seed_state(sp.seed)])
+    ds = DeviceSamplers(ss, Vs, hist_cap=256, device=dev)
+    print("[batching] long run: 700 steps, 3 rows", flush=True)
+    for step in range(700):
+        x = (rng.standard_normal((3, Vs)) * 1.5).astype(np.float32)
+        res = ds.step(torch.from_numpy(x).to(dev))
+        for r, sp in enumerate(sps):
+            nxt, u = S.xorshift64s_next(refs[r][0])
+            want = S.sample(x[r], sp, u, S.counts_from_history(hists[r]), len(hists[r]) - (300 if r == 0 else 0))
+            _check(f"long step {step} row {r}", res.ids[r], res.logprobs[r], want)
+            if want.kind == "sample":
+                refs[r][0] = nxt
+            hists[r].append(res.ids[r])
+    st = ds.host_state()
+    tabs = ds.tabs.cpu().numpy()
+    for r in range(3):
+        q = ds.order[r]
+        base, off, n = int(st[q]["hist_base"]), int(st[q]["tab_off"]), int(st[q]["tab_len"])
+        assert base > 256 and base <= len(hists[r])  # folded at least once
+        ids, cnt = np.unique(np.asarray(hists[r][:base]), return_counts=True)
+        tab = tabs[off:off + 2 * n].reshape(-1, 2)
+        assert np.array_equal(tab[:, 0], ids) and np.array_equal(tab[:, 1], cnt), f"row {r}: table"
+        assert ds.history(q) == hists[r]
+    assert ds.cap > 256  # the pool (and the tables) grew past the first capacity

@@ -26,7 +26,7 @@ def test_header_symbols_exported():
 def test_row_struct_size_matches_header():
     hdr = (ROOT / "include" / "volundr_sampling.h").read_text()
     assert "96 bytes" in hdr and _lib.ROW_DTYPE.itemsize == 96
-    assert "32 bytes" in hdr and _lib.STATE_DTYPE.itemsize == 32
+    assert "48 bytes" in hdr and _lib.STATE_DTYPE.itemsize == 48
     assert f"increments on any signature or struct change): {_lib.ABI_VERSION}." in hdr
 
 
@@ -36,7 +36,7 @@ def test_errors_without_device_calls():
     assert b"B < 0" in L.vs_last_error()
     assert L.vs_sample_batch(0, 0, 0, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_OK
     assert L.vs_verify_greedy(0, 0, 1, 0, 10, 10, 10, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
-    assert L.vs_sample_batch_state(0, 0, 1, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
+    assert L.vs_sample_batch_state(0, 0, 1, 10, 10, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == _lib.VS_EINVAL
     assert b"null state" in L.vs_last_error()
 
 

@@ -96,7 +96,7 @@ int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stre
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 8; }
+int vs_version(void) { return 9; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;

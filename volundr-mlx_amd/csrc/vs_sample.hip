@@ -44,6 +44,7 @@ constexpr int RANK_MAX = 512;    // largest set ranked by counting
 constexpr int KEYS_CAP = 8192;   // LDS key area (64 KB): the merged candidate lists of a row
 constexpr int KCAP = 256;        // largest top_k of the TOPK class
 constexpr int RPL_MAX = 64;      // rows per launch (workspace is sized for this many)
+constexpr int PAIRS_ALL = 2048;  // (id, count) tables up to this many entries are loaded whole by every workgroup
 // Row-barrier time bounds in ticks of the 100 MHz real-time counter. A row's workgroups arrive within ~10 us of one
 // another on an idle device; under a plain launch a wait that outlasts 200 us means some workgroup of the row is not
 // resident (other streams hold the CUs), and the row gives up so that the host can repeat the call cooperatively.
@@ -134,6 +135,7 @@ struct SampleArgs {
   float* list_vals;     // [B, list_k]
   int32_t* pool;        // history pool of the state entry point
   const int32_t* slots;  // state entry point: row r uses params[slots[r]] and state[slots[r]] (null: r)
+  const int32_t* tabs;   // state entry point: the (id, count) tables the states point into
   const int32_t* hist;
   const int32_t* bias_ids;
   const float* bias_vals;
@@ -997,6 +999,36 @@ __device__ __forceinline__ void hist_count(const int32_t* h, const HistWin& w, i
   }
 }
 
+// fn(id) for every id of a history window whose whole vectors are all in the prefetched batches r (w.nv <= HD *
+// SNT * HB); the unaligned head and tail ids are loaded again. Ids outside the window are not visited.
+template <typename Fn>
+__device__ __forceinline__ void hist_visit_prefetched(const int32_t* h, const HistWin& w, const int4 (&r)[HD][HB],
+                                                      Fn fn) {
+  const int t = threadIdx.x;
+  {
+    const int nh = (int)(w.a - w.b);
+    const int64_t tb = w.a + w.nv * 4;
+    const int nt = (int)(w.e - tb);
+    if (t < nh) fn(h[w.b + t]);
+    else if (t - nh < nt) fn(h[tb + (t - nh)]);
+  }
+  constexpr int64_t BATCH = (int64_t)SNT * HB;
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    const int64_t vb = d * BATCH;
+    if (vb >= w.nv) break;  // uniform
+#pragma unroll
+    for (int u = 0; u < HB; ++u) {
+      if (vb + (int64_t)u * SNT + t < w.nv) {
+        fn(r[d][u].x);
+        fn(r[d][u].y);
+        fn(r[d][u].z);
+        fn(r[d][u].w);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Penalty counts given as a table (VS_ROW_HIST_PAIRS): n (id, count) pairs sorted by id with unique ids, the form of
 // Sampler.counts (sampler.py:77-78, iterated at :113-122). A workgroup needs the entries with ids in [lo, hi) only.
@@ -1050,7 +1082,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     P = vs_row_params{1.0f, 1.0f, 0.0f, 0.0f, A.list_k, 0u, 1.0, 0.0, 0.0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   }
   // state entry point: the draw, the history range and the stop mask come from the request's device state
-  vs_row_state st = {0, 0, 0, 0, 0, 0};
+  vs_row_state st = {};
   uint64_t rng_next = 0;
   if (A.state) st = A.state[srow];
   // a token forced by the reasoning budget (sampler.py:88-90): the logits are not read, no draw is consumed
@@ -1068,10 +1100,12 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   if (A.state) {
     rng_next = xorshift64s_step(st.rng);
     P.u = xorshift64s_uniform(rng_next);
-    P.hist_begin = st.hist_off;
+    // the penalty counts: the table (history up to hist_base) plus the tokens recorded since
+    P.hist_begin = st.hist_off + st.hist_base;
     P.hist_end = st.hist_off + st.hist_len;
     if (st.produced >= st.min_new_tokens) P.stop_end = P.stop_begin;
   }
+  const int64_t tlen = (A.state && A.tabs) ? st.tab_len : 0;  // table entries of a state row
   char* rws = A.ws + (size_t)row * ROW_WS;
   RowCtl* ctl = (RowCtl*)rws;
   Part* parts = (Part*)(rws + OFF_PART);
@@ -1114,13 +1148,29 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   const float rep = P.repetition_penalty, fpen = P.frequency_penalty, ppen = P.presence_penalty;
   const bool pairs = (P.flags & VS_ROW_HIST_PAIRS) && !A.state;  // the state pool always holds raw ids
   const int64_t npairs = (P.hist_end - P.hist_begin) >> 1;
-  const bool has_pen = A.has_hist && (pairs ? npairs > 0 : P.hist_end > P.hist_begin) &&
+  const bool has_pen = A.has_hist && (pairs ? npairs > 0 : (P.hist_end > P.hist_begin || tlen > 0)) &&
                        (rep != 1.0f || fpen != 0.0f || ppen != 0.0f);
   HistWin hw;
   int4 hpre[HD][HB];
-  int32_t probe = 0;  // pairs: the id at entry t * npairs / SNT, loaded with the logits
+  // An (id, count) table (pairs, or a state row's table) of up to PAIRS_ALL entries is loaded whole with the logits,
+  // PAIRS_ALL / SNT entries per thread, and each workgroup takes the entries of its range from registers; a longer
+  // one is searched (probe: the id at entry t * n / SNT, loaded with the logits) and its bracket loaded after.
+  const int2* tabp = (const int2*)(pairs ? A.hist + P.hist_begin : (tlen > 0 ? A.tabs + st.tab_off : nullptr));
+  const int64_t tabn = pairs ? npairs : tlen;
+  const bool tab_all = tabn > 0 && tabn <= PAIRS_ALL;
+  int2 tabe[PAIRS_ALL / SNT];
+  int32_t probe = 0;
+  if (has_pen && tab_all) {
+#pragma unroll
+    for (int u = 0; u < PAIRS_ALL / SNT; ++u) {
+      const int64_t i = (int64_t)u * SNT + t;
+      tabe[u] = tabp[i < tabn ? i : 0];
+      tabe[u].x = i < tabn ? tabe[u].x : -1;
+    }
+  } else if (has_pen && tabn > 0) {
+    probe = tabp[probe_at(tabn, t)].x;
+  }
   if (has_pen && pairs) {
-    probe = A.hist[P.hist_begin + 2 * probe_at(npairs, t)];
   } else if (has_pen) {
     hw = hist_window(P.hist_begin, P.hist_end);
     if (hw.nv > 0) {
@@ -1170,7 +1220,25 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     }
     __syncthreads();
   }
-  if (has_pen && pairs) {  // :113-122 over the (id, count) table: each entry edits its own logit
+  if (has_pen && pairs && tab_all) {  // :113-122 over the (id, count) table: each entry edits its own logit
+#pragma unroll
+    for (int u = 0; u < PAIRS_ALL / SNT; ++u) {
+      const int id = tabe[u].x;
+      const int32_t c = tabe[u].y;
+      if ((unsigned)(id - lo) < (unsigned)(hi - lo)) {
+        float y = s.xv[id - lo];
+        if (rep != 1.0f) {
+          const float dv = y / rep, ml = y * rep;
+          y = y > 0.0f ? dv : ml;
+        }
+        const float fc = fpen * (float)c;
+        const float sub = fc + (c > 0 ? ppen : 0.0f);
+        s.xv[id - lo] = y - sub;
+      }
+    }
+    __syncthreads();
+    VS_TR(A, 24);
+  } else if (has_pen && pairs) {
     int64_t p0, p1;
     pair_range(npairs, probe, lo, hi, s.redi, &p0, &p1);
     VS_TR(A, 24);
@@ -1201,9 +1269,65 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
     }
     __syncthreads();
+  } else if (has_pen && A.state && (tlen == 0 || tab_all) && hw.nv <= (int64_t)HD * SNT * HB) {
+    // A state row whose table is in registers and whose recent tokens are all prefetched: the recent tokens are
+    // counted, then each table entry edits its logit with its total count and clears the recent count of its id,
+    // then the first visit of each id left among the recent tokens claims its count and edits (sampler.py:113-122).
+    hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
+    __syncthreads();
+    auto edit = [&](int i, uint32_t c) {
+      float y = s.xv[i];
+      if (rep != 1.0f) {
+        const float dv = y / rep, ml = y * rep;
+        y = y > 0.0f ? dv : ml;
+      }
+      const float fc = fpen * (float)c;
+      s.xv[i] = y - (fc + ppen);
+    };
+    if (tab_all) {
+#pragma unroll
+      for (int u = 0; u < PAIRS_ALL / SNT; ++u)
+        if ((unsigned)(tabe[u].x - lo) < (unsigned)(hi - lo)) {
+          const int i = tabe[u].x - lo;
+          edit(i, (uint32_t)tabe[u].y + s.cnt[i]);
+          s.cnt[i] = 0;
+        }
+      __syncthreads();
+    }
+    hist_visit_prefetched(A.hist, hw, hpre, [&](int id) {
+      if ((unsigned)(id - lo) < (unsigned)(hi - lo)) {
+        const uint32_t c = atomicExch(&s.cnt[id - lo], 0u);
+        if (c) edit(id - lo, c);
+      }
+    });
+    __syncthreads();
+    VS_TR(A, 24);
   } else if (has_pen) {  // :113-122 over the multiset of generated tokens
     hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
     __syncthreads();
+    if (tab_all) {  // a state row's table adds its counts (ids unique: plain updates after the counting above)
+#pragma unroll
+      for (int u = 0; u < PAIRS_ALL / SNT; ++u)
+        if ((unsigned)(tabe[u].x - lo) < (unsigned)(hi - lo)) s.cnt[tabe[u].x - lo] += (uint32_t)tabe[u].y;
+      __syncthreads();
+    } else if (tlen > 0) {
+      int64_t p0, p1;
+      pair_range(tlen, probe, lo, hi, s.redi, &p0, &p1);
+      const int2* tp = (const int2*)(A.tabs + st.tab_off);
+      constexpr int PU = 4;
+      for (int64_t p = p0 + t; p < p1; p += (int64_t)PU * SNT) {
+        int2 e[PU];
+#pragma unroll
+        for (int u = 0; u < PU; ++u) {
+          const int64_t q = p + (int64_t)u * SNT;
+          e[u] = tp[q < p1 ? q : p];
+        }
+#pragma unroll
+        for (int u = 0; u < PU; ++u)
+          if (p + (int64_t)u * SNT < p1 && (unsigned)(e[u].x - lo) < (unsigned)(hi - lo)) s.cnt[e[u].x - lo] += (uint32_t)e[u].y;
+      }
+      __syncthreads();
+    }
     VS_TR(A, 24);
     auto penalised = [&](float y, uint32_t c) -> float {
       if (rep != 1.0f) {
@@ -3358,7 +3482,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
                          const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
                          uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes, vs_stream_t stream,
                          int list_k = 0, int32_t* list_ids = nullptr, float* list_vals = nullptr,
-                         int rows_cap = RPL_MAX, const int32_t* slots = nullptr) {
+                         int rows_cap = RPL_MAX, const int32_t* slots = nullptr, const int32_t* tabs = nullptr) {
   if (B < 0) return fail(VS_EINVAL, "vs_sample_batch: B < 0");
   if (B == 0) return VS_OK;
   if (V < 1) return fail(VS_EINVAL, "vs_sample_batch: V < 1");
@@ -3435,6 +3559,7 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   a.state = state;
   a.pool = pool;
   a.slots = slots;
+  a.tabs = tabs;
   a.hist = state ? pool : hist;
   a.bias_ids = bias_ids;
   a.bias_vals = bias_vals;
@@ -3479,13 +3604,126 @@ extern "C" int vs_topk_batch(const void* logits, int dtype, int B, int V, int64_
 
 extern "C" int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t ld,
                                      const vs_row_params* params, vs_row_state* state, int32_t* pool,
-                                     const int32_t* slots, const int32_t* bias_ids, const float* bias_vals,
-                                     const int32_t* mask_ids, int32_t* out_ids, float* out_logprob,
-                                     uint32_t* out_flags, int32_t* out_keep, void* ws, size_t ws_bytes,
-                                     vs_stream_t stream) {
+                                     const int32_t* tabs, const int32_t* slots, const int32_t* bias_ids,
+                                     const float* bias_vals, const int32_t* mask_ids, int32_t* out_ids,
+                                     float* out_logprob, uint32_t* out_flags, int32_t* out_keep, void* ws,
+                                     size_t ws_bytes, vs_stream_t stream) {
   if (!state) return fail(VS_EINVAL, "vs_sample_batch_state: null state");
   return sample_launch(logits, dtype, B, V, ld, params, state, pool, nullptr, bias_ids, bias_vals, mask_ids, out_ids,
-                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream, 0, nullptr, nullptr, RPL_MAX, slots);
+                       out_logprob, out_flags, out_keep, ws, ws_bytes, stream, 0, nullptr, nullptr, RPL_MAX, slots,
+                       tabs);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// vs_state_fold: one 512-thread workgroup per listed request merges its recent history tokens (<= FOLD_MAX) into
+// its (id, count) table, writing the merged table to the other half of its table region.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int FOLD_MAX = 512;
+__global__ __launch_bounds__(SNT) void vs_state_fold_kernel(vs_row_state* state, const int32_t* pool, int32_t* tabs,
+                                                            int64_t tab_cap, const int32_t* slots) {
+  __shared__ u64 raw[FOLD_MAX];    // the recent tokens as (id << 32 | position), then sorted
+  __shared__ u64 srt[FOLD_MAX];
+  __shared__ int32_t uid[FOLD_MAX];  // distinct recent ids, ascending
+  __shared__ int32_t ucnt[FOLD_MAX];
+  __shared__ int32_t ulb[FOLD_MAX];  // each one's lower bound in the table
+  __shared__ int32_t ufound[FOLD_MAX];
+  __shared__ int32_t newpre[FOLD_MAX + 1];  // new ids (not in the table) before index j
+  __shared__ int red[NRED];
+  const int t = threadIdx.x;
+  const int q = slots ? slots[blockIdx.x] : blockIdx.x;
+  vs_row_state* S = state + q;
+  const vs_row_state st = *S;
+  const int nr = st.hist_len - st.hist_base;
+  if (nr <= 0) return;
+  const int n = nr < FOLD_MAX ? nr : FOLD_MAX;  // the host folds before FOLD_MAX tokens accumulate
+  for (int i = t; i < n; i += SNT) raw[i] = ((u64)(uint32_t)pool[st.hist_off + st.hist_base + i] << 32) | (u64)i;
+  __syncthreads();
+  // ascending by (id, position): the rank of each key (keys are unique)
+  for (int i = t; i < n; i += SNT) {
+    const u64 k = raw[i];
+    int r = 0;
+    for (int j = 0; j < n; ++j) r += raw[j] < k ? 1 : 0;
+    srt[r] = k;
+  }
+  __syncthreads();
+  // distinct ids and their counts: a run head starts each id
+  int nu;
+  {
+    int heads = 0;
+    for (int i = t; i < n; i += SNT) heads += (i == 0 || (srt[i] >> 32) != (srt[i - 1] >> 32)) ? 1 : 0;
+    nu = block_sum<SNT>(heads, red);
+    __syncthreads();
+    for (int i = t; i < n; i += SNT) {
+      if (i == 0 || (srt[i] >> 32) != (srt[i - 1] >> 32)) {
+        int u = 0;  // the run's index: heads before it
+        for (int j = 1; j <= i; ++j) u += ((srt[j] >> 32) != (srt[j - 1] >> 32)) ? 1 : 0;
+        int e = i + 1;
+        while (e < n && (srt[e] >> 32) == (srt[i] >> 32)) ++e;
+        uid[u] = (int32_t)(srt[i] >> 32);
+        ucnt[u] = e - i;
+      }
+    }
+  }
+  __syncthreads();
+  const int2* tab = (const int2*)(tabs + st.tab_off);
+  const int64_t tl = st.tab_len;
+  // each distinct recent id: its lower bound in the table and whether it is there
+  for (int j = t; j < nu; j += SNT) {
+    int64_t b = 0, e = tl;
+    while (b < e) {
+      const int64_t m = (b + e) >> 1;
+      if (tab[m].x < uid[j]) b = m + 1;
+      else e = m;
+    }
+    ulb[j] = (int32_t)b;
+    ufound[j] = (b < tl && tab[b].x == uid[j]) ? 1 : 0;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int c = 0;
+    for (int j = 0; j < nu; ++j) {
+      newpre[j] = c;
+      c += ufound[j] ? 0 : 1;
+    }
+    newpre[nu] = c;
+  }
+  __syncthreads();
+  const int64_t region = (int64_t)4 * tab_cap;
+  const int64_t base = st.tab_off - st.tab_off % region;
+  const int64_t alt = st.tab_off == base ? base + 2 * tab_cap : base;
+  int2* out = (int2*)(tabs + alt);
+  // table entries, shifted past the new ids that go before them, with the recent counts added
+  for (int64_t i = t; i < tl; i += SNT) {
+    const int2 e = tab[i];
+    int lo = 0, hi = nu;  // the first distinct recent id >= e.x
+    while (lo < hi) {
+      const int m = (lo + hi) >> 1;
+      if (uid[m] < e.x) lo = m + 1;
+      else hi = m;
+    }
+    const int add = (lo < nu && uid[lo] == e.x) ? ucnt[lo] : 0;
+    out[i + newpre[lo]] = make_int2(e.x, e.y + add);
+  }
+  // new ids: before table entry ulb[j], after the new ids before them
+  for (int j = t; j < nu; j += SNT)
+    if (!ufound[j]) out[ulb[j] + newpre[j]] = make_int2(uid[j], ucnt[j]);
+  __syncthreads();
+  if (t == 0) {
+    S->tab_off = alt;
+    S->tab_len = (int32_t)(tl + newpre[nu]);
+    S->hist_base = st.hist_base + n;
+  }
+}
+
+extern "C" int vs_state_fold(vs_row_state* state, const int32_t* pool, int32_t* tabs, int64_t tab_cap,
+                             const int32_t* slots, int n, vs_stream_t stream) {
+  if (n < 0) return fail(VS_EINVAL, "vs_state_fold: n < 0");
+  if (n == 0) return VS_OK;
+  if (!state || !pool || !tabs || tab_cap < 1) return fail(VS_EINVAL, "vs_state_fold: null pointer or tab_cap < 1");
+  hipLaunchKernelGGL(vs_state_fold_kernel, dim3(n), dim3(SNT), 0, (hipStream_t)stream, state, pool, tabs, tab_cap,
+                     slots);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VS_OK : hip_fail(e, "vs_state_fold: launch");
 }
 
 // =================================================================================================================

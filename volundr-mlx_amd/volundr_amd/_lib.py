@@ -42,13 +42,14 @@ ROW_DTYPE = np.dtype([
 ])
 assert ROW_DTYPE.itemsize == 96
 
-# vs_row_state, 32 bytes: the per-request sampler state of vs_sample_batch_state
+# vs_row_state, 48 bytes: the per-request sampler state of vs_sample_batch_state
 STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4"), ("hist_cap", "<i4"),
-                        ("produced", "<i4"), ("min_new_tokens", "<i4")])
-assert STATE_DTYPE.itemsize == 32
+                        ("produced", "<i4"), ("min_new_tokens", "<i4"), ("tab_off", "<i8"), ("tab_len", "<i4"),
+                        ("hist_base", "<i4")])
+assert STATE_DTYPE.itemsize == 48
 
-ABI_VERSION = 8
-EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_sample_workspace_bytes", "vs_verify_greedy",
+ABI_VERSION = 9
+EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_state_fold", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_lmhead_sample",
            "vs_lmhead_sample_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
@@ -76,7 +77,10 @@ def load():
     L.vs_sample_batch_noalloc.restype = i32
     L.vs_sample_noalloc_scratch_bytes.argtypes = []
     L.vs_sample_noalloc_scratch_bytes.restype = sz
-    L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    L.vs_sample_batch_state.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz,
+                                        vp]
+    L.vs_state_fold.argtypes = [vp, vp, vp, i64, vp, i32, vp]
+    L.vs_state_fold.restype = i32
     L.vs_sample_batch_state.restype = i32
     L.vs_lmhead_verify_greedy.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, sz,
                                           vp]

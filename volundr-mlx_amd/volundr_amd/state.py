@@ -41,6 +41,8 @@ from .ops import (_DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, 
 from .sampler import TokenHistory
 
 _NO_ACTION = ("none", None)
+FOLD_AT = 256     # unmerged history tokens at which a slot's (id, count) table takes them in
+FOLD_CHECK = 128  # steps between checks
 
 
 @dataclass
@@ -96,6 +98,8 @@ class DeviceSamplers:
         self._act: list = [None] * self.S  # the budget action each slot's uploaded row encodes
         self._edits: list = [None] * self.S  # per slot: (bias ids, bias vals, mask ids, n_supp) as uploaded
         self._hmax = np.zeros(self.S, dtype=np.int64)  # upper bound of each slot's device history length
+        self._rawbase = np.zeros(self.S, dtype=np.int64)  # _hmax when the slot's table last took its history
+        self._since_fold = 0  # steps since the tables were last checked
         self._budget = set()  # live slots whose request has a reasoning budget
         self._prod = [0] * self.S  # produced, as of the last synchronous step (budget rows need it)
         self.params_h = np.zeros(self.S, dtype=ROW_DTYPE)
@@ -115,17 +119,21 @@ class DeviceSamplers:
         self.params = torch.zeros(S * ROW_DTYPE.itemsize, dtype=torch.uint8, device=dev)
         self.state = torch.zeros(S * STATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)
         self.pool = torch.zeros(S * self.cap, dtype=torch.int32, device=dev)
+        # (id, count) tables: per slot a region of 4 * cap int32, two halves of `cap` pairs (vs_state_fold writes
+        # the merged table to the half not in use)
+        self.tabs = torch.zeros(S * 4 * self.cap, dtype=torch.int32, device=dev)
         self.bias_ids = torch.zeros(S * self.EB, dtype=torch.int32, device=dev)
         self.bias_vals = torch.zeros(S * self.EB, dtype=torch.float32, device=dev)
         self.mask_ids = torch.zeros(S * self.EM, dtype=torch.int32, device=dev)
 
     def _grow_slots(self, S2: int):
         """More slots: every table is re-allocated and the live slots' rows copied on the device."""
-        old = (self.params, self.state, self.pool, self.bias_ids, self.bias_vals, self.mask_ids)
+        old = (self.params, self.state, self.pool, self.tabs, self.bias_ids, self.bias_vals, self.mask_ids)
         S1 = self.S
         self.S = S2
         self._alloc_tables()
-        for new, o in zip((self.params, self.state, self.pool, self.bias_ids, self.bias_vals, self.mask_ids), old):
+        for new, o in zip((self.params, self.state, self.pool, self.tabs, self.bias_ids, self.bias_vals,
+                           self.mask_ids), old):
             new[:o.numel()].copy_(o)
         ph = np.zeros(S2, dtype=ROW_DTYPE)
         ph[:S1] = self.params_h
@@ -133,20 +141,27 @@ class DeviceSamplers:
         for lst, fill in ((self.slot_sampler, None), (self._act, None), (self._edits, None), (self._prod, 0)):
             lst.extend([fill] * (S2 - S1))
         self._hmax = np.concatenate([self._hmax, np.zeros(S2 - S1, dtype=np.int64)])
+        self._rawbase = np.concatenate([self._rawbase, np.zeros(S2 - S1, dtype=np.int64)])
 
     def _grow_history(self, need: int):
-        """Per-slot history capacity >= need: a new pool, each slot's history copied on the device, and every
-        slot's hist_off / hist_cap rewritten in place (stream-ordered before the next step)."""
+        """Per-slot history capacity >= need: a new pool and table pool, each slot's history and tables copied on the
+        device, and every slot's hist_off / hist_cap / tab_off rewritten in place (stream-ordered before the next
+        step)."""
         cap2 = self.cap
         while cap2 < need:
             cap2 *= 2
         S, cap1 = self.S, self.cap
         pool2 = torch.zeros(S * cap2, dtype=torch.int32, device=self.dev)
         pool2.view(S, cap2)[:, :cap1].copy_(self.pool.view(S, cap1))
-        self.pool, self.cap = pool2, cap2
-        st64 = self.state.view(torch.int64).view(S, 4)
-        st64[:, 1].copy_(torch.arange(S, dtype=torch.int64, device=self.dev) * cap2)
-        self.state.view(torch.int32).view(S, 8)[:, 5].fill_(cap2)
+        tabs2 = torch.zeros(S * 4 * cap2, dtype=torch.int32, device=self.dev)
+        tabs2.view(S, 2, 2 * cap2)[:, :, :2 * cap1].copy_(self.tabs.view(S, 2, 2 * cap1))
+        self.pool, self.tabs, self.cap = pool2, tabs2, cap2
+        st64 = self.state.view(torch.int64).view(S, 6)
+        q = torch.arange(S, dtype=torch.int64, device=self.dev)
+        half = (st64[:, 4] % (4 * cap1)) // (2 * cap1)
+        st64[:, 1].copy_(q * cap2)
+        st64[:, 4].copy_(q * 4 * cap2 + half * 2 * cap2)
+        self.state.view(torch.int32).view(S, 12)[:, 5].fill_(cap2)
 
     def _grow_edits(self, nb: int, nm: int):
         EB2, EM2 = self.EB, self.EM
@@ -227,10 +242,18 @@ class DeviceSamplers:
         st[0]["hist_cap"] = self.cap
         st[0]["produced"] = int(sampler.produced)
         st[0]["min_new_tokens"] = int(sampler.sp.min_new_tokens)
+        # the penalty counts of the history so far as a sorted (id, count) table (the content of Sampler.counts)
+        ids, cnt = np.unique(h, return_counts=True) if h.size else (np.zeros(0, np.int64), np.zeros(0, np.int64))
+        st[0]["tab_off"] = q * 4 * self.cap
+        st[0]["tab_len"] = ids.size
+        st[0]["hist_base"] = h.size
         sb = STATE_DTYPE.itemsize
         _dev_copy(self.state[q * sb:(q + 1) * sb], st)
         _dev_copy(self.pool[q * self.cap:q * self.cap + h.size], h.astype(np.int32))
+        t0 = q * 4 * self.cap
+        _dev_copy(self.tabs[t0:t0 + 2 * ids.size], np.stack([ids, cnt], axis=1).astype(np.int32).reshape(-1))
         self._flush()
+        self._rawbase[q] = h.size
         self._hmax[q] = h.size
         self._prod[q] = int(sampler.produced)
         self._edits[q] = None
@@ -283,7 +306,10 @@ class DeviceSamplers:
                     raise ValueError("a request can take only one row of a step")
                 if len(self._keys) >= 256:
                     self._keys.clear()
-                ent = (np.asarray(key, dtype=np.int64), torch.tensor(key, dtype=torch.int32).to(self.dev),
+                # slots 0..n-1 in order need no slots array (the kernel then skips a dependent load)
+                ident = key == tuple(range(len(key)))
+                ent = (np.asarray(key, dtype=np.int64),
+                       None if ident else torch.tensor(key, dtype=torch.int32).to(self.dev),
                        [(i, q) for i, q in enumerate(key) if q in self._budget])
                 self._keys[key] = ent
             self._slots_key, self._key_base = key, int(self._hmax[ent[0]].max())
@@ -298,15 +324,38 @@ class DeviceSamplers:
         need = self._key_base + self._key_steps + 1
         if need > self.cap and self.grow_history:
             self._grow_history(need + 64)
+        self._since_fold += 1
+        if self._since_fold >= FOLD_CHECK:
+            self._fold_due()
         return ent[1]
 
-    def _launch(self, logits: torch.Tensor, slots_t: torch.Tensor, out: SampleOut):
+    def _fold_due(self):
+        """Merge the recent history of every slot with FOLD_AT or more tokens since its last merge into its (id, count)
+        table (vs_state_fold, one launch). Checked every FOLD_CHECK steps, so a slot never holds more than
+        FOLD_AT + FOLD_CHECK < 512 unmerged tokens."""
+        key = self._slots_key
+        self._flush()
+        self._since_fold = 0
+        due = [q for q in self.order if self._hmax[q] - self._rawbase[q] >= FOLD_AT]
+        if due:
+            st = torch.tensor(due, dtype=torch.int32).to(self.dev)
+            L = _lib.load()
+            check(L.vs_state_fold(self.state.data_ptr(), self.pool.data_ptr(), self.tabs.data_ptr(), self.cap,
+                                  st.data_ptr(), len(due), _stream_handle(self.dev)), "vs_state_fold")
+            for q in due:
+                self._rawbase[q] = self._hmax[q]
+            self._fold_keep = st  # alive until the launch has read it (the next fold replaces it)
+        if key is not None:  # resume the current slot set's bookkeeping
+            self._slots_key, self._key_base, self._key_steps = key, int(self._hmax[self._keys[key][0]].max()), 0
+
+    def _launch(self, logits: torch.Tensor, slots_t: Optional[torch.Tensor], out: SampleOut):
         n = logits.shape[0]
         L = _lib.load()
         ws = workspace(self.dev, L.vs_sample_workspace_bytes(n, self.V))
         rc = L.vs_sample_batch_state(logits.data_ptr(), _DTYPES[logits.dtype], n, self.V, logits.stride(0),
                                      self.params.data_ptr(), self.state.data_ptr(), self.pool.data_ptr(),
-                                     slots_t.data_ptr(), self.bias_ids.data_ptr(), self.bias_vals.data_ptr(),
+                                     self.tabs.data_ptr(), 0 if slots_t is None else slots_t.data_ptr(),
+                                     self.bias_ids.data_ptr(), self.bias_vals.data_ptr(),
                                      self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
                                      out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(),
                                      _stream_handle(self.dev))
@@ -402,10 +451,12 @@ class DeviceSamplers:
         ws = workspace(self.dev, _lib.load().vs_sample_workspace_bytes(n, self.V))
         slots = [x.data_ptr() for x in logits_slots]
         rest = (_DTYPES[logits_slots[0].dtype], n, self.V, logits_slots[0].stride(0), self.params.data_ptr(),
-                self.state.data_ptr(), self.pool.data_ptr(), slots_t.data_ptr(), self.bias_ids.data_ptr(),
+                self.state.data_ptr(), self.pool.data_ptr(), self.tabs.data_ptr(),
+                0 if slots_t is None else slots_t.data_ptr(), self.bias_ids.data_ptr(),
                 self.bias_vals.data_ptr(), self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
                 out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
-        keep = (list(logits_slots), slots_t, ws, self.params, self.state, self.pool, self.bias_ids, self.mask_ids)
+        keep = (list(logits_slots), slots_t, ws, self.params, self.state, self.pool, self.tabs, self.bias_ids,
+                self.mask_ids)
 
         def call(i: int = 0) -> SampleOut:
             rc = fn(slots[i], *rest)
