@@ -107,3 +107,28 @@ def test_device_state_bind_matches_step(dev):
         assert torch.equal(ia, ib)
     assert np.array_equal(a.host_state(), b.host_state())
     assert a.history(0) == b.history(0)
+
+
+def test_bound_calls_grow_and_fold_like_step(dev):
+    """600 bound calls from a pool of 16 tokens: the history grows and the tables take in the recent tokens on the
+    same schedule as step(); a step() between bound calls keeps the bookkeeping. Tokens, slot states, tables and
+    histories equal those of step() throughout."""
+    V = 3000
+    rng = np.random.default_rng(19)
+    sps = [Sampling(top_k=20, seed=23, repetition_penalty=1.3, frequency_penalty=0.1),
+           Sampling(top_p=0.9, seed=24, presence_penalty=0.5)]
+    a = DeviceSamplers([Sampler(sp, vocab_valid=V) for sp in sps], V, hist_cap=16, device=dev)
+    b = DeviceSamplers([Sampler(sp, vocab_valid=V) for sp in sps], V, hist_cap=16, device=dev)
+    xs = [torch.from_numpy(rng.standard_normal((2, V)).astype(np.float32) * 2).to(dev) for _ in range(4)]
+    call = b.bind(xs)
+    print("[state] 600 bound calls", flush=True)
+    for k in range(600):
+        x = xs[k % 4]
+        ia = a.step(x, sync=False).ids.clone()
+        ib = (b.step(x, sync=False) if k == 300 else call(k % 4)).ids.clone()
+        assert torch.equal(ia, ib), f"call {k}"
+    assert np.array_equal(a.host_state(), b.host_state())
+    st = b.host_state()
+    assert all(int(st[q]["hist_base"]) >= 256 for q in range(2))  # folded under the bound calls
+    assert torch.equal(a.tabs, b.tabs) and b.cap > 600
+    assert a.history(0) == b.history(0) and len(b.history(1)) == 600

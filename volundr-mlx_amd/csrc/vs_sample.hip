@@ -1269,10 +1269,23 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
     }
     __syncthreads();
-  } else if (has_pen && A.state && (tlen == 0 || tab_all) && hw.nv <= (int64_t)HD * SNT * HB) {
-    // A state row whose table is in registers and whose recent tokens are all prefetched: the recent tokens are
-    // counted, then each table entry edits its logit with its total count and clears the recent count of its id,
-    // then the first visit of each id left among the recent tokens claims its count and edits (sampler.py:113-122).
+  } else if (has_pen && A.state && hw.nv <= (int64_t)HD * SNT * HB) {
+    // A state row whose recent tokens are all prefetched: the recent tokens are counted, then each table entry of
+    // the chunk edits its logit with its total count and clears the recent count of its id, then the first visit of
+    // each id left among the recent tokens claims its count and edits (sampler.py:113-122). A table longer than
+    // PAIRS_ALL is bracketed by the probes and its first entries loaded before the counting.
+    constexpr int PU = 4;  // bracket entries per lane in flight
+    int64_t p0 = 0, p1 = 0;
+    int2 e[PU];
+    const int2* tp = (const int2*)(A.tabs + st.tab_off);
+    if (!tab_all && tlen > 0) {
+      pair_range(tlen, probe, lo, hi, s.redi, &p0, &p1);
+#pragma unroll
+      for (int u = 0; u < PU; ++u) {
+        const int64_t q = p0 + t + (int64_t)u * SNT;
+        e[u] = tp[q < p1 ? q : 0];
+      }
+    }
     hist_count(A.hist, hw, hpre, lo, hi, s.cnt);
     __syncthreads();
     auto edit = [&](int i, uint32_t c) {
@@ -1292,6 +1305,24 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           edit(i, (uint32_t)tabe[u].y + s.cnt[i]);
           s.cnt[i] = 0;
         }
+      __syncthreads();
+    } else if (p1 > p0) {
+      for (int64_t p = p0 + t; p < p1; p += (int64_t)PU * SNT) {
+        if (p != p0 + t) {
+#pragma unroll
+          for (int u = 0; u < PU; ++u) {
+            const int64_t q = p + (int64_t)u * SNT;
+            e[u] = tp[q < p1 ? q : p];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < PU; ++u)  // the bracket's entries outside [lo, hi) are skipped
+          if (p + (int64_t)u * SNT < p1 && (unsigned)(e[u].x - lo) < (unsigned)(hi - lo)) {
+            const int i = e[u].x - lo;
+            edit(i, (uint32_t)e[u].y + s.cnt[i]);
+            s.cnt[i] = 0;
+          }
+      }
       __syncthreads();
     }
     hist_visit_prefetched(A.hist, hw, hpre, [&](int id) {

@@ -436,33 +436,47 @@ class DeviceSamplers:
 
     def bind(self, logits_slots: Sequence[torch.Tensor]):
         """A callable f(i) running step(logits_slots[i], sync=False) for the current `order`, with every argument
-        bound once (serving loops that reuse the same buffers and membership): one C call, no host checks. Not for
-        requests with a reasoning budget, and the pool does not grow under it: size hist_cap for the calls made."""
+        bound once (serving loops that reuse the same buffers and membership): one C call per step, and the host
+        bookkeeping of step() (the history pool grows, the tables take in their recent tokens every FOLD_CHECK
+        calls) done on a few integers. Not for requests with a reasoning budget."""
         n = len(self.order)
         for x in logits_slots:
             self._check_logits(x, n)
         if any(getattr(self.slot_sampler[q], "budget", None) is not None for q in self.order):
             raise ValueError("bind() does not serve requests with a reasoning budget; use step()")
-        slots_t = self._prepare(self.order, sync=False)
+        order = list(self.order)
         if self.out.ids.shape[0] != n:
             self.out = alloc_out(n, self.dev)
         fn = _lib.load().vs_sample_batch_state
         out = self.out
         ws = workspace(self.dev, _lib.load().vs_sample_workspace_bytes(n, self.V))
         slots = [x.data_ptr() for x in logits_slots]
-        rest = (_DTYPES[logits_slots[0].dtype], n, self.V, logits_slots[0].stride(0), self.params.data_ptr(),
-                self.state.data_ptr(), self.pool.data_ptr(), self.tabs.data_ptr(),
-                0 if slots_t is None else slots_t.data_ptr(), self.bias_ids.data_ptr(),
-                self.bias_vals.data_ptr(), self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
-                out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
-        keep = (list(logits_slots), slots_t, ws, self.params, self.state, self.pool, self.tabs, self.bias_ids,
-                self.mask_ids)
+        b = {"key": object()}  # no slot set yet: the first call binds
+
+        def rebind():
+            # the arguments of the launch; the pool and the tables move when the history grows
+            slots_t = self._prepare(order, sync=False)
+            b["key"] = self._slots_key
+            b["rest"] = (_DTYPES[logits_slots[0].dtype], n, self.V, logits_slots[0].stride(0), self.params.data_ptr(),
+                         self.state.data_ptr(), self.pool.data_ptr(), self.tabs.data_ptr(),
+                         0 if slots_t is None else slots_t.data_ptr(), self.bias_ids.data_ptr(),
+                         self.bias_vals.data_ptr(), self.mask_ids.data_ptr(), out.ids.data_ptr(),
+                         out.logprobs.data_ptr(), out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(),
+                         _stream_handle(self.dev))
+            b["keep"] = (list(logits_slots), slots_t, ws, self.params, self.state, self.pool, self.tabs,
+                         self.bias_ids, self.mask_ids)
 
         def call(i: int = 0) -> SampleOut:
-            rc = fn(slots[i], *rest)
+            if (self._slots_key is b["key"] and self._since_fold + 1 < FOLD_CHECK
+                    and self._key_base + self._key_steps + 1 <= self.cap):
+                self._since_fold += 1  # what _prepare would do for this slot set on this step
+            else:
+                rebind()
+            rc = fn(slots[i], *b["rest"])
             if rc:
                 check(rc, "vs_sample_batch_state")
-            return keep and out
+            self._key_steps += 1
+            return out
 
         return call
 
