@@ -329,9 +329,8 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
         pool = _pool_for(logits.device, logits.shape[-1])
         slots = [e[1] if (e := s._vs) is not None and e[0] is pool and e[2] else _slot_in(pool, s) for s in samplers]
         res = pool.step(sub, slots)
-        lps, fl = res.logprobs, res.flags
-        for i, s in enumerate(samplers):
+        for s, lp, f in zip(samplers, res.logprobs, res.flags):
             s._ahead = True
-            if not fl[i] & OUT_FORCED:
-                s.last_logprob = lps[i]
+            if not f & OUT_FORCED:
+                s.last_logprob = lp
     return res.ids

@@ -108,7 +108,9 @@ class DeviceSamplers:
         self._key_steps = 0     # ... the steps taken with them since _hmax was last brought up to date
         self._key_base = 0      # ... and their largest _hmax at that time
         self._keys: dict = {}   # slots tuple -> (index array, device int32 tensor, budget rows)
-        self._host_out: dict = {}  # n -> SampleOut in pinned host memory that synchronous steps write into
+        self._host_out: dict = {}  # n -> (SampleOut in pinned host memory that synchronous steps write into, its
+        #                            [4, n] int32 NumPy view, the flags as uint32, the logprobs as float32)
+        self._argc: dict = {}  # the launch arguments of recent steps (keyed by every pointer they hold)
         self.out = alloc_out(max(len(samplers), 1), dev)
         for s in samplers:
             self.admit(s)
@@ -352,14 +354,23 @@ class DeviceSamplers:
         n = logits.shape[0]
         L = _lib.load()
         ws = workspace(self.dev, L.vs_sample_workspace_bytes(n, self.V))
-        rc = L.vs_sample_batch_state(logits.data_ptr(), _DTYPES[logits.dtype], n, self.V, logits.stride(0),
-                                     self.params.data_ptr(), self.state.data_ptr(), self.pool.data_ptr(),
-                                     self.tabs.data_ptr(), 0 if slots_t is None else slots_t.data_ptr(),
-                                     self.bias_ids.data_ptr(), self.bias_vals.data_ptr(),
-                                     self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(),
-                                     out.flags.data_ptr(), out.keep.data_ptr(), ws.data_ptr(), ws.numel(),
-                                     _stream_handle(self.dev))
-        check(rc, "vs_sample_batch_state")
+        key = (logits.data_ptr(), logits.dtype, n, logits.stride(0), 0 if slots_t is None else slots_t.data_ptr(),
+               out.ids.data_ptr(), ws.data_ptr(), self.pool.data_ptr(), self.params.data_ptr())
+        a = self._argc.get(key)
+        if a is None:
+            if len(self._argc) >= 64:
+                self._argc.clear()
+            # every pointer of the call is in the key, the tables' own through params and pool (they are
+            # re-allocated together), the stream through the workspace (one per stream)
+            a = self._argc[key] = (
+                logits.data_ptr(), _DTYPES[logits.dtype], n, self.V, logits.stride(0), self.params.data_ptr(),
+                self.state.data_ptr(), self.pool.data_ptr(), self.tabs.data_ptr(),
+                0 if slots_t is None else slots_t.data_ptr(), self.bias_ids.data_ptr(), self.bias_vals.data_ptr(),
+                self.mask_ids.data_ptr(), out.ids.data_ptr(), out.logprobs.data_ptr(), out.flags.data_ptr(),
+                out.keep.data_ptr(), ws.data_ptr(), ws.numel(), _stream_handle(self.dev))
+        rc = L.vs_sample_batch_state(*a)
+        if rc:
+            check(rc, "vs_sample_batch_state")
 
     def _check_logits(self, logits: torch.Tensor, n: int):
         _require_cuda(logits, "logits")
@@ -379,11 +390,15 @@ class DeviceSamplers:
             raise ValueError("no live requests to step")
         self._check_logits(logits, n)
         slots_t = self._prepare(slots, sync)
+        hv = None
         if out is None:
             if sync:  # results land in pinned host memory: no copy, only the stream's completion is awaited
-                out = self._host_out.get(n)
-                if out is None:
-                    out = self._host_out[n] = _alloc_out_host(n, self.dev)
+                hv = self._host_out.get(n)
+                if hv is None:
+                    o = _alloc_out_host(n, self.dev)
+                    h = o.block.numpy()
+                    hv = self._host_out[n] = (o, h, h[2].view(np.uint32), h[1].view(np.float32))
+                out = hv[0]
             else:
                 if self.out.ids.shape[0] != n:
                     self.out = alloc_out(n, self.dev)
@@ -392,27 +407,36 @@ class DeviceSamplers:
         self._key_steps += 1
         if not sync:
             return out
-        if out.block.is_cuda:
-            hb = torch.empty((4, n), dtype=torch.int32)
-            hb.copy_(out.block)
-        else:
-            hb = out.block
-            if self.dev.type == "cuda":
-                torch.cuda.current_stream(self.dev).synchronize()
-        host = hb.numpy()
-        fl = host[2].view(np.uint32)
-        anyf = int(np.bitwise_or.reduce(fl))
+        if hv is None:  # the caller's buffers
+            if out.block.is_cuda:
+                hb = torch.empty((4, n), dtype=torch.int32)
+                hb.copy_(out.block)
+            else:
+                hb = out.block
+                if self.dev.type == "cuda":
+                    torch.cuda.current_stream(self.dev).synchronize()
+            h = hb.numpy()
+            hv = (out, h, h[2].view(np.uint32), h[1].view(np.float32))
+        elif self.dev.type == "cuda":
+            torch.cuda.current_stream(self.dev).synchronize()
+        host, flv = hv[1], hv[2]
+        fl = flv.tolist()
+        anyf = 0
+        for f in fl:
+            anyf |= f
         if anyf & OUT_TIMEOUT:
-            self._retry(logits, list(slots), np.nonzero(fl & OUT_TIMEOUT)[0], out)
-            fl = host[2].view(np.uint32)
-            anyf = int(np.bitwise_or.reduce(fl))
+            self._retry(logits, list(slots), np.nonzero(flv & OUT_TIMEOUT)[0], out)
+            fl = flv.tolist()
+            anyf = 0
+            for f in fl:
+                anyf |= f
         if anyf & OUT_HIST_FULL and self.grow_history:
             raise VsError("vs_sample_batch_state: a history slot was full (the pool should have grown)")
         ids = host[0].tolist()
         for i, q in self._keys[self._slots_key][2]:
             self.slot_sampler[q].budget.accept(self._prod[q], ids[i])
             self._prod[q] += 1
-        return StepResult(ids, host[1].view(np.float32).tolist(), fl.tolist(), host[3].tolist(), out)
+        return StepResult(ids, hv[3].tolist(), fl, host[3].tolist(), out)
 
     def _retry(self, logits, slots, bad, out):
         """Repeat the rows that reported VS_OUT_TIMEOUT (they committed nothing) under a cooperative launch; their
