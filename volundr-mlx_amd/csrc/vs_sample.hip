@@ -3299,29 +3299,32 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
   __shared__ int misc[NMISC];
   __shared__ u64 bound;
   __shared__ int qlist[LS_KMAX + 1];  // the qualifying lists, then their number
-  const int pos = blockIdx.x, t = threadIdx.x, ln = lane_id();
+  __shared__ float exf[SNW];
+  __shared__ int exn[SNW], exz[SNW];
+  __shared__ uint32_t hist1[256], hist2[256];  // list heads by the first / second byte of their value
+  __shared__ int rsel[4];
+  __shared__ int redi[NRED];
+  const int pos = blockIdx.x, t = threadIdx.x, w = t / WAVE, ln = lane_id();
   VS_TR_DECL(A);
   VS_TR(A, 0);
-  // Every load of the row at once, before its class is known: the parameters, the workgroups' partials (one per
-  // thread) and the list heads (wave 0, HPL per lane; unused unless the row is a top-k row).
+  // Every load of the row at once, before its class is known: the parameters and, one per thread, the workgroups'
+  // partials and list heads (the heads are used only by a top-k row).
   const vs_row_params P = A.params[pos];
   const LSParts q = ls_parts(A.ws, A.R);
   const size_t base = (size_t)pos * LS_PMAX;
   static_assert(LS_PMAX <= SNT, "one partial per thread");
-  constexpr int HPL = LS_PMAX / WAVE;
   const bool in = t < A.P;
-  u64 hv[HPL];
-  if (t < WAVE) {
-#pragma unroll
-    for (int u = 0; u < HPL; ++u) {
-      const int g = ln + WAVE * u;
-      hv[u] = q.heads[base + (g < A.P ? g : 0)];
-    }
+  const int ti = in ? t : 0;
+  u64 hd = q.heads[base + ti];
+  const u64 k0 = q.amkey[base + ti];
+  const float m0 = q.mf[base + ti];
+  const double s0 = q.se[base + ti];
+  const uint32_t n0 = q.nfin[base + ti];
+  hd = in ? hd : (u64)0;
+  if (t < 256) {
+    hist1[t] = 0;
+    hist2[t] = 0;
   }
-  const u64 k0 = q.amkey[base + (in ? t : 0)];
-  const float m0 = q.mf[base + (in ? t : 0)];
-  const double s0 = q.se[base + (in ? t : 0)];
-  const uint32_t n0 = q.nfin[base + (in ? t : 0)];
   int vlim;
   const int cls = ls_class(P, A.N, &vlim);
   auto out = [&](int32_t tok, float lp, uint32_t fl, int32_t keep) {
@@ -3338,19 +3341,35 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
     out(-1, 0.0f, VS_OUT_UNSUPPORTED, 0);
     return;
   }
-  if (t < WAVE) {
-#pragma unroll
-    for (int u = 0; u < HPL; ++u) hv[u] = ln + WAVE * u < A.P ? hv[u] : (u64)0;
+  // one exchange for the row's argmax key, maximum, finite count and non-empty lists
+  {
+    const u64 wa = wave_max(in ? k0 : (u64)0);
+    const float wm = wave_max(in ? m0 : -__builtin_inff());
+    const int wn = wave_sum(in ? (int)n0 : 0);
+    const int wz = (int)__popcll(__ballot(hd != 0));
+    if (ln == 0) {
+      red64[w] = wa;
+      exf[w] = wm;
+      exn[w] = wn;
+      exz[w] = wz;
+    }
   }
-  const u64 am = block_max<SNT>(in ? k0 : (u64)0, red64);
-  const float M = block_max<SNT>(in ? m0 : -__builtin_inff(), (float*)redf);
-  const int n = block_sum<SNT>(in ? (int)n0 : 0, misc);
-  const float L2E = 1.44269504088896340736f;
-  const double S = block_sum<SNT>((in && s0 > 0.0 && is_finite(M)) ? s0 * (double)__builtin_amdgcn_exp2f((m0 - M) * L2E)
-                                                                   : 0.0,
-                                  redf);
+  __syncthreads();
+  u64 am = 0;
+  float M = -__builtin_inff();
+  int n = 0, nzh = 0;
+#pragma unroll
+  for (int i = 0; i < SNW; ++i) {
+    am = red64[i] > am ? red64[i] : am;
+    M = exf[i] > M ? exf[i] : M;
+    n += exn[i];
+    nzh += exz[i];
+  }
   VS_TR(A, 1);
   if (cls == LS_GREEDY) {  // sampler.py:127-128 (or :95-96 over [0, vv)): first maximum, log-softmax there
+    const float L2E = 1.44269504088896340736f;
+    const double S = block_sum<SNT>(
+        (in && s0 > 0.0 && is_finite(M)) ? s0 * (double)__builtin_amdgcn_exp2f((m0 - M) * L2E) : 0.0, redf);
     const float xj = am_is_nan(am) ? __builtin_nanf("") : key_value(am);
     out((int32_t)key_index(am),
         (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f,
@@ -3363,51 +3382,73 @@ __global__ __launch_bounds__(SNT) void vs_lmhead_sample_merge_kernel(LSMArgs A) 
   }
   const int keff = cls < n ? cls : n;  // sampler.py:133-134
   // The bound T: the keff-th largest list head (heads are keys of the row, so its keff-th largest key reaches it),
-  // to its 16-bit value prefix; exact only when more than LS_KMAX heads share that prefix. Only the lists whose heads
-  // reach T can hold keys >= T (<= LS_KMAX lists of LS_KMAX keys); their indices go to LDS.
-  if (t < WAVE) {
-    auto count_ge = [&](u64 c) -> int {
-      int m = 0;
+  // to its 16-bit value prefix, found by a two-round radix select over the heads (one byte per round, every thread
+  // holding one head); exact only when more than LS_KMAX heads share that prefix. Only the lists whose heads reach T
+  // can hold keys >= T (<= LS_KMAX lists of LS_KMAX keys); their indices go to LDS.
+  // Wave 0: the bin of a 256-bin histogram (bins visited from the top) where the count from the top first reaches
+  // `need`, and the count above it.
+  auto find_desc = [&](const uint32_t* h, int need) {
+    if (t < WAVE) {
+      uint32_t c[4];
+      int tot = 0;
 #pragma unroll
-      for (int u = 0; u < HPL; ++u) m += (int)__popcll(__ballot(hv[u] >= c));
-      return m;
-    };
-    u64 T = 1;
-    if (count_ge(1) >= keff) {
-      // the value prefix on the heads' high words (32-bit compares)
-      uint32_t hh[HPL];
-#pragma unroll
-      for (int u = 0; u < HPL; ++u) hh[u] = (uint32_t)(hv[u] >> 32);
-      uint32_t H = 0;
-      for (int b = 15; b >= 0; --b) {
-        const uint32_t c = H | (1u << b);
-        int cnt = 0;
-#pragma unroll
-        for (int u = 0; u < HPL; ++u) cnt += (int)__popcll(__ballot(hh[u] >= (c << 16)));
-        H = cnt >= keff ? c : H;
+      for (int j = 0; j < 4; ++j) {
+        c[j] = h[255 - 4 * ln - j];
+        tot += (int)c[j];
       }
-      T = (u64)H << 48;
-      if (count_ge(T) > LS_KMAX) {
-        for (int b = 47; b >= 0; --b) {
-          const u64 c = T | ((u64)1 << b);
-          T = count_ge(c) >= keff ? c : T;
+      const int incl = wave_scan(tot);
+      int run = incl - tot, hit = -1, before = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (hit < 0 && run + (int)c[j] >= need) {
+          hit = j;
+          before = run;
         }
+        run += (int)c[j];
+      }
+      const unsigned long long hb = __ballot(hit >= 0);
+      const int L = hb ? __ffsll((long long)hb) - 1 : WAVE - 1;
+      if (ln == L) {
+        const int bin = hit >= 0 ? 255 - 4 * ln - hit : 0;
+        rsel[0] = bin;
+        rsel[1] = hit >= 0 ? before : 0;
+        rsel[2] = (int)h[bin];
       }
     }
-    int nq = 0;
-#pragma unroll
-    for (int u = 0; u < HPL; ++u) {
-      const bool qual = hv[u] >= T;
-      const unsigned long long mb = __ballot(qual);
-      const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mb, 0u));
-      if (qual && nq + below < LS_KMAX) qlist[nq + below] = ln + WAVE * u;
-      nq += (int)__popcll(mb);
+  };
+  u64 T = 1;
+  if (nzh >= keff) {
+    if (hd) atomicAdd(&hist1[hd >> 56], 1u);
+    __syncthreads();
+    find_desc(hist1, keff);
+    __syncthreads();
+    const int b1 = rsel[0], above1 = rsel[1];
+    if (hd && (int)(hd >> 56) == b1) atomicAdd(&hist2[(hd >> 48) & 0xFF], 1u);
+    __syncthreads();
+    find_desc(hist2, keff - above1);
+    __syncthreads();
+    const int b2 = rsel[0];
+    T = ((u64)b1 << 56) | ((u64)b2 << 48);
+    if (above1 + rsel[1] + rsel[2] > LS_KMAX) {
+      // more than LS_KMAX heads share the prefix: the exact keff-th head, bit by bit below it (rare: long runs of
+      // equal logits)
+      for (int b = 47; b >= 0; --b) {
+        const u64 c = T | ((u64)1 << b);
+        T = block_sum<SNT>(hd >= c ? 1 : 0, redi) >= keff ? c : T;
+      }
     }
-    if (t == 0) {
-      bound = T;
-      qlist[LS_KMAX] = nq < LS_KMAX ? nq : LS_KMAX;
-      misc[0] = 0;
-    }
+  }
+  if (t == 0) misc[1] = 0;
+  __syncthreads();
+  {
+    const int p = wave_append(hd != 0 && hd >= T, &misc[1]);
+    if (p >= 0 && p < LS_KMAX) qlist[p] = t;
+  }
+  __syncthreads();
+  if (t == 0) {
+    bound = T;
+    qlist[LS_KMAX] = misc[1] < LS_KMAX ? misc[1] : LS_KMAX;
+    misc[0] = 0;
   }
   __syncthreads();
   VS_TR(A, 2);
