@@ -169,7 +169,9 @@ int vs_sample_batch_state(const void* logits, int dtype, int B, int V, int64_t l
 /* Merge the history tokens recorded since each listed request's last merge (pool[hist_off + hist_base, hist_off +
  * hist_len), at most 512 of them) into its (id, count) table: the merged table is written to the other half of the
  * request's table region (a region of 4 * tab_cap int32 at a multiple of 4 * tab_cap; tab_cap >= the number of
- * distinct ids the request can hold), tab_off / tab_len / hist_base are updated. Stream-ordered with the sampling
+ * distinct ids the request can hold), tab_off / tab_len / hist_base are updated; a request whose table length plus
+ * the tokens to merge exceeds tab_cap is left unchanged (its tokens stay counted from the history, every later step
+ * exact). Stream-ordered with the sampling
  * calls that read the tables. No counterpart in the reference (Sampler.counts is a dict updated per token,
  * sampler.py:77-78). */
 int vs_state_fold(vs_row_state* state, const int32_t* pool, int32_t* tabs, int64_t tab_cap, const int32_t* slots, int n,

@@ -192,3 +192,38 @@ def test_long_run_folds_the_tables(dev):
         assert np.array_equal(tab[:, 0], ids) and np.array_equal(tab[:, 1], cnt), f"row {r}: table"
         assert ds.history(q) == hists[r]
     assert ds.cap > 256  # the pool (and the tables) grew past the first capacity
+
+
+def test_fold_leaves_a_slot_whose_table_cannot_fit(dev):
+    """vs_state_fold with a tab_cap below the slot's table plus its recent tokens changes nothing (the tokens stay
+    counted from the history), and the next steps still equal the oracle."""
+    from volundr_amd import _lib
+    from volundr_amd.ops import _stream_handle
+
+    Vs = 2000
+    rng = np.random.default_rng(41)
+    sp = Sampling(top_k=40, repetition_penalty=1.4, frequency_penalty=0.2, seed=81)
+    ds = DeviceSamplers([Sampler(sp, vocab_valid=Vs)], Vs, hist_cap=512, device=dev)
+    hist, ref = [], [S.seed_state(sp.seed)]
+
+    def step():
+        x = (rng.standard_normal((1, Vs)) * 1.5).astype(np.float32)
+        res = ds.step(torch.from_numpy(x).to(dev))
+        nxt, u = S.xorshift64s_next(ref[0])
+        want = S.sample(x[0], sp, u, S.counts_from_history(hist), len(hist))
+        _check(f"step {len(hist)}", res.ids[0], res.logprobs[0], want)
+        if want.kind == "sample":
+            ref[0] = nxt
+        hist.append(res.ids[0])
+
+    for _ in range(100):
+        step()
+    before = ds.host_state().copy()
+    assert int(before[0]["hist_len"]) - int(before[0]["hist_base"]) == 100
+    sl = torch.zeros(1, dtype=torch.int32, device=dev)
+    L = _lib.load()
+    _lib.check(L.vs_state_fold(ds.state.data_ptr(), ds.pool.data_ptr(), ds.tabs.data_ptr(), 50, sl.data_ptr(), 1,
+                               _stream_handle(dev)), "vs_state_fold")
+    assert np.array_equal(ds.host_state(), before)
+    for _ in range(20):
+        step()

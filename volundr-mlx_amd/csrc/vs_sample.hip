@@ -1795,7 +1795,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           const int idx = t + u * SNT;
           r8[u] = idx < tot ? ld_dev(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
         }
-#ifdef VS_TRACE
+#ifdef VS_TRACE_WAITS
         publish_wait();
         VS_TRX(50);
 #endif
@@ -1823,7 +1823,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             h2 = full ? h : h2;
           }
         }
-#ifdef VS_TRACE
+#ifdef VS_TRACE_WAITS
         publish_wait();
         VS_TRX(51);
 #endif
@@ -3708,6 +3708,9 @@ __global__ __launch_bounds__(SNT) void vs_state_fold_kernel(vs_row_state* state,
   const int nr = st.hist_len - st.hist_base;
   if (nr <= 0) return;
   const int n = nr < FOLD_MAX ? nr : FOLD_MAX;  // the host folds before FOLD_MAX tokens accumulate
+  // the merged table must fit half of the slot's region (tab_cap pairs); a slot laid out otherwise keeps its tokens
+  // counted from the history (every later step stays exact)
+  if ((int64_t)st.tab_len + n > tab_cap) return;
   for (int i = t; i < n; i += SNT) raw[i] = ((u64)(uint32_t)pool[st.hist_off + st.hist_base + i] << 32) | (u64)i;
   __syncthreads();
   // ascending by (id, position): the rank of each key (keys are unique)
