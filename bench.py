@@ -168,7 +168,7 @@ def bench_dropin(torch, dev, d, steps):
             ss.append(s)
         return ss
 
-    n = max(steps // 50, 10)
+    n = max(steps // 5, 50)
     ss = mk()
     for _ in range(3):
         sample_rows_for(x, ss)

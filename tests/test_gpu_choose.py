@@ -210,3 +210,21 @@ def test_host_state_follows_the_device_pool(dev):
     run(1, "after a drop")
     assert len(pool.order) == live - 1
     assert SM._pools  # the pool is kept for later calls
+
+
+def test_samplers_moving_between_pools(dev):
+    """The same Samplers served from logits of two widths (two device pools) in turn: each move re-admits the
+    request with its current state, and the batch's cached slots in the pool it left are not reused."""
+    rng = np.random.default_rng(123)
+    sps = [Sampling(top_k=30, repetition_penalty=1.3, seed=91), Sampling(top_p=0.9, frequency_penalty=0.3, seed=92)]
+    ss = [Sampler(sp, vocab_valid=VV) for sp in sps]
+    oracle = [OracleRequest(sp) for sp in sps]
+    for step, width in enumerate((V, V, V - 8, V, V - 8, V - 8, V)):
+        x = np.ascontiguousarray(_logits(rng, len(ss))[:, :width])
+        toks = sample_rows_for(torch.from_numpy(x).to(dev), ss)
+        for r in range(len(ss)):
+            res, nxt = oracle[r].step(x[r])
+            _check(f"step {step} width {width} row {r}", toks[r], ss[r].last_logprob, res)
+            oracle[r].accept(toks[r], res, nxt)
+    for r, s in enumerate(ss):
+        assert s.rng == oracle[r].rng and list(s.history) == oracle[r].gen and s.produced == 7

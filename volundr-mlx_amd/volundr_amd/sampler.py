@@ -179,6 +179,7 @@ class Sampler:
     def _host_changed(self):
         if self._vs is not None:
             self._vs[2] = False  # the pool re-takes the host state before its next step
+            self._vs[0]._epoch += 1  # and its cached slot lists are stale
 
     def _field(name):  # noqa: N805
         attr = "_" + name
@@ -278,9 +279,12 @@ def _pool_for(dev: torch.device, V: int):
     if p is None:
         p = DeviceSamplers([], V, hist_cap=4096, device=dev, capacity=64)
         p._released = []
+        p._epoch = 0  # bumped by every admission, release and host-side change of a Sampler it holds
+        p._slot_cache = {}  # ids of a batch's Samplers -> (epoch, their slots)
         _pools[key] = p
     while p._released:
         p.retire(p._released.pop(), write_back=False)
+        p._epoch += 1
     return p
 
 
@@ -294,9 +298,11 @@ def _slot_in(pool, s) -> int:
         s._pull()
         ent[3].detach()
         ent[0].retire(ent[1], write_back=False)
+        ent[0]._epoch += 1
         s._vs = None
     q = pool.admit(weakref.proxy(s))
     s._vs = [pool, q, True, weakref.finalize(s, _release, pool, q)]
+    pool._epoch += 1
     return q
 
 
@@ -327,7 +333,18 @@ def sample_rows_for(logits: torch.Tensor, samplers: Sequence[Sampler], rows: Opt
         sub = sub.contiguous()
     with _pool_lock:
         pool = _pool_for(logits.device, logits.shape[-1])
-        slots = [e[1] if (e := s._vs) is not None and e[0] is pool and e[2] else _slot_in(pool, s) for s in samplers]
+        # keyed by object ids, which hold no reference: an id is reused only after its Sampler died, and that
+        # death queued a release, which bumps the epoch before this lookup (_pool_for drains the releases)
+        key = tuple(map(id, samplers))
+        ent = pool._slot_cache.get(key)
+        if ent is not None and ent[0] == pool._epoch:
+            slots = ent[1]
+        else:
+            slots = [e[1] if (e := s._vs) is not None and e[0] is pool and e[2] else _slot_in(pool, s)
+                     for s in samplers]
+            if len(pool._slot_cache) >= 64:
+                pool._slot_cache.clear()
+            pool._slot_cache[key] = (pool._epoch, slots)
         res = pool.step(sub, slots)
         for s, lp, f in zip(samplers, res.logprobs, res.flags):
             s._ahead = True
