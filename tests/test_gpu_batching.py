@@ -227,3 +227,44 @@ def test_fold_leaves_a_slot_whose_table_cannot_fit(dev):
     assert np.array_equal(ds.host_state(), before)
     for _ in range(20):
         step()
+
+
+@pytest.mark.parametrize("n_hist", [0, 2047, 2048, 2049, 6000])
+def test_state_tables_around_the_prefetch_size(dev, n_hist):
+    """State rows whose (id, count) tables hold up to PAIRS_ALL = 2048 entries (loaded whole) and beyond (bracketed
+    by probes, the table entries and the recent tokens merged in one pass): 400 steps at V = 163840 (the first fold
+    comes at step 384: checks every 128 steps, 256 recent tokens due) against the oracle over the whole history."""
+    Vb = 163840
+    rng = np.random.default_rng(n_hist + 5)
+    sps = [Sampling(top_k=50, repetition_penalty=1.3, frequency_penalty=0.05, presence_penalty=0.3, seed=95),
+           Sampling(top_p=0.9, repetition_penalty=0.8, frequency_penalty=-0.1, seed=96),
+           Sampling(temperature=0.0, repetition_penalty=1.5, seed=97)]
+    ss = [Sampler(sp, vocab_valid=Vb) for sp in sps]
+    hists = []
+    for s in ss:
+        # n_hist distinct ids (some repeated) spread over the vocabulary: a table of about n_hist entries
+        ids = rng.choice(Vb, size=n_hist, replace=False) if n_hist else np.zeros(0, dtype=np.int64)
+        h = np.concatenate([ids, ids[: n_hist // 3]]).astype(np.int64)
+        rng.shuffle(h)
+        for t in h.tolist():
+            s.history.append(t)
+            s.counts[t] = s.counts.get(t, 0) + 1
+        hists.append(h.tolist())
+    pre = [len(h) for h in hists]
+    refs = [S.seed_state(sp.seed) for sp in sps]
+    ds = DeviceSamplers(ss, Vb, hist_cap=max(pre) + 512, device=dev)
+    print(f"[batching] tables of {n_hist} entries, 400 steps", flush=True)
+    for step in range(400):
+        x = (rng.standard_normal((3, Vb)) * 2.0).astype(np.float32)
+        if hists[0]:  # logits that the penalties decide: the history's ids near the top
+            x[:, hists[0][:64]] += 4.0
+        res = ds.step(torch.from_numpy(x).to(dev))
+        for r, sp in enumerate(sps):
+            nxt, u = S.xorshift64s_next(refs[r])
+            want = S.sample(x[r], sp, u, S.counts_from_history(hists[r]), len(hists[r]) - pre[r])
+            _check(f"tables {n_hist} step {step} row {r}", res.ids[r], res.logprobs[r], want)
+            if want.kind == "sample":
+                refs[r] = nxt
+            hists[r].append(res.ids[r])
+    st = ds.host_state()
+    assert all(int(st[q]["hist_base"]) > pre[r] for r, q in enumerate(ds.order))  # folded during the run
