@@ -271,8 +271,15 @@ int vs_set_spin_limit(unsigned polls);
  * VS_DEBUG_SPIN_LATER_BARRIERS: the spin limit of vs_set_spin_limit applies only from a row's second barrier on, so
  * that every workgroup passes the first and some give up at a later one while others pass it.
  * VS_DEBUG_WAIT_CLOCK: every row barrier is treated as unreachable, so each wait ends at its time bound (measures
- * the bound; every such row reports VS_OUT_TIMEOUT). No counterpart in the reference. */
-enum { VS_DEBUG_FORCE_RADIX = 1u, VS_DEBUG_SPIN_LATER_BARRIERS = 2u, VS_DEBUG_WAIT_CLOCK = 4u };
+ * the bound; every such row reports VS_OUT_TIMEOUT). VS_DEBUG_NO_XCD_EXCHANGE: the workgroups of a row exchange their
+ * data through the device-coherent level even when they all run on one XCD (the default then uses that XCD's L2;
+ * results are identical either way). No counterpart in the reference. */
+enum {
+  VS_DEBUG_FORCE_RADIX = 1u,
+  VS_DEBUG_SPIN_LATER_BARRIERS = 2u,
+  VS_DEBUG_WAIT_CLOCK = 4u,
+  VS_DEBUG_NO_XCD_EXCHANGE = 8u
+};
 int vs_set_debug(unsigned flags);
 
 /* on != 0: the calling thread's later sampling calls launch cooperatively (every workgroup of the grid resident at
@@ -293,13 +300,19 @@ int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stre
  * impossible value. No counterpart in the reference. */
 int vs_stream_read(const void* p, size_t bytes, int blocks, uint32_t* out, vs_stream_t stream);
 
+/* Write, for each of `blocks` workgroups of `threads` threads, the id of the XCD it runs on (out: device, >= blocks
+ * words): a placement check. The sampling kernel lets the workgroups of a row exchange data through their XCD's L2
+ * when the grid puts each row on one XCD, which holds when workgroups b and b + 8 always share an XCD. No
+ * counterpart in the reference. */
+int vs_xcd_ids(uint32_t* out, int blocks, int threads, vs_stream_t stream);
+
 /* Zero a workspace (stream-ordered). */
 int vs_workspace_init(void* ws, size_t bytes, vs_stream_t stream);
 
 /* Text of the calling thread's last error ("" if none). */
 const char* vs_last_error(void);
 
-/* Library ABI version (increments on any signature or struct change): 9. */
+/* Library ABI version (increments on any signature or struct change): 10. */
 int vs_version(void);
 
 #ifdef __cplusplus

@@ -412,3 +412,43 @@ def test_sampler_shim_sequence(dev):
         counts[ref.token] = counts.get(ref.token, 0) + 1
         produced += 1
     assert smp.counts == counts
+
+
+@pytest.mark.parametrize("B,V,radix", [(16, 163840, False), (16, 163840, True), (24, 40000, False), (8, 65536, True),
+                                       (32, 20000, False)])
+def test_xcd_exchange_identical(dev, B, V, radix):
+    """Batches whose rows each sit on one XCD exchange their data through that XCD's L2; the same calls with
+    VS_DEBUG_NO_XCD_EXCHANGE use the device-coherent level. Every class (greedy, top-k, whole-row value bins, the
+    gather and the radix fallback) returns the same bits both ways, and matches the oracle."""
+    from volundr_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(B * 7 + V + radix)
+    x = (rng.standard_normal((B, V)) * rng.choice([0.1, 1.0, 3.0], size=(B, 1))).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    hists = [rng.integers(0, V, size=int(rng.integers(0, 500))) for _ in range(B)]
+    u = rng.random(B)
+    base = _lib.DEBUG_FORCE_RADIX if radix else 0
+    try:
+        L.vs_set_debug(base)
+        a, _, _ = run(dev, x, ps, u, hists, label=f"xcd B{B} V{V} radix={radix}")
+        a = tuple(t.cpu() for t in (a.ids, a.logprobs, a.keep, a.flags))
+        L.vs_set_debug(base | _lib.DEBUG_NO_XCD_EXCHANGE)
+        b, _, _ = run(dev, x, ps, u, hists, label=f"coherent B{B} V{V} radix={radix}")
+        b = tuple(t.cpu() for t in (b.ids, b.logprobs, b.keep, b.flags))
+    finally:
+        L.vs_set_debug(0)
+    assert all(torch.equal(p, q) for p, q in zip(a, b))
+
+
+def test_xcd_placement(dev):
+    """The placement the L2 exchange relies on: workgroups b and b + 8 of a grid run on the same XCD (the dispatcher
+    deals workgroups to the 8 XCDs in turn), for grids of the sampling kernel's sizes."""
+    from volundr_amd import _lib
+    L = _lib.load()
+    for nb in (8, 160, 240, 256, 1024):
+        out = torch.full((nb,), 99, dtype=torch.int32, device=dev)
+        assert L.vs_xcd_ids(out.data_ptr(), nb, 512, torch.cuda.current_stream(dev).cuda_stream) == 0
+        ids = out.cpu().numpy()
+        assert (ids < 8).all(), ids
+        assert (ids == ids[np.arange(nb) % 8]).all(), f"grid {nb}: {ids[:32]}"
+        print(f"grid {nb}: XCDs of workgroups 0-7 {ids[:8].tolist()}", flush=True)

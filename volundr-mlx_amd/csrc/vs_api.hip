@@ -71,9 +71,23 @@ __global__ __launch_bounds__(512) void vs_stream_read_kernel(const uint4* __rest
   }
   if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
 }
+// The XCD (XCC id hardware register) each workgroup runs on: the placement check of vs_xcd_ids.
+__global__ void vs_xcd_ids_kernel(uint32_t* out) {
+  uint32_t id;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
+  if (threadIdx.x == 0) out[blockIdx.x] = id & 0xFu;
+}
 }  // namespace
 
 extern "C" {
+
+int vs_xcd_ids(uint32_t* out, int blocks, int threads, vs_stream_t stream) {
+  if (!out || blocks < 1 || threads < 1 || threads > 1024) return vs::fail(VS_EINVAL, "vs_xcd_ids: bad arguments");
+  hipLaunchKernelGGL(vs_xcd_ids_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return vs::hip_fail(e, "vs_xcd_ids: launch");
+  return VS_OK;
+}
 
 int vs_stream_read(const void* p, size_t bytes, int blocks, uint32_t* out, vs_stream_t stream) {
   if (!p || !out || blocks < 1 || bytes % 16 != 0 || (uintptr_t)p % 16 != 0)
@@ -96,7 +110,7 @@ int vs_launch_floor(int blocks, int threads, size_t lds_bytes, int reps, vs_stre
 
 const char* vs_last_error(void) { return vs::g_err.c_str(); }
 
-int vs_version(void) { return 9; }
+int vs_version(void) { return 10; }
 
 int vs_set_spin_limit(unsigned polls) {
   vs::g_spin_limit = polls;

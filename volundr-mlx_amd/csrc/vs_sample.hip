@@ -1057,7 +1057,7 @@ __device__ __forceinline__ void pair_range(int64_t n, int32_t probe, int lo, int
   *r1 = c1 == SNT ? n : probe_at(n, c1);
 }
 
-template <int DT>
+template <int DT, bool XL>
 __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   typedef DTraits<DT> TR;
   typedef typename TR::LT LT;
@@ -1476,11 +1476,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   };
   auto put_part = [&](u64 am, uint32_t nf, uint32_t kc, float mf, double se) {
     if (t == 0) {
-      st_dev(&parts[g].amkey, am);
-      st_dev(&parts[g].nfin, nf);
-      st_dev(&parts[g].kc, kc);
-      st_dev(&parts[g].mf, mf);
-      st_dev(&parts[g].se, se);
+      st_row<XL>(&parts[g].amkey, am);
+      st_row<XL>(&parts[g].nfin, nf);
+      st_row<XL>(&parts[g].kc, kc);
+      st_row<XL>(&parts[g].mf, mf);
+      st_row<XL>(&parts[g].se, se);
     }
   };
 
@@ -1561,9 +1561,9 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         float m = -__builtin_inff();
         double e = 0.0;
         if (t < G) {
-          k = ld_dev(&parts[t].amkey);
-          m = ld_dev(&parts[t].mf);
-          e = ld_dev(&parts[t].se);
+          k = ld_row<XL>(&parts[t].amkey);
+          m = ld_row<XL>(&parts[t].mf);
+          e = ld_row<XL>(&parts[t].se);
         }
         const u64 bam = wave_max(k);
         const float M = wave_max(m);
@@ -1691,7 +1691,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         int off = 0;
 #pragma unroll
         for (int v = 0; v < SNW; ++v) off += v < wv ? segc[v] : 0;
-        for (int j = Ln; j < cw; j += WAVE) st_dev(&cand[g * A.kcap + off + j], segw[j]);
+        for (int j = Ln; j < cw; j += WAVE) st_row<XL>(&cand[g * A.kcap + off + j], segw[j]);
         if (t < SNW) {  // the wave heads in descending order (equal ones, i.e. zeros, by wave): all 8 written
           const u64 hx = s.red64[8 + t];
           int rk = 0;
@@ -1700,7 +1700,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             const u64 hy = s.red64[8 + v];
             rk += ((hy > hx) | ((hy == hx) & (v < t))) ? 1 : 0;
           }
-          st_dev(&parts[g].heads[rk], hx);
+          st_row<XL>(&parts[g].heads[rk], hx);
         }
         kc = C;
         listed = true;
@@ -1758,11 +1758,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       VS_TR(A, 13);
     }
     if (listed) {
-      for (int i = C + t; i < CP; i += SNT) st_dev(&cand[g * A.kcap + i], (u64)0);
+      for (int i = C + t; i < CP; i += SNT) st_row<XL>(&cand[g * A.kcap + i], (u64)0);
     } else {  // the sorted local top-kc, zero padded to kr (sorted format) or CP (unsorted format)
       const int plen = ufmt ? CP : kr;
-      for (int i = t; i < plen; i += SNT) st_dev(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
-      if (ufmt && t < 8) st_dev(&parts[g].heads[t], t < kc ? s.tk[t] : (u64)0);
+      for (int i = t; i < plen; i += SNT) st_row<XL>(&cand[g * A.kcap + i], i < kc ? s.tk[i] : (u64)0);
+      if (ufmt && t < 8) st_row<XL>(&parts[g].heads[t], t < kc ? s.tk[t] : (u64)0);
     }
     // C counts every finite logit when there is no bound, and is >= k otherwise: the row's sum decides
     // min(k, finite count) exactly.
@@ -1793,7 +1793,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #pragma unroll
         for (int u = 0; u < KEYS_CAP / SNT; ++u) {
           const int idx = t + u * SNT;
-          r8[u] = idx < tot ? ld_dev(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
+          r8[u] = idx < tot ? ld_row<XL>(&cand[(idx >> lpl) * A.kcap + (idx & (plen - 1))]) : (u64)0;
         }
 #ifdef VS_TRACE_WAITS
         publish_wait();
@@ -1811,15 +1811,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           if (u < hu) {
             const int hx = ln + WAVE * u;
             const int hg = hx / r, hj = hx - hg * r;
-            if (hx < nh) hv[u] = ld_dev(ufmt ? &parts[hg].heads[hj] : &cand[hg * A.kcap + hj]);
+            if (hx < nh) hv[u] = ld_row<XL>(ufmt ? &parts[hg].heads[hj] : &cand[hg * A.kcap + hj]);
           }
         }
         if (ln < G) {
-          nf2 = (int)ld_dev(&parts[ln].nfin);
-          k2 = ld_dev(&parts[ln].amkey);
+          nf2 = (int)ld_row<XL>(&parts[ln].nfin);
+          k2 = ld_row<XL>(&parts[ln].amkey);
           if (!hb8) {
-            full = (int)ld_dev(&parts[ln].kc) >= r;
-            const u64 h = ld_dev(&cand[ln * A.kcap + r - 1]);
+            full = (int)ld_row<XL>(&parts[ln].kc) >= r;
+            const u64 h = ld_row<XL>(&cand[ln * A.kcap + r - 1]);
             h2 = full ? h : h2;
           }
         }
@@ -2292,7 +2292,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         if (t == 0) {
           atomicAdd(&ctl->gcount, (uint32_t)cb);
           atomicMax(&ctl->gmax, (uint32_t)cb);
-          st_dev(&parts[g].kc, (uint32_t)cb);
+          st_row<XL>(&parts[g].kc, (uint32_t)cb);
         }
         if (cb <= GB && cb <= GSMALL) {
           if (!few) {  // rare: many lane maxima near the bound but few kept logits
@@ -2305,7 +2305,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             })
             __syncthreads();
           }
-          for (int i = t; i < cb; i += SNT) st_dev(&gather[g * GB + i], s.keys[i]);
+          for (int i = t; i < cb; i += SNT) st_row<XL>(&gather[g * GB + i], s.keys[i]);
         }
         VS_TR(A, 26);
         HistSlot* h1 = hslots + slot++;
@@ -2327,7 +2327,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               int* offs = s.misc + M_OFFS;  // [G]
               int* cnts = s.misc + M_CNTS;  // [G]
               if (t < WAVE) {
-                const int c = t < G ? (int)ld_dev(&parts[t].kc) : 0;
+                const int c = t < G ? (int)ld_row<XL>(&parts[t].kc) : 0;
                 const int incl = wave_scan(c);
                 if (t < G) {
                   offs[t] = incl - c;
@@ -2341,7 +2341,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #pragma unroll
                 for (int u = 0; u < GCAP / SNT; ++u) {
                   const int idx = t + u * SNT;
-                  r[u] = (idx < G * GB && (idx & (GB - 1)) < cnts[idx >> sh]) ? ld_dev(&gather[idx]) : (u64)0;
+                  r[u] = (idx < G * GB && (idx & (GB - 1)) < cnts[idx >> sh]) ? ld_row<XL>(&gather[idx]) : (u64)0;
                 }
 #pragma unroll
                 for (int u = 0; u < GCAP / SNT; ++u) {
@@ -2474,7 +2474,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   hm &= hm - 1;
                   const int k = bt & 15;
                   const int i = 8 * (t + (k >> 2) * SNT) + 2 * (k & 3) + (bt >> 4);
-                  st_dev(&big[p++], key64(s.xv[i], (uint32_t)(lo + i)));
+                  st_row<XL>(&big[p++], key64(s.xv[i], (uint32_t)(lo + i)));
                 }
               }
               g0_writes = false;
@@ -2515,7 +2515,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #pragma unroll
                 for (int u = 0; u < NL; ++u) {  // every load in flight at once
                   const int i = t + u * SNT;
-                  r[u] = i < m ? ld_dev(&big[i]) : (u64)0;
+                  r[u] = i < m ? ld_row<XL>(&big[i]) : (u64)0;
                 }
                 __syncthreads();  // the fine bins are clear
                 VS_TRX(53);
@@ -2859,7 +2859,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   const int nloc = s.misc[16];  // <= gcount <= GCAP2
                   if (t == 0 && nloc) s.misc[17] = (int)atomicAdd(&ctl->g2count, (uint32_t)nloc);
                   __syncthreads();
-                  for (int i = t; i < nloc; i += SNT) st_dev(&gather[s.misc[17] + i], s.keys[i]);
+                  for (int i = t; i < nloc; i += SNT) st_row<XL>(&gather[s.misc[17] + i], s.keys[i]);
                   g0_writes = false;
                   VS_TR(A, 6);
                   {  // the last workgroup of the row resolves the exact positions
@@ -2882,7 +2882,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     // picks with scans and ballots, no barrier. A fine bin's members are contiguous in key order,
                     // so the in-bin cumulative masses are masked scans of the sorted keys.
                     if (t < WAVE) {
-                      u64 e1[1] = {t < m ? ld_dev(&gather[t]) : (u64)0};
+                      u64 e1[1] = {t < m ? ld_row<XL>(&gather[t]) : (u64)0};
                       wave_sort_desc<1>(e1);
                       const u64 kk = e1[0];
                       const float xs = key_value(kk) / tt;
@@ -2953,7 +2953,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   double* fds = (double*)(s.keys + 2 * GCAP2 + GCAP2 / 2);
                   u64* xch = (u64*)(s.misc + M_XCH);  // two 8-byte exchange slots
                   for (int i = t; i < m; i += SNT) {
-                    const u64 kk = ld_dev(&gather[i]);
+                    const u64 kk = ld_row<XL>(&gather[i]);
                     const float x = key_value(kk);
                     fk[i] = kk;
                     const float xs = x / tt;
@@ -3512,17 +3512,17 @@ using namespace vs;
 
 // Workgroups of the sampling kernel per CU for a dynamic LDS size, cached per (device, dtype): the query costs more
 // than the rest of a launch's host work, and a serving loop launches one shape over and over.
-static hipError_t occupancy(int dev, int dtype, const void* kfn, size_t lds, int* per_cu) {
+static hipError_t occupancy(int dev, int dtype, bool xl, const void* kfn, size_t lds, int* per_cu) {
   struct Entry {
     size_t lds;
     int per_cu;
   };
   static std::mutex mu;
-  static Entry cache[64][3];  // zero lds: not yet queried (every launch has LDS)
+  static Entry cache[64][3][2];  // zero lds: not yet queried (every launch has LDS)
   if (dev < 0 || dev >= 64 || dtype < 0 || dtype > 2)
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, kfn, SNT, lds);
   std::lock_guard<std::mutex> lk(mu);
-  Entry& c = cache[dev][dtype];
+  Entry& c = cache[dev][dtype][xl ? 1 : 0];
   if (c.lds != lds) {
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&c.per_cu, kfn, SNT, lds);
     if (e != hipSuccess) {
@@ -3586,12 +3586,22 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
   const int lds_ch = CH;
   const size_t lds = smem_bytes(lds_ch);
   if (lds > dv->lds_per_block) return fail(VS_EINVAL, "vs_sample_batch: LDS need exceeds the device limit");
-  const void* kfn = dtype == VS_F32    ? (const void*)vs_sample_kernel<VS_F32>
-                    : dtype == VS_BF16 ? (const void*)vs_sample_kernel<VS_BF16>
-                                       : (const void*)vs_sample_kernel<VS_F16>;
-  int per_cu = 0;
-  hipError_t e = occupancy(dv->device, dtype, kfn, lds, &per_cu);
+  // Two instances per dtype: XL exchanges a row's data through its XCD's L2 (every workgroup of each row on one XCD),
+  // the other through the device-coherent level.
+  auto kernel_fn = [dtype](bool xl) -> const void* {
+    if (xl)
+      return dtype == VS_F32    ? (const void*)vs_sample_kernel<VS_F32, true>
+             : dtype == VS_BF16 ? (const void*)vs_sample_kernel<VS_BF16, true>
+                                : (const void*)vs_sample_kernel<VS_F16, true>;
+    return dtype == VS_F32    ? (const void*)vs_sample_kernel<VS_F32, false>
+           : dtype == VS_BF16 ? (const void*)vs_sample_kernel<VS_BF16, false>
+                              : (const void*)vs_sample_kernel<VS_F16, false>;
+  };
+  int per_cu = 0, per_cu_xl = 0;
+  hipError_t e = occupancy(dv->device, dtype, false, kernel_fn(false), lds, &per_cu);
+  if (e == hipSuccess) e = occupancy(dv->device, dtype, true, kernel_fn(true), lds, &per_cu_xl);
   if (e != hipSuccess) return hip_fail(e, "vs_sample_batch: occupancy query");
+  if (per_cu_xl < per_cu) per_cu = per_cu_xl;
   const int maxres = per_cu * dv->cus;
   int RB = maxres / G;
   if (RB > rows_target) RB = rows_target;
@@ -3646,6 +3656,13 @@ static int sample_launch(const void* logits, int dtype, int B, int V, int64_t ld
     a.row0 = r0;
     a.B = (B - r0) < RB ? (B - r0) : RB;
     void* kargs[] = {&a};
+    // Workgroup b runs on XCD b % 8 (the dispatcher deals a grid's workgroups to the 8 XCDs in turn; a rotation of
+    // that order keeps equal b % 8 together, which is all this needs), and the kernel gives row r the workgroups
+    // b with (b % 8) * nb / 8 + b / 8 in [r G, r G + G). A row lies on one XCD exactly when nb is a multiple of 8
+    // and each XCD's nb / 8 workgroups hold whole rows.
+    const int nbl = a.B * G;
+    const bool xl = !(g_debug & VS_DEBUG_NO_XCD_EXCHANGE) && nbl % 8 == 0 && (nbl / 8) % G == 0;
+    const void* kfn = kernel_fn(xl);
     // The grid never exceeds what the device holds at once (RB above), so on an otherwise idle device every
     // workgroup of a row is resident and the row barriers complete; a plain launch is ~18 us cheaper than a
     // cooperative one on MI355X. VS_COOPERATIVE=1 requests the residency guarantee of a cooperative launch; without

@@ -31,6 +31,7 @@ OUT_TIMEOUT = 1 << 31
 DEBUG_FORCE_RADIX = 1
 DEBUG_SPIN_LATER_BARRIERS = 2
 DEBUG_WAIT_CLOCK = 4
+DEBUG_NO_XCD_EXCHANGE = 8
 
 # vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([
@@ -48,12 +49,12 @@ STATE_DTYPE = np.dtype([("rng", "<u8"), ("hist_off", "<i8"), ("hist_len", "<i4")
                         ("hist_base", "<i4")])
 assert STATE_DTYPE.itemsize == 48
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 EXPORTS = ("vs_sample_batch", "vs_sample_batch_state", "vs_state_fold", "vs_sample_workspace_bytes", "vs_verify_greedy",
            "vs_verify_workspace_bytes", "vs_topk_batch", "vs_draft_walk", "vs_draft_propose",
            "vs_draft_workspace_bytes", "vs_lmhead_verify_greedy", "vs_lmhead_workspace_bytes", "vs_lmhead_sample",
            "vs_lmhead_sample_workspace_bytes", "vs_set_spin_limit", "vs_workspace_init", "vs_last_error", "vs_version",
-           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_stream_read", "vs_set_cooperative", "vs_set_debug")
+           "vs_sample_batch_noalloc", "vs_sample_noalloc_scratch_bytes", "vs_launch_floor", "vs_stream_read", "vs_xcd_ids", "vs_set_cooperative", "vs_set_debug")
 
 _lib = None
 
@@ -95,6 +96,8 @@ def load():
     L.vs_lmhead_workspace_bytes.restype = sz
     L.vs_launch_floor.argtypes = [i32, i32, sz, i32, vp]
     L.vs_launch_floor.restype = i32
+    L.vs_xcd_ids.argtypes = [vp, i32, i32, vp]
+    L.vs_xcd_ids.restype = i32
     L.vs_set_debug.argtypes = [ctypes.c_uint]
     L.vs_set_debug.restype = i32
     L.vs_set_cooperative.argtypes = [i32]
