@@ -422,4 +422,39 @@ __device__ __forceinline__ bool row_barrier(uint32_t* ctr, uint32_t target, uint
   return *flag_lds != 0;
 }
 
+// Row barrier inside one XCD (the XL exchange of st_row / ld_row): workgroup g stores `want` in its own flag word
+// (flags[g]), then one wave polls the G words with non-temporal loads until each holds `want` or a later value of the
+// same call. A flag is ((u64)epoch << 32) | barrier number, where epoch counts the calls of the row (so a word left
+// by an earlier call, still in memory or in a stale L2 line, never passes) and barrier numbers grow within a call (a
+// workgroup that has passed may already have stored the next one). Every prior store and atomic of the
+// workgroup is acknowledged before its flag is stored (publish_wait). Bounded like row_barrier; `unreachable`
+// (a testing flag) makes every wait run to its bound.
+__device__ __forceinline__ bool flag_barrier(u64* flags, int g, int G, u64 want, bool unreachable, uint32_t limit,
+                                             uint64_t ticks, int* flag_lds) {
+  publish_wait();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(&flags[g], want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (threadIdx.x < WAVE) {
+    const int L = threadIdx.x;
+    const uint32_t ep = (uint32_t)(want >> 32);
+    uint32_t polls = 0;
+    int ok = 1;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      asm volatile("" ::: "memory");  // each trip loads the flags again
+      const u64 f = L < G ? __builtin_nontemporal_load(&flags[L]) : want;
+      const bool here = (uint32_t)(f >> 32) == ep && (uint32_t)f >= (uint32_t)want;
+      if (__all(here) && !unreachable) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++polls > limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {
+        ok = 0;
+        break;
+      }
+    }
+    if (L == 0) *flag_lds = ok;
+  }
+  __syncthreads();
+  return *flag_lds != 0;
+}
+
 }  // namespace vs

@@ -76,7 +76,7 @@ struct RowCtl {
   uint32_t mcnt;    // min-p kept count
   u64 mfix;         // min-p kept fixed-point mass
   double mf64;      // min-p kept float64 mass
-  uint32_t spare;   // kept zero
+  uint32_t epoch;   // calls of this row so far (the XL row-barrier flags carry it); cleanup advances it
   uint32_t nminkey; // ~ord32 of the smallest finite logit (max-reduced)
   uint32_t g2count; // second gather reservations
   uint32_t gmax;    // largest per-workgroup kept count
@@ -101,12 +101,18 @@ struct HistSlot {
   u64 mk[NBIN];
 };
 
-constexpr size_t OFF_PART = sizeof(RowCtl);
+// Areas written with workgroup-scope stores (parts, lists, gathers, flags) start on their own 128-byte lines,
+// apart from the lines that device-scope atomics update (the control block, the histogram slots).
+constexpr size_t OFF_PART = 128;
 constexpr size_t OFF_CAND = OFF_PART + sizeof(Part) * GMAX;
 constexpr size_t OFF_GATHER = OFF_CAND + sizeof(u64) * KEYS_CAP;
 constexpr size_t OFF_HIST = OFF_GATHER + sizeof(u64) * GCAP;
 constexpr size_t OFF_BIG = OFF_HIST + sizeof(HistSlot) * MAX_ROUNDS;
-constexpr size_t ROW_WS = OFF_BIG + sizeof(u64) * BIGCAP;
+constexpr size_t OFF_FLAGS = OFF_BIG + sizeof(u64) * BIGCAP;  // [GMAX] XL row-barrier flags
+constexpr size_t ROW_WS = OFF_FLAGS + sizeof(u64) * GMAX;
+static_assert(OFF_CAND % 128 == 0 && OFF_GATHER % 128 == 0 && OFF_HIST % 128 == 0 && OFF_BIG % 128 == 0 &&
+                  OFF_FLAGS % 128 == 0 && ROW_WS % 128 == 0,
+              "row workspace areas on 128-byte lines");
 
 struct SampleArgs {
   const void* logits;
@@ -1112,6 +1118,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   u64* cand = (u64*)(rws + OFF_CAND);
   u64* gather = (u64*)(rws + OFF_GATHER);
   HistSlot* hslots = (HistSlot*)(rws + OFF_HIST);
+  u64* bflags = (u64*)(rws + OFF_FLAGS);
+  const uint32_t epoch = ld_dev(&ctl->epoch);  // used at the row barriers and by the cleanup; lands with the logits
 
   const int V = A.V;
   // A request that needs no logits (sampler.py:96) reads only [0, vocab_valid) and takes no edits; with its stop
@@ -1472,7 +1480,8 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         st_dev(&hs->mk[t], (u64)0);
       }
     }
-    if (t < (int)(sizeof(RowCtl) / 4)) st_dev(&((uint32_t*)ctl)[t], 0u);
+    constexpr int EPW = offsetof(RowCtl, epoch) / 4;
+    if (t < (int)(sizeof(RowCtl) / 4)) st_dev(&((uint32_t*)ctl)[t], t == EPW ? epoch + 1u : 0u);
   };
   auto put_part = [&](u64 am, uint32_t nf, uint32_t kc, float mf, double se) {
     if (t == 0) {
@@ -1943,6 +1952,15 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   };
   // the testing flag VS_DEBUG_WAIT_CLOCK makes every row barrier unreachable, so each wait ends at the time bound
   auto bar_target = [&](uint32_t target) -> uint32_t { return (A.debug & VS_DEBUG_WAIT_CLOCK) ? 0xFFFFFFFFu : target; };
+  // the row's next barrier: flag words in its XCD's L2 (XL) or the device-scope arrival counter
+  auto rbar = [&]() -> bool {
+    ++nbar;
+    if constexpr (XL)
+      return flag_barrier(bflags, g, G, ((u64)epoch << 32) | nbar, (A.debug & VS_DEBUG_WAIT_CLOCK) != 0, bar_limit(nbar),
+                          A.spin_ticks, &s.misc[11]);
+    else
+      return row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+  };
   auto timed_out_final = [&]() {
     Final f;
     f.token = -1;
@@ -1996,12 +2014,18 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     if (st.n == 0) st.am = chunk_amkey();
     VS_TR(A, 21);
     if (t == 0) {
-      if (st.n) {
-        atomicAdd(&ctl->nfin, (uint32_t)st.n);
-        atomicMax(&ctl->mkey, st.mx1);
-        atomicMax(&ctl->nminkey, st.mx2);
+      if constexpr (XL) {  // each workgroup of the row reduces the G partials itself after the barrier
+        st_row<XL>(&parts[g].amkey, st.am);
+        st_row<XL>(&parts[g].nfin, (uint32_t)st.n);
+        st_row<XL>(&parts[g].heads[0], st.n ? ((u64)st.mx1 << 32) | st.mx2 : (u64)0);
+      } else {
+        if (st.n) {
+          atomicAdd(&ctl->nfin, (uint32_t)st.n);
+          atomicMax(&ctl->mkey, st.mx1);
+          atomicMax(&ctl->nminkey, st.mx2);
+        }
+        atomicMax(&ctl->amkey, st.am);
       }
-      atomicMax(&ctl->amkey, st.am);
     }
   }
 #ifdef VS_TRACE
@@ -2009,8 +2033,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   __syncthreads();
   VS_TR(A, 22);
 #endif
-  ++nbar;
-  ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+  ok = rbar();
   VS_TR(A, 3);
   VS_TRC(A, 31);
   Final fin;
@@ -2020,10 +2043,39 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   fin.keep = 0;
   bool g0_writes = true;  // false when the last workgroup of the row writes the result itself
   if (ok) {
-    const int n = (int)ld_relaxed(&ctl->nfin);
-    const uint32_t mkey = ld_relaxed(&ctl->mkey);
-    const uint32_t minkey = ~ld_relaxed(&ctl->nminkey);
-    const u64 amk = ld_relaxed64(&ctl->amkey);
+    int n;
+    uint32_t mkey, minkey;
+    u64 amk;
+    if constexpr (XL) {
+      if (t < WAVE) {
+        int nf = 0;
+        u64 mm = 0, ak = 0;
+        if (t < G) {
+          nf = (int)ld_row<XL>(&parts[t].nfin);
+          mm = ld_row<XL>(&parts[t].heads[0]);
+          ak = ld_row<XL>(&parts[t].amkey);
+        }
+        nf = wave_sum(nf);
+        const uint32_t m1 = wave_max((uint32_t)(mm >> 32)), m2 = wave_max((uint32_t)mm);
+        ak = wave_max(ak);
+        if (t == 0) {
+          s.red64[0] = ak;
+          s.red64[1] = ((u64)m1 << 32) | m2;
+          s.red64[2] = (u64)nf;
+        }
+      }
+      __syncthreads();
+      amk = s.red64[0];
+      mkey = (uint32_t)(s.red64[1] >> 32);
+      minkey = ~(uint32_t)s.red64[1];
+      n = (int)s.red64[2];
+      __syncthreads();
+    } else {
+      n = (int)ld_relaxed(&ctl->nfin);
+      mkey = ld_relaxed(&ctl->mkey);
+      minkey = ~ld_relaxed(&ctl->nminkey);
+      amk = ld_relaxed64(&ctl->amkey);
+    }
     if (n == 0) {  // sampler.py:131-132
       fin.token = (int32_t)key_index(amk);
       fin.flags = VS_OUT_NOFINITE;
@@ -2053,8 +2105,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           __syncthreads();
           HistSlot* hs = hslots + slot;
           if (t < NBIN && s.hc[t]) atomicAdd(&hs->cnt[t], s.hc[t]);
-          ++nbar;
-          ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+          ok = rbar();
           if (!ok) break;
           if (t < NBIN) {
             s.hc[t] = ld_relaxed(&hs->cnt[t]);
@@ -2290,8 +2341,10 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // each workgroup gathers into its own region of GB keys when its kept count fits
         const int GB = 1 << (31 - __builtin_clz(GCAP / G));  // power of two <= GCAP / G
         if (t == 0) {
-          atomicAdd(&ctl->gcount, (uint32_t)cb);
-          atomicMax(&ctl->gmax, (uint32_t)cb);
+          if constexpr (!XL) {
+            atomicAdd(&ctl->gcount, (uint32_t)cb);
+            atomicMax(&ctl->gmax, (uint32_t)cb);
+          }
           st_row<XL>(&parts[g].kc, (uint32_t)cb);
         }
         if (cb <= GB && cb <= GSMALL) {
@@ -2309,16 +2362,43 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         }
         VS_TR(A, 26);
         HistSlot* h1 = hslots + slot++;
-        if (t < NBIN && s.hc[t]) {
+        // XL rows with fixed-point sums only: each workgroup stores its whole coarse histogram in its own slot of
+        // the row's list area (unused by this class), and every workgroup sums the G slots in workgroup order after
+        // the barrier (integer sums: the same bits as the atomics). Otherwise the histograms meet in h1 by atomics.
+        constexpr int PSLOT_G = (KEYS_CAP * 8) / (NBIN * 12);
+        const bool pslot = XL && zfix_only && G <= PSLOT_G;
+        u64* pfix = cand;                           // [G][NBIN]
+        uint32_t* pcnt = (uint32_t*)(cand + G * NBIN);  // [G][NBIN]
+        if (pslot) {
+          if (t < NBIN) {
+            st_row<XL>(&pfix[g * NBIN + t], s.hfix[t]);
+            st_row<XL>(&pcnt[g * NBIN + t], s.hc[t]);
+          }
+        } else if (t < NBIN && s.hc[t]) {
           atomicAdd(&h1->cnt[t], s.hc[t]);
           atomicAdd(&h1->fix[t], s.hfix[t]);
           if (!zfix_only) unsafeAtomicAdd(&h1->f64[t], s.hf64[t]);
         }
-        ++nbar;
-        ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+        ok = rbar();
         if (ok) {
-          const int total = (int)ld_relaxed(&ctl->gcount);
-          const int gmax = (int)ld_relaxed(&ctl->gmax);
+          int total, gmax;
+          if constexpr (XL) {
+            if (t < WAVE) {
+              const int c = t < G ? (int)ld_row<XL>(&parts[t].kc) : 0;
+              const int tot = wave_sum(c), mx = wave_max(c);
+              if (t == 0) {
+                s.redi[0] = tot;
+                s.redi[1] = mx;
+              }
+            }
+            __syncthreads();
+            total = s.redi[0];
+            gmax = s.redi[1];
+            __syncthreads();
+          } else {
+            total = (int)ld_relaxed(&ctl->gcount);
+            gmax = (int)ld_relaxed(&ctl->gmax);
+          }
           VS_TR(A, 5);
           bool radix = false;
           if (total <= GSMALL && gmax <= GB) {
@@ -2360,7 +2440,28 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             radix = true;  // min-p on a large kept set: the radix path below handles it
           } else {
             // ---- large kept set: locate the top-p and draw positions by value bins ----
-            if (t < NBIN) {
+            if (pslot) {
+              if (t < NBIN) {  // every slot's loads in flight at once (slots past G read slot 0 and are dropped)
+                uint32_t cv[PSLOT_G];
+                u64 fv[PSLOT_G];
+#pragma unroll
+                for (int q = 0; q < PSLOT_G; ++q) {
+                  const int qq = q < G ? q : 0;
+                  cv[q] = ld_row<XL>(&pcnt[qq * NBIN + t]);
+                  fv[q] = ld_row<XL>(&pfix[qq * NBIN + t]);
+                }
+                uint32_t c = 0;
+                u64 f = 0;
+#pragma unroll
+                for (int q = 0; q < PSLOT_G; ++q) {
+                  c += q < G ? cv[q] : 0u;
+                  f += q < G ? fv[q] : (u64)0;
+                }
+                s.hc[t] = c;
+                s.hfix[t] = f;
+                s.hf64[t] = 0.0;
+              }
+            } else if (t < NBIN) {
               s.hc[t] = ld_relaxed(&h1->cnt[t]);
               s.hfix[t] = ld_relaxed64(&h1->fix[t]);
               s.hf64[t] = zfix_only ? 0.0 : ld_relaxed_f64(&h1->f64[t]);
@@ -2775,8 +2876,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                 }
               }
               VS_TR(A, 16);
-              ++nbar;
-              ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+              ok = rbar();
               VS_TR(A, 18);
               if (ok) {
                 for (int i = t; i < ns * NBIN; i += SNT) {
@@ -3102,8 +3202,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               unsafeAtomicAdd(&hr->f64[t], s.hf64[t]);
               atomicMax(&hr->mk[t], s.hmk[t]);
             }
-            ++nbar;
-            ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+            ok = rbar();
             if (ok) {
               auto load_slot = [&](HistSlot* hs) {
                 if (t < NBIN) {
@@ -3162,8 +3261,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                     unsafeAtomicAdd(&hs->f64[t], s.hf64[t]);
                     atomicMax(&hs->mk[t], s.hmk[t]);
                   }
-                  ++nbar;
-                  ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+                  ok = rbar();
                   if (!ok) return r;
                   load_slot(hs);
                 }
@@ -3210,8 +3308,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   atomicAdd(&ctl->mfix, mfx);
                   unsafeAtomicAdd(&ctl->mf64, mff);
                 }
-                ++nbar;
-                ok = row_barrier(&ctl->bar, bar_target(nbar * G), bar_limit(nbar), A.spin_ticks, &s.misc[11]);
+                ok = rbar();
                 if (ok) {
                   const int cm = (int)ld_relaxed(&ctl->mcnt);
                   const int km = cm > 1 ? cm : 1;
