@@ -882,13 +882,14 @@ __device__ __forceinline__ u64 fixed_mass(float e, float sh, float sc) {
 // e^d for d <= 0 with about 2 ulp relative error: 2^(d log2 e) from the hardware base-2 exponential, with the
 // rounding error of the product d * log2(e) (exact through an fma, plus the constant's own tail) applied as a
 // first-order correction: e^d = 2^y * 2^(lo) ~ 2^y (1 + lo ln 2) for the tiny lo.
-__device__ __forceinline__ float exp_nonpos(float d) {
+// `corr` is ln 2 for that correction (0 drops it: plain 2^(d L)).
+__device__ __forceinline__ float exp_nonpos(float d, float corr = 0.693147180559945309f) {
   const float L = 1.44269502162933349609375f;  // log2(e) rounded to float
   const float Llo = 1.9259629891e-8f;          // log2(e) - L
   const float y = d * L;
   const float lo = fmaf(d, L, -y) + d * Llo;
   const float e = __builtin_amdgcn_exp2f(y);
-  return fmaf(e, lo * 0.693147180559945309f, e);
+  return fmaf(e, lo * corr, e);
 }
 
 // Sorted-id range search: first position in ids[b, e) with ids[p] >= x.
@@ -2190,7 +2191,6 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           const bool m2 = (mode == 2) & ((x >= xhi) | (xs >= thr));
           return is_finite(x) & ((mode == 0) | m1 | m2);
         };
-        const double scale = A.fix_scale;
         // Value bins: u = xs0 - x/t >= 0 is monotone in the logit, so the fine index f = u * 65536 / span splits
         // the kept set, in sampler.py:140 order, into contiguous ranges. Bins are stored by digit 255 - c (coarse
         // c = f >> 8) and 255 - (f & 255) (fine), so that the 256-bin scan walks them in descending-logit order.
@@ -2200,18 +2200,32 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         // every kept mass is >= exp(-span) >= 1e6 / scale: each mass then carries a relative rounding error
         // <= 5e-7, and so does every partial sum of them, far inside the logprob tolerance. Otherwise (masses down
         // to exp(-40)) the passes also keep float64 sums per bin.
-        const bool zfix_only = (double)span <= A.zspan_max;
+        // Narrow rows (unit temperature, no top-k cut, span <= 4: near-flat rows such as
+        // whole-vocabulary nucleus sampling) take a shorter value-bin pass: masses 2^(d log2 e) from the hardware
+        // exponential without the product's correction term, in fixed point at 2^31, one LDS atomic per logit that
+        // carries the count in bits 45 and up (a workgroup's count <= 12288 < 2^14 and mass sum < 12288 * 2^31 <
+        // 2^45). Every mass is >= e^-4, so its relative error (the exponent's rounding, <= 2^-24 |d| log2 e, the
+        // constant's tail and the instruction's own ulp, ~4e-7 together; the fixed point's half unit, 1.3e-8) stays
+        // within the 5e-7 the fixed-point normaliser allows (below), and cumulative masses inherit that bound.
+        const bool narrow = tt == 1.0f && mode != 1 && span <= 4.0f;  // row-uniform: every workgroup agrees
+        const int fshift = narrow ? 31 : A.fix_shift;
+        const double scale = __builtin_ldexp(1.0, fshift);
+        const bool zfix_only = narrow || (double)span <= A.zspan_max;
         const double inv_scale = 1.0 / scale;  // a power of two: exact
-        const float fsc = __builtin_amdgcn_ldexpf(1.0f, A.fix_shift), fsh = __builtin_amdgcn_ldexpf(1.0f, A.fix_shift - 32);
+        const float fsc = __builtin_amdgcn_ldexpf(1.0f, fshift), fsh = __builtin_amdgcn_ldexpf(1.0f, fshift - 32);
+        constexpr float L2E_F = 1.44269502162933349609375f;  // log2(e) rounded to float
         auto fine_of = [&](float xs) -> int {  // xs = x / t
           const float u = xs0 - xs;
           int f = (int)(u * fscale);
           f = f < 1 ? 1 : (f > 65535 ? 65535 : f);
           return 65535 - f;  // (coarse digit << 8) | fine digit, at most 0xFFFE
         };
+        // exp_nonpos's correction weight: 0 in narrow rows, whose masses are then the narrow pass's bit for bit
+        // (fma(e, 0, e) == e, and fixed_mass at 2^31 is rint(e * 2^31))
+        const float corr = narrow ? 0.0f : 0.693147180559945309f;
         auto mass = [&](float xs, u64* fx) -> double {  // pr = exp(float32(x/t - xs0)) (sampler.py:141-142)
           const float d = xs - xs0;
-          const float e = exp_nonpos(d);
+          const float e = exp_nonpos(d, corr);
           *fx = fixed_mass(e, fsh, fsc);  // == rint((double)e * scale)
           return (double)e;
         };
@@ -2259,7 +2273,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         __syncthreads();
         // With few qualifying lanes the kept logits are also listed in LDS for the gather below; otherwise the
         // kept count exceeds GSMALL and no gather happens.
-        const bool few = nq * 4 <= SNT;
+        const bool few = nq * 4 <= SNT && !narrow;  // narrow rows take the dense pass in every workgroup
         // one instance of the loop per zfix_only value, so that the float64 atomic is not a branch in it, and a
         // third for the dense case at unit temperature without float64 sums and without a top-k cut: no division,
         // and the kept set is x >= xkeep (finite), since x / 1 == x
@@ -2327,7 +2341,39 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           })
           return cnt;
         };
-        const int cbr = !zfix_only ? pass1(std::true_type{}, std::false_type{})
+        // the narrow pass (see above): x / 1 == x, kept iff finite and x >= xkeep, bins and masses from d = x - xs0
+        // (xs0 - x == -d exactly, so the fine bin equals fine_of's)
+        auto pass1n = [&]() -> int {
+          int cnt = 0;
+          const int nel = hi - lo;
+          const float nfs = -fscale;
+          for (int i0 = t; i0 < nel; i0 += 4 * SNT) {
+            float xq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int iq = i0 + u * SNT;
+              xq[u] = s.xv[iq < nel ? iq : 0];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int i = i0 + u * SNT;
+              const float x = xq[u];
+              const bool keep = (i < nel) & (x >= xkeep) & (x < __builtin_inff());
+              const float d = x - xs0;
+              const uint32_t m = (uint32_t)__builtin_rintf(__builtin_amdgcn_exp2f(d * L2E_F) * 2147483648.0f);
+              int f = (int)(d * nfs);
+              f = f < 1 ? 1 : (f > 65535 ? 65535 : f);
+              const int fo = 65535 - f;
+              if (i < nel) fid[i] = keep ? (uint16_t)fo : (uint16_t)0xFFFFu;
+              const int dmy = t & (NBIN - 1);
+              atomicAdd(keep ? &s.hfix[fo >> 8] : &s.rfix[dmy], keep ? ((u64)1 << 45) | m : (u64)0);
+              cnt += keep ? 1 : 0;
+            }
+          }
+          return cnt;
+        };
+        const int cbr = narrow ? pass1n()
+                        : !zfix_only ? pass1(std::true_type{}, std::false_type{})
                         : (!few && tt == 1.0f && mode != 1) ? pass1(std::false_type{}, std::true_type{})
                                                             : pass1(std::false_type{}, std::false_type{});
         int cb;
@@ -2335,7 +2381,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           __syncthreads();
           cb = s.misc[15];
         } else {
-          cb = block_sum<SNT>(cbr, s.redi);
+          cb = block_sum<SNT>(cbr, s.redi);  // its barriers also order the pass's atomics before the unpacking
+          if (narrow && t < NBIN) {  // count in bits 45 and up, mass below
+            const u64 v = s.hfix[t];
+            s.hc[t] = (uint32_t)(v >> 45);
+            s.hfix[t] = v & (((u64)1 << 45) - 1);
+          }
+          if (narrow) __syncthreads();
         }
         VS_TR(A, 25);
         // each workgroup gathers into its own region of GB keys when its kept count fits
