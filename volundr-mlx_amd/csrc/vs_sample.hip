@@ -1093,7 +1093,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   uint64_t rng_next = 0;
   if (A.state) st = A.state[srow];
   // a token forced by the reasoning budget (sampler.py:88-90): the logits are not read, no draw is consumed
-  if (P.flags & VS_ROW_FORCE) {
+  if (__builtin_expect((P.flags & VS_ROW_FORCE) != 0, 0)) {
     if (g == 0) {
       Final f;
       f.token = P.force_token;
@@ -1625,7 +1625,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         mag = max3u(mag, __float_as_uint(xq[u]) & 0x7FFFFFFFu, __float_as_uint(xq[u + 1]) & 0x7FFFFFFFu);
       }
       hasf = t < nel;
-      if (mag >= 0x7F800000u) {
+      if (__builtin_expect(mag >= 0x7F800000u, 0)) {
         fmx = -__builtin_inff();
         hasf = false;
         FOR_XV({
@@ -1919,7 +1919,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
           A.list_vals[(size_t)r * A.list_k + i] = i < have ? key_value(s.tk[i]) : -__builtin_inff();
         }
       };
-      if (n == 0) {  // sampler.py:131-132
+      if (__builtin_expect(n == 0, 0)) {  // sampler.py:131-132
         if (A.list_k > 0) {
           write_list(0);
         } else {
@@ -1996,7 +1996,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       }
     }
     int nf = t < nel ? (nel - t + SNT - 1) / SNT : 0;
-    if (mag >= 0x7F800000u) {
+    if (__builtin_expect(mag >= 0x7F800000u, 0)) {
       nf = 0;
       fmx = -__builtin_inff();
       fmn = __builtin_inff();
@@ -2012,7 +2012,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
     lane_mk = mk;
     VS_TR(A, 20);
     Stats st = block_stats(nf, mk, nmk, s);
-    if (st.n == 0) st.am = chunk_amkey();
+    if (__builtin_expect(st.n == 0, 0)) st.am = chunk_amkey();
     VS_TR(A, 21);
     if (t == 0) {
       if constexpr (XL) {  // each workgroup of the row reduces the G partials itself after the barrier
@@ -2077,7 +2077,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       minkey = ~ld_relaxed(&ctl->nminkey);
       amk = ld_relaxed64(&ctl->amkey);
     }
-    if (n == 0) {  // sampler.py:131-132
+    if (__builtin_expect(n == 0, 0)) {  // sampler.py:131-132
       fin.token = (int32_t)key_index(amk);
       fin.flags = VS_OUT_NOFINITE;
     } else {
@@ -2558,7 +2558,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
 #pragma unroll
             for (int q = 0; q < NSET; ++q) ncand += q < ns ? (int)s.hc[set[q]] : 0;
             const int bigcap = BIGCAP < A.lds_ch / 2 ? BIGCAP : A.lds_ch / 2;  // they must fit the chunk area
-            if (ns > NSET) {
+            if (__builtin_expect(ns > NSET, 0)) {
               radix = true;
             } else if (ncand <= bigcap) {
               // ---- the selected coarse bins hold few enough logits: gather them all, and let the row's last
@@ -2638,7 +2638,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                   VS_TR_FLUSH(A);
                   return;
                 }
-                if (old >> 24) {  // a workgroup timed out and gathered nothing
+                if (__builtin_expect((old >> 24) != 0, 0)) {  // a workgroup timed out and gathered nothing
                   timed_out_final();
                   VS_TR_FLUSH(A);
                   return;
@@ -3020,7 +3020,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
                       VS_TR_FLUSH(A);
                       return;
                     }
-                    if (old >> 24) {  // a workgroup timed out and gathered nothing
+                    if (__builtin_expect((old >> 24) != 0, 0)) {  // a workgroup timed out and gathered nothing
                       timed_out_final();
                       VS_TR_FLUSH(A);
                       return;
@@ -3234,7 +3234,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
               }
             }
           }
-          if (ok && radix) {
+          if (__builtin_expect(ok && radix, 0)) {
             // ---- radix fallback: cooperative mass-weighted radix select on the 64-bit keys ----
             hist_clear(s);
             FOR_KEPT({
