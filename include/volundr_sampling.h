@@ -273,12 +273,15 @@ int vs_set_spin_limit(unsigned polls);
  * VS_DEBUG_WAIT_CLOCK: every row barrier is treated as unreachable, so each wait ends at its time bound (measures
  * the bound; every such row reports VS_OUT_TIMEOUT). VS_DEBUG_NO_XCD_EXCHANGE: the workgroups of a row exchange their
  * data through the device-coherent level even when they all run on one XCD (the default then uses that XCD's L2;
- * results are identical either way). No counterpart in the reference. */
+ * results are identical either way). VS_DEBUG_FAKE_XCD_SPLIT: in launches that use the XCD's L2, every row's last
+ * workgroup reports a neighbouring XCD, so the placement guard flags each such row VS_OUT_TIMEOUT (the path taken
+ * if the dispatcher ever split a row across XCDs). No counterpart in the reference. */
 enum {
   VS_DEBUG_FORCE_RADIX = 1u,
   VS_DEBUG_SPIN_LATER_BARRIERS = 2u,
   VS_DEBUG_WAIT_CLOCK = 4u,
-  VS_DEBUG_NO_XCD_EXCHANGE = 8u
+  VS_DEBUG_NO_XCD_EXCHANGE = 8u,
+  VS_DEBUG_FAKE_XCD_SPLIT = 16u
 };
 int vs_set_debug(unsigned flags);
 

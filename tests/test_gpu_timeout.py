@@ -293,3 +293,53 @@ def test_wait_time_bound(dev, coop):
     again = ops.sample_rows(x, rows)
     assert again.ids.cpu().tolist() == ids0
 
+
+
+def _debug(flags, fn):
+    L = _lib.load()
+    L.vs_set_debug(flags)
+    try:
+        r = fn()
+        torch.cuda.synchronize()
+    finally:
+        L.vs_set_debug(0)
+    return r
+
+
+def test_xcd_split_guard_flags_every_row(dev):
+    """The placement guard of the L2 exchange: with the testing flag that makes each row's last workgroup claim a
+    neighbouring XCD, every row of a batch laid out one row per XCD group (GREEDY, TOPK and FULL rows of C3 plus
+    greedy rows) reports VS_OUT_TIMEOUT rather than a result resolved from partials it cannot trust, commits
+    nothing, and leaves the workspace zeroed: the next ordinary call is exact."""
+    d = synth.CONFIGS["c3"](seed=2)
+    d["params"][3] = Sampling(temperature=0.0)  # a GREEDY row beside the TOPK and FULL ones
+    x = torch.from_numpy(d["logits"]).to(dev)
+    V = x.shape[1]
+    rows = ops.pack_rows(d["params"], d["u"], V, d["hists"]).to(dev)
+    clean = ops.sample_rows(x, rows)
+    ids0, lp0, fl0 = clean.ids.cpu().tolist(), clean.logprobs.cpu().tolist(), _flags(clean)
+    assert not any(f & OUT_TIMEOUT for f in fl0)
+    print("[xcd split] fake split, c3 seed 2", flush=True)
+    t = _debug(_lib.DEBUG_FAKE_XCD_SPLIT, lambda: ops.sample_rows(x, rows))
+    assert all(f & OUT_TIMEOUT for f in _flags(t)), _flags(t)
+    again = ops.sample_rows(x, rows)
+    assert again.ids.cpu().tolist() == ids0
+    assert again.logprobs.cpu().tolist() == lp0
+    assert _flags(again) == fl0
+
+
+def test_xcd_split_recovers_with_the_coherent_exchange(dev):
+    """The retry path under a (faked) split, on a 16-row batch laid out one row group per XCD: the plain and the
+    cooperative launch both report every row, the retry switches the process to the device-coherent exchange and
+    repeats the call, and the results equal an unforced call's."""
+    from volundr_amd.sampler import _sample_checked
+    d = synth.CONFIGS["c3"](seed=3)
+    x = torch.from_numpy(d["logits"]).to(dev)
+    n = x.shape[0]
+    args = (d["params"], list(d["u"]), d["hists"], [0] * n, [()] * n)
+    want = ops.sample_batch(x, *args)
+    w = (want.ids.cpu().tolist(), want.logprobs.cpu().tolist())
+    print("[xcd split] retry path with a fake split, c3 seed 3", flush=True)
+    with pytest.warns(RuntimeWarning, match="device-coherent"):
+        got, _ = _debug(_lib.DEBUG_FAKE_XCD_SPLIT, lambda: _sample_checked(x, *args))
+    assert (got.ids.cpu().tolist(), got.logprobs.cpu().tolist()) == w

@@ -409,12 +409,12 @@ __device__ __forceinline__ bool row_barrier(uint32_t* ctr, uint32_t target, uint
     uint32_t polls = 0;
     int ok = 1;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (ld_dev(ctr) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++polls > limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {
+    while (ld_dev(ctr) < target) {  // at most `limit` polls
+      if (++polls >= limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {
         ok = 0;
         break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
     *flag_lds = ok;
   }
@@ -445,11 +445,11 @@ __device__ __forceinline__ bool flag_barrier(u64* flags, int g, int G, u64 want,
       const u64 f = L < G ? __builtin_nontemporal_load(&flags[L]) : want;
       const bool here = (uint32_t)(f >> 32) == ep && (uint32_t)f >= (uint32_t)want;
       if (__all(here) && !unreachable) break;
-      __builtin_amdgcn_s_sleep(1);
-      if (++polls > limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {
+      if (++polls >= limit || __builtin_amdgcn_s_memrealtime() - t0 > ticks) {  // at most `limit` polls
         ok = 0;
         break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
     if (L == 0) *flag_lds = ok;
   }

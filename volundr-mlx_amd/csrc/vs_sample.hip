@@ -1121,6 +1121,18 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   HistSlot* hslots = (HistSlot*)(rws + OFF_HIST);
   u64* bflags = (u64*)(rws + OFF_FLAGS);
   const uint32_t epoch = ld_dev(&ctl->epoch);  // used at the row barriers and by the cleanup; lands with the logits
+  // XL placement guard: each workgroup tags its partial with (epoch << 4) | the XCD it runs on, and whoever reads
+  // the partials checks every tag against its own. A workgroup of the row on another XCD leaves a tag that is stale
+  // (its store stayed in its own XCD's L2) or names that XCD, so the row is reported VS_OUT_TIMEOUT instead of
+  // being resolved from data that could be stale (the host then repeats it with the device-coherent exchange). The
+  // testing flag VS_DEBUG_FAKE_XCD_SPLIT makes every row's last workgroup claim the neighbouring XCD.
+  uint32_t xcc = 0;
+  if constexpr (XL) {
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xFu;
+    if ((A.debug & VS_DEBUG_FAKE_XCD_SPLIT) && g == G - 1) xcc ^= 1u;
+  }
+  auto xtag = [&]() -> uint32_t { return (epoch << 4) | xcc; };
 
   const int V = A.V;
   // A request that needs no logits (sampler.py:96) reads only [0, vocab_valid) and takes no edits; with its stop
@@ -1491,7 +1503,19 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
       st_row<XL>(&parts[g].kc, kc);
       st_row<XL>(&parts[g].mf, mf);
       st_row<XL>(&parts[g].se, se);
+      if constexpr (XL) st_row<XL>(&parts[g].pad, xtag());
     }
+  };
+  // the timeout result of a row whose finishing workgroup found a partial from another XCD (or a stale one)
+  auto split_final = [&]() {
+    Final f;
+    f.token = -1;
+    f.lp = 0.0f;
+    f.flags = VS_OUT_TIMEOUT;
+    f.keep = 0;
+    write_out(A, row, f, st, rng_next);
+    __syncthreads();
+    cleanup(0);
   };
 
   if (cls == CLS_GREEDY) {
@@ -1570,17 +1594,27 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         u64 k = 0;
         float m = -__builtin_inff();
         double e = 0.0;
+        bool bad = false;
         if (t < G) {
           k = ld_row<XL>(&parts[t].amkey);
           m = ld_row<XL>(&parts[t].mf);
           e = ld_row<XL>(&parts[t].se);
+          if constexpr (XL) bad = ld_row<XL>(&parts[t].pad) != xtag();
         }
+        const bool split = XL && __any(bad);  // a partial from another XCD (or a stale one): no result
         const u64 bam = wave_max(k);
         const float M = wave_max(m);
         const float L2E = 1.44269504088896340736f;
         const double S =
             wave_sum((e > 0.0 && is_finite(M)) ? e * (double)__builtin_amdgcn_exp2f((m - M) * L2E) : 0.0);
-        if (t == 0) {
+        if (split) {
+          Final f;
+          f.token = -1;
+          f.lp = 0.0f;
+          f.flags = VS_OUT_TIMEOUT;
+          f.keep = 0;
+          write_out(A, row, f, st, rng_next);
+        } else if (t == 0) {
           const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
           const int r = A.row0 + row;
           const uint32_t fl = commit_state(A, r, (int32_t)key_index(bam), VS_OUT_GREEDY, st, rng_next);
@@ -1824,9 +1858,11 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
             if (hx < nh) hv[u] = ld_row<XL>(ufmt ? &parts[hg].heads[hj] : &cand[hg * A.kcap + hj]);
           }
         }
+        bool xbad = false;
         if (ln < G) {
           nf2 = (int)ld_row<XL>(&parts[ln].nfin);
           k2 = ld_row<XL>(&parts[ln].amkey);
+          if constexpr (XL) xbad = ld_row<XL>(&parts[ln].pad) != xtag();
           if (!hb8) {
             full = (int)ld_row<XL>(&parts[ln].kc) >= r;
             const u64 h = ld_row<XL>(&cand[ln * A.kcap + r - 1]);
@@ -1838,6 +1874,13 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         VS_TRX(51);
 #endif
         n = wave_sum(nf2);
+        if constexpr (XL) {
+          if (__any(xbad)) {  // every wave read the same tags: the whole workgroup takes this branch
+            split_final();
+            VS_TR_FLUSH(A);
+            return;
+          }
+        }
         bam = wave_max(k2);
         keff = k < n ? k : n;  // sampler.py:133-134
         if (keff < 1) keff = 1;
@@ -2019,6 +2062,7 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
         st_row<XL>(&parts[g].amkey, st.am);
         st_row<XL>(&parts[g].nfin, (uint32_t)st.n);
         st_row<XL>(&parts[g].heads[0], st.n ? ((u64)st.mx1 << 32) | st.mx2 : (u64)0);
+        st_row<XL>(&parts[g].pad, xtag());
       } else {
         if (st.n) {
           atomicAdd(&ctl->nfin, (uint32_t)st.n);
@@ -2043,40 +2087,46 @@ __global__ __launch_bounds__(SNT) void vs_sample_kernel(SampleArgs A) {
   fin.flags = VS_OUT_TIMEOUT;
   fin.keep = 0;
   bool g0_writes = true;  // false when the last workgroup of the row writes the result itself
-  if (ok) {
-    int n;
-    uint32_t mkey, minkey;
-    u64 amk;
-    if constexpr (XL) {
-      if (t < WAVE) {
-        int nf = 0;
-        u64 mm = 0, ak = 0;
-        if (t < G) {
-          nf = (int)ld_row<XL>(&parts[t].nfin);
-          mm = ld_row<XL>(&parts[t].heads[0]);
-          ak = ld_row<XL>(&parts[t].amkey);
-        }
-        nf = wave_sum(nf);
-        const uint32_t m1 = wave_max((uint32_t)(mm >> 32)), m2 = wave_max((uint32_t)mm);
-        ak = wave_max(ak);
-        if (t == 0) {
-          s.red64[0] = ak;
-          s.red64[1] = ((u64)m1 << 32) | m2;
-          s.red64[2] = (u64)nf;
-        }
+  // the row statistics: reduced from the G partials (XL; a failed barrier leaves them unused), or the atomics' sums
+  int n = 0;
+  uint32_t mkey = 0, minkey = 0;
+  u64 amk = 0;
+  if constexpr (XL) {
+    if (t < WAVE) {
+      int nf = 0;
+      u64 mm = 0, ak = 0;
+      bool bad = false;
+      if (t < G) {
+        nf = (int)ld_row<XL>(&parts[t].nfin);
+        mm = ld_row<XL>(&parts[t].heads[0]);
+        ak = ld_row<XL>(&parts[t].amkey);
+        bad = ld_row<XL>(&parts[t].pad) != xtag();
       }
-      __syncthreads();
-      amk = s.red64[0];
-      mkey = (uint32_t)(s.red64[1] >> 32);
-      minkey = ~(uint32_t)s.red64[1];
-      n = (int)s.red64[2];
-      __syncthreads();
-    } else {
-      n = (int)ld_relaxed(&ctl->nfin);
-      mkey = ld_relaxed(&ctl->mkey);
-      minkey = ~ld_relaxed(&ctl->nminkey);
-      amk = ld_relaxed64(&ctl->amkey);
+      const bool anybad = __any(bad);
+      nf = wave_sum(nf);
+      const uint32_t m1 = wave_max((uint32_t)(mm >> 32)), m2 = wave_max((uint32_t)mm);
+      ak = wave_max(ak);
+      if (t == 0) {
+        s.red64[0] = ak;
+        s.red64[1] = ((u64)m1 << 32) | m2;
+        s.red64[2] = (u64)nf;
+        s.red64[3] = anybad ? 1u : 0u;
+      }
     }
+    __syncthreads();
+    amk = s.red64[0];
+    mkey = (uint32_t)(s.red64[1] >> 32);
+    minkey = ~(uint32_t)s.red64[1];
+    n = (int)s.red64[2];
+    if (s.red64[3] != 0) ok = false;  // a partial from another XCD (or a stale one): the row reports VS_OUT_TIMEOUT
+    __syncthreads();
+  } else if (ok) {
+    n = (int)ld_relaxed(&ctl->nfin);
+    mkey = ld_relaxed(&ctl->mkey);
+    minkey = ~ld_relaxed(&ctl->nminkey);
+    amk = ld_relaxed64(&ctl->amkey);
+  }
+  if (ok) {
     if (__builtin_expect(n == 0, 0)) {  // sampler.py:131-132
       fin.token = (int32_t)key_index(amk);
       fin.flags = VS_OUT_NOFINITE;

@@ -32,6 +32,7 @@ DEBUG_FORCE_RADIX = 1
 DEBUG_SPIN_LATER_BARRIERS = 2
 DEBUG_WAIT_CLOCK = 4
 DEBUG_NO_XCD_EXCHANGE = 8
+DEBUG_FAKE_XCD_SPLIT = 16
 
 # vs_row_params, 96 bytes (layout fixed by the C header)
 ROW_DTYPE = np.dtype([

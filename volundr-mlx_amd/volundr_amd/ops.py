@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import math
 import threading
+import warnings
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
@@ -64,6 +65,17 @@ def reset_workspace(dev: torch.device, kind: str = "sample"):
         w = _ws.get(key)
         if w is not None:
             check(_lib.load().vs_workspace_init(w.data_ptr(), w.numel(), key[1]), "vs_workspace_init")
+
+
+def coherent_exchange_fallback():
+    """Make every later sampling launch of the process exchange row data at the device-coherent level
+    (VS_DEBUG_NO_XCD_EXCHANGE). The retry paths call it when rows still report VS_OUT_TIMEOUT under a cooperative
+    launch: with every workgroup resident, that means the placement guard saw a row whose workgroups did not share
+    one XCD. It replaces any testing flags set with vs_set_debug."""
+    L = _lib.load()
+    L.vs_set_debug(_lib.DEBUG_NO_XCD_EXCHANGE)
+    warnings.warn("volundr_amd: rows reported VS_OUT_TIMEOUT under a cooperative launch; sampling now exchanges row "
+                  "data at the device-coherent level (VS_DEBUG_NO_XCD_EXCHANGE)", RuntimeWarning, stacklevel=3)
 
 
 def _require_cuda(t: torch.Tensor, name: str):

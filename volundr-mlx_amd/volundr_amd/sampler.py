@@ -258,8 +258,15 @@ def _sample_checked(logits, sps, us, hists, prods, extras, argmax_vv=None):
     finally:
         L.vs_set_cooperative(prev)
     if (host[2].view(np.uint32) & OUT_TIMEOUT).any():
+        # every workgroup was resident, so the rows' workgroups cannot all have shared one XCD: from now on the
+        # process exchanges row data at the device-coherent level (ops.coherent_exchange_fallback)
         ops.reset_workspace(logits.device)
-        raise VsError("vs_sample_batch: an inter-workgroup wait timed out, also under a cooperative launch")
+        ops.coherent_exchange_fallback()
+        out = ops.sample_batch(logits, sps, us, hists, prods, extras, argmax_vv=argmax_vv)
+        host = out.block.cpu().numpy()
+        if (host[2].view(np.uint32) & OUT_TIMEOUT).any():
+            ops.reset_workspace(logits.device)
+            raise VsError("vs_sample_batch: an inter-workgroup wait timed out, also under a cooperative launch")
     return out, host
 
 

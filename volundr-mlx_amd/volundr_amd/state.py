@@ -36,7 +36,8 @@ import torch
 
 from . import _lib
 from ._lib import OUT_HIST_FULL, OUT_TIMEOUT, ROW_DTYPE, STATE_DTYPE, VS_ROW_FORCE, VsError, check
-from .ops import (_DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, pack_rows,
+from .ops import (_DTYPES, SampleOut, _require_cuda, _stream_handle, alloc_out, argmax_only_ok, coherent_exchange_fallback,
+                  pack_rows,
                   reset_workspace, workspace)
 from .sampler import TokenHistory
 
@@ -453,6 +454,12 @@ class DeviceSamplers:
             sub = sub_out.block.cpu()
         finally:
             L.vs_set_cooperative(prev)
+        if (sub[2].numpy().view(np.uint32) & OUT_TIMEOUT).any():
+            # as in sampler._sample_checked: the device-coherent exchange from now on, and one more attempt
+            reset_workspace(self.dev)
+            coherent_exchange_fallback()
+            self._launch(sub_x, sub_t, sub_out)
+            sub = sub_out.block.cpu()
         if (sub[2].numpy().view(np.uint32) & OUT_TIMEOUT).any():
             reset_workspace(self.dev)
             raise VsError("vs_sample_batch_state: an inter-workgroup wait timed out, also under a cooperative launch")
