@@ -452,3 +452,16 @@ def test_xcd_placement(dev):
         assert (ids < 8).all(), ids
         assert (ids == ids[np.arange(nb) % 8]).all(), f"grid {nb}: {ids[:32]}"
         print(f"grid {nb}: XCDs of workgroups 0-7 {ids[:8].tolist()}", flush=True)
+
+
+def test_xcd_and_coherent_launches_alternate(dev):
+    """One workspace shared by launches that alternate between the L2 exchange (16 rows: every row on one XCD) and
+    the device-coherent one (12 rows): the rows' control blocks carry their call count across both kinds, so the
+    flag barriers of a later call never pass on flags an earlier call left, and every call matches the oracle."""
+    rng = np.random.default_rng(77)
+    V = 163840
+    for rep, B in enumerate([16, 12, 16, 12, 16]):
+        x = (rng.standard_normal((B, V)) * rng.choice([0.1, 1.0], size=(B, 1))).astype(np.float32)
+        ps = [Sampling(temperature=float(rng.choice([1.0, 0.8])), top_p=float(rng.choice([0.9, 0.95, 1.0])),
+                       top_k=int(rng.choice([0, 0, 20]))) for _ in range(B)]
+        run(dev, x, ps, rng.random(B), label=f"alternate {rep} B{B}", max_excused=1)
