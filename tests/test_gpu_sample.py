@@ -465,3 +465,44 @@ def test_xcd_and_coherent_launches_alternate(dev):
         ps = [Sampling(temperature=float(rng.choice([1.0, 0.8])), top_p=float(rng.choice([0.9, 0.95, 1.0])),
                        top_k=int(rng.choice([0, 0, 20]))) for _ in range(B)]
         run(dev, x, ps, rng.random(B), label=f"alternate {rep} B{B}", max_excused=1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_xcd_exchange_half_precision(dev, dtype):
+    """16 rows of 163840 half-precision logits (one row per XCD group, the L2 exchange) with every class, penalties
+    and near-flat rows: oracle parity, and the same bits with the device-coherent exchange."""
+    from volundr_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(91 + (dtype == torch.float16))
+    B, V = 16, 163840
+    x = (rng.standard_normal((B, V)) * rng.choice([0.1, 1.0, 3.0], size=(B, 1))).astype(np.float32)
+    ps = rand_params(rng, B, V)
+    hists = [rng.integers(0, V, size=int(rng.integers(0, 800))) for _ in range(B)]
+    u = rng.random(B)
+    a, _, _ = run(dev, x, ps, u, hists, dtype=dtype, label=f"xcd {dtype}", max_excused=1)
+    try:
+        L.vs_set_debug(_lib.DEBUG_NO_XCD_EXCHANGE)
+        b, _, _ = run(dev, x, ps, u, hists, dtype=dtype, label=f"coherent {dtype}", max_excused=1)
+    finally:
+        L.vs_set_debug(0)
+    assert all(torch.equal(p.cpu(), q.cpu()) for p, q in zip((a.ids, a.logprobs, a.keep, a.flags),
+                                                             (b.ids, b.logprobs, b.keep, b.flags)))
+
+
+@pytest.mark.parametrize("span,radix", [(0.5, False), (3.9, False), (4.2, False), (1.0, True)])
+def test_narrow_rows(dev, span, radix):
+    """Unit-temperature whole-vocabulary rows whose kept values span about `span` (the narrow value-bin pass at 2^31
+    fixed point up to 4, the general one above), with top-p cuts, min-p (its radix select computes the same masses)
+    and the radix fallback forced: oracle parity."""
+    from volundr_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(int(span * 10) + radix)
+    B, V = 16, 163840
+    x = rng.uniform(-span / 2, span / 2, size=(B, V)).astype(np.float32)
+    ps = [Sampling(temperature=1.0, top_p=float(rng.choice([0.5, 0.9, 0.95, 1.0])),
+                   min_p=float(rng.choice([0.0, 0.0, 0.3]))) for _ in range(B)]
+    try:
+        L.vs_set_debug(_lib.DEBUG_FORCE_RADIX if radix else 0)
+        run(dev, x, ps, rng.random(B), label=f"narrow span {span} radix {radix}", max_excused=1)
+    finally:
+        L.vs_set_debug(0)
