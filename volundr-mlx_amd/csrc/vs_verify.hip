@@ -331,7 +331,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     const int wv = t / WAVE;
     const u64 kw = wave_max(am);
     const float mw = wave_max(m);
-    const double sw = wave_sum((se > 0.0 && is_finite(mw)) ? se * (double)expf(m - mw) : 0.0);
+    const float L2E = 1.44269504088896340736f;
+    const double sw = wave_sum((se > 0.0 && is_finite(mw)) ? se * (double)__builtin_amdgcn_exp2f((m - mw) * L2E) : 0.0);
     if (lane_id() == 0) {
       red64[wv] = kw;
       redf[wv] = mw;
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       double sb = 0.0;
 #pragma unroll
       for (int w = 0; w < VNW; ++w)
-        sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)expf(redf[w] - mb) : 0.0;
+        sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)__builtin_amdgcn_exp2f((redf[w] - mb) * L2E) : 0.0;
       VPart* pp = parts + (size_t)row * G + g;
       st_dev(&pp->amkey, kb);
       st_dev(&pp->mf, mb);
@@ -375,13 +376,20 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     }
     const u64 bam = wave_max(k);
     const float M = wave_max(mm);
-    const double S = wave_sum((e > 0.0 && is_finite(M)) ? e * exp((double)mm - (double)M) : 0.0);
+    // the rescaling factors and the logarithm in float (the logprob's tolerance is 1e-5 relative): v_exp_f32 of
+    // (m - M) log2 e, and log(S) = log1p(S - 1) with S >= 1 (it holds the maximum's own term), which keeps the float
+    // log1p's relative accuracy when one token dominates
+    const float L2E = 1.44269504088896340736f;
+    const double S =
+        wave_sum((e > 0.0 && is_finite(M)) ? e * (double)__builtin_amdgcn_exp2f((mm - M) * L2E) : 0.0);
     const int req = row / A.T;
     uint32_t last = 0;
     if (t == 0) {
       const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
       const int32_t tok = (int32_t)key_index(bam);
-      if (A.out_lp) A.out_lp[row] = (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + log(S))) : 0.0f;
+      if (A.out_lp)
+        A.out_lp[row] =
+            (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f;
       st_dev(&rowdone[row], 0u);
       if (A.T <= 33) {
         // one atomic carries the arrival and this position's mismatch bit (each row adds its own bit, so the sum is
