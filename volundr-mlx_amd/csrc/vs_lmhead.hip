@@ -245,14 +245,15 @@ __device__ __forceinline__ void ls_select(uint16_t* vbuf, int nw, int k, IdOf id
   if (ln == 0) *head = best;
 }
 
-// (m, s) pairs: s = sum exp(x - m) over finite x, accumulated in float64; the rescale factor exp(m - mm) <= 1 is a
-// float32 expf (relative error ~1e-7, far inside the logprob tolerance; a float64 exp per merge step made the
-// cross-lane and cross-workgroup merges cost tens of microseconds)
+// (m, s) pairs: s = sum exp(x - m) over finite x, accumulated in float64; the rescale factor exp(m - mm) <= 1 is
+// v_exp_f32 of (m - mm) log2 e (relative error a few 1e-7, far inside the logprob tolerance; a float64 exp per
+// merge step made the cross-lane and cross-workgroup merges cost tens of microseconds)
+__device__ __forceinline__ float exp_le0(float d) { return __builtin_amdgcn_exp2f(d * 1.44269504088896340736f); }
 __device__ __forceinline__ void lse_merge(float& m, double& s, float m2, double s2) {
   const float mm = m2 > m ? m2 : m;
   double r = 0.0;
-  if (s > 0.0 && is_finite(mm)) r += s * (double)expf(m - mm);
-  if (s2 > 0.0 && is_finite(mm)) r += s2 * (double)expf(m2 - mm);
+  if (s > 0.0 && is_finite(mm)) r += s * (double)exp_le0(m - mm);
+  if (s2 > 0.0 && is_finite(mm)) r += s2 * (double)exp_le0(m2 - mm);
   m = mm;
   s = r;
 }
@@ -821,7 +822,7 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
   double sm = 0.0;
 #pragma unroll
   for (int u = 0; u < MPT; ++u)
-    sm += (u * MNT + t < P && ss[u] > 0.0 && is_finite(m)) ? ss[u] * (double)expf(mm[u] - m) : 0.0;
+    sm += (u * MNT + t < P && ss[u] > 0.0 && is_finite(m)) ? ss[u] * (double)exp_le0(mm[u] - m) : 0.0;
   sm = wave_sum(sm);
   if (ln == 0) rs[wv] = sm;
   __syncthreads();
@@ -832,7 +833,10 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
     const float xj = am_is_nan(k) ? __builtin_nanf("") : key_value(k);
     const int32_t tok = (int32_t)key_index(k);
     A.out_argmax[pos] = tok;
-    if (A.out_lp) A.out_lp[pos] = (is_finite(xj) && sm > 0.0) ? (float)((double)xj - ((double)m + log(sm))) : 0.0f;
+    // log(sm) = log1p(sm - 1): sm >= 1 (the maximum's own term) keeps the float log1p's relative accuracy
+    if (A.out_lp)
+      A.out_lp[pos] =
+          (is_finite(xj) && sm > 0.0) ? (float)((double)xj - ((double)m + (double)log1pf((float)(sm - 1.0)))) : 0.0f;
     const int b = pos / A.T, tp = pos % A.T;
     if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
   }
