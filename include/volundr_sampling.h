@@ -16,7 +16,8 @@
  * stream-ordered on `stream` (a hipStream_t; 0 = the null stream); nothing is allocated inside the hot calls.
  * Return codes: 0 = OK; VS_EINVAL = bad argument; VS_EWORKSPACE = workspace too small; VS_EHIP = a HIP runtime
  * call failed. vs_last_error() describes the last failure of the calling thread.
- * Workspaces must be zeroed once (vs_workspace_init) before first use; the kernels leave them zeroed again.
+ * Workspaces must be zeroed once (vs_workspace_init) before first use; every call leaves its workspace ready for
+ * the next one, so no reset is needed.
  * Calls that share one workspace must be ordered on one stream.
  */
 #ifndef VOLUNDR_SAMPLING_H

@@ -122,3 +122,30 @@ def test_accept_lengths_around_the_packed_limit(dev, T):
             drafts[b, b] = (drafts[b, b] + 1) % V
     o = check(dev, x, drafts, V, torch.float32, f"T={T}")
     assert o.accept.cpu().tolist() == list(range(T))
+
+
+def test_more_rows_than_one_launch_holds(dev):
+    """2040 positions: more workgroups than the device keeps resident at once, so the call runs as several
+    launches, and requests whose rows straddle two launches read the earlier launch's tokens."""
+    rng = np.random.default_rng(21)
+    B, T, V = 120, 17, 5000
+    x = rng.standard_normal((B, T, V)).astype(np.float32)
+    tok = np.argmax(x, -1)
+    drafts = tok[:, :-1].astype(np.int32).copy()
+    for b in range(B):
+        j = b % T
+        if j < T - 1:
+            drafts[b, j] = (drafts[b, j] + 1) % V
+    o = check(dev, x, drafts, V, torch.float32, "B120 T17")
+    assert o.accept.cpu().tolist() == [b % T for b in range(B)]
+
+
+def test_repeated_calls_on_one_workspace(dev):
+    """Calls of different shapes back to back on one workspace: the words a call reads carry its own tag, so a
+    call never takes what an earlier one left."""
+    rng = np.random.default_rng(22)
+    for rep, (B, T, V) in enumerate([(4, 17, 7000), (1, 17, 7000), (3, 5, 9000), (4, 17, 7000), (2, 33, 4000)]):
+        x = rng.standard_normal((B, T, V)).astype(np.float32)
+        drafts = np.argmax(x, -1)[:, :-1].astype(np.int32).copy()
+        drafts[0, rep % (T - 1)] += 1
+        check(dev, x, drafts, V, torch.float32, f"shape {B}x{T}x{V}")

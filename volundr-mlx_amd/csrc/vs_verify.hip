@@ -7,10 +7,15 @@
 //
 // Each (b, t) row is split into G chunks, one 256-thread workgroup each, so B*T = 17..68 rows still fill the
 // 256 CUs. A workgroup reads its chunk once with 16-byte loads into VGPRs, reduces (first-max key, finite max) with
-// wave64 reductions, then sum(exp(x - max)); the last workgroup of a row (done counter) merges the G partials, and
-// the last row of a request computes the accept length. No workgroup ever waits for another.
+// wave64 reductions, then sum(exp(x - max)). No atomics: every word a workgroup publishes carries the call's tag
+// (a host counter), the row's last workgroup (g = G - 1) reloads the row's G partials until each shows the tag and
+// merges them, and the finisher of a request's last row reloads the request's other tokens the same way and
+// computes the accept length. A launch holds only as many rows as the device keeps resident at once, so every
+// workgroup a finisher waits for is running or done.
 #include "vs_common.h"
 #include "vs_host.h"
+
+#include <atomic>
 
 #pragma clang fp contract(off)
 
@@ -23,14 +28,17 @@ constexpr int VNF = 8;       // 16-byte loads per lane held in VGPRs by the fast
 constexpr int VGMAX = 64;
 constexpr int VRMAX = 8192;  // rows (B*T) per call: the counters live at fixed offsets so any call finds them zero
 
+// A workgroup's partial: five 64-bit words, each the call's tag (high half) over 32 bits of payload: the first-max
+// key (high, low), the finite maximum's bits, sum-exp's float64 bits (high, low). A 64-bit store is single-copy
+// atomic, so a word that shows the current tag holds the current payload.
 struct VPart {
-  u64 amkey;
-  float mf;
-  uint32_t pad;
-  double se;
-  u64 pad2;
+  u64 w[8];
 };
-static_assert(sizeof(VPart) == 32, "VPart layout");
+static_assert(sizeof(VPart) == 64, "VPart layout");
+constexpr int VPW = 5;  // words in use
+// Wall-clock bound (100 MHz ticks, 2 ms) on a finisher's wait; reached only if the device stopped running the
+// launch's other workgroups (the row then reports token -1, which no draft matches).
+constexpr uint64_t VWAIT_TICKS = 200000;
 
 struct VerifyArgs {
   const void* logits;
@@ -41,7 +49,9 @@ struct VerifyArgs {
   int32_t* out_argmax;
   int32_t* out_accept;
   float* out_lp;
-  char* ws;  // [VRMAX] row counters | [VRMAX] request counters | [R*G] VPart
+  int row0;       // first row of this launch
+  uint32_t tag;   // the call's tag (never 0), shared by its launches
+  char* ws;  // [VRMAX] row tokens (tag | token) | [R*G] VPart
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
@@ -137,16 +147,14 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   __shared__ u64 red64[VNW];
   __shared__ float redf[VNW];
   __shared__ double redd[VNW];
-  __shared__ uint32_t flag;
   const int t = threadIdx.x;
   const int G = A.G;
   const int nb = gridDim.x, b = blockIdx.x;
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
-  const int row = l / G, g = l % G;
-  uint32_t* rowdone = (uint32_t*)A.ws;
-  uint32_t* reqdone = rowdone + VRMAX;
-  u64* reqword = (u64*)(A.ws + 8 * VRMAX);  // T <= 33: arrivals << 32 | mismatch bit per draft position
-  VPart* parts = (VPart*)(A.ws + 16 * VRMAX);
+  const int row = A.row0 + l / G, g = l % G;
+  u64* rowtok = (u64*)A.ws;
+  VPart* parts = (VPart*)(A.ws + 8 * VRMAX);
+  const u64 tag = (u64)A.tag << 32;
 
   const int lo = g * A.CH;
   const int hi = min(A.vv, lo + A.CH);
@@ -352,28 +360,48 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       for (int w = 0; w < VNW; ++w)
         sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)__builtin_amdgcn_exp2f((redf[w] - mb) * L2E) : 0.0;
       VPart* pp = parts + (size_t)row * G + g;
-      st_dev(&pp->amkey, kb);
-      st_dev(&pp->mf, mb);
-      st_dev(&pp->se, sb);
+      const u64 sbits = (u64)__double_as_longlong(sb);
+      st_dev(&pp->w[0], tag | (kb >> 32));
+      st_dev(&pp->w[1], tag | (kb & 0xFFFFFFFFull));
+      st_dev(&pp->w[2], tag | (u64)__float_as_uint(mb));
+      st_dev(&pp->w[3], tag | (sbits >> 32));
+      st_dev(&pp->w[4], tag | (sbits & 0xFFFFFFFFull));
     }
   }
   VS_TR(A, 2);
-  if (block_arrive(&rowdone[row], &flag) != (uint32_t)(G - 1)) {
+  if (g != G - 1) {
     VS_TR_FLUSH(A);
     return;
   }
-  VS_TR(A, 3);
-  // last workgroup of this row: merge the G partials in one wave (G <= 64)
+  // the row's finisher: merge the G partials in one wave (G <= 64), each reloaded until all its words show the tag
   if (t < WAVE) {
     u64 k = 0;
     float mm = -__builtin_inff();
     double e = 0.0;
+    bool ok = true;
     if (t < G) {
       const VPart* pp = parts + (size_t)row * G + t;
-      k = ld_dev(&pp->amkey);
-      mm = ld_dev(&pp->mf);
-      e = ld_dev(&pp->se);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      u64 w[VPW];
+      for (;;) {
+#pragma unroll
+        for (int i = 0; i < VPW; ++i) w[i] = ld_dev(&pp->w[i]);
+        ok = true;
+#pragma unroll
+        for (int i = 0; i < VPW; ++i) ok = ok && (w[i] & 0xFFFFFFFF00000000ull) == tag;
+        if (ok || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      k = (w[0] << 32) | (w[1] & 0xFFFFFFFFull);
+      mm = __uint_as_float((uint32_t)w[2]);
+      e = __longlong_as_double((long long)((w[3] << 32) | (w[4] & 0xFFFFFFFFull)));
     }
+    if (__builtin_expect(!__all(ok), 0)) {  // the time bound was reached: token -1
+      k = 0;
+      mm = __builtin_nanf("");
+      e = 0.0;
+    }
+    VS_TR(A, 3);
     const u64 bam = wave_max(k);
     const float M = wave_max(mm);
     // the rescaling factors and the logarithm in float (the logprob's tolerance is 1e-5 relative): v_exp_f32 of
@@ -382,41 +410,35 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     const float L2E = 1.44269504088896340736f;
     const double S =
         wave_sum((e > 0.0 && is_finite(M)) ? e * (double)__builtin_amdgcn_exp2f((mm - M) * L2E) : 0.0);
-    const int req = row / A.T;
-    uint32_t last = 0;
+    const int req = row / A.T, tp = row - req * A.T;
+    const int32_t tok = bam ? (int32_t)key_index(bam) : -1;
     if (t == 0) {
       const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
-      const int32_t tok = (int32_t)key_index(bam);
       if (A.out_lp)
         A.out_lp[row] =
             (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f;
-      st_dev(&rowdone[row], 0u);
-      if (A.T <= 33) {
-        // one atomic carries the arrival and this position's mismatch bit (each row adds its own bit, so the sum is
-        // the union); the request's last row reads every mismatch from the returned word (specdec.py:327)
-        const int tp = row - req * A.T;
-        const bool mis = tp < A.T - 1 && A.drafts[(size_t)req * (A.T - 1) + tp] != tok;
-        const u64 add = (1ull << 32) | (mis ? (1ull << tp) : 0ull);
-        A.out_argmax[row] = tok;
-        const u64 old = __hip_atomic_fetch_add(&reqword[req], add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((uint32_t)(old >> 32) == (uint32_t)(A.T - 1)) {
-          const uint32_t mask = (uint32_t)((old + add) & 0xFFFFFFFFull) | (A.T - 1 < 32 ? (1u << (A.T - 1)) : 0u);
-          A.out_accept[req] = mask ? __builtin_ctz(mask) : 32;
-          st_dev(&reqword[req], 0ull);
-        }
-      } else {
-        st_dev(&A.out_argmax[row], tok);
-        publish_wait();
-        last = ctr_add(&reqdone[req], 1u) == (uint32_t)(A.T - 1);
-      }
+      A.out_argmax[row] = tok;
+      if (tp < A.T - 1) st_dev(&rowtok[row], tag | (u64)(uint32_t)tok);
     }
-    // last row of the request: accept prefix (specdec.py:327), 64 positions per ballot
-    if (lane_bcast(last, 0)) {
+    // the request's last row: its accept length (specdec.py:327), the other rows' tokens reloaded until they show
+    // the tag, 64 positions per ballot, stopping at the first mismatch
+    if (tp == A.T - 1) {
+      const int32_t* dr = A.drafts + (size_t)req * (A.T - 1);
       int nacc = 0;
       for (int base = 0; base < A.T - 1; base += WAVE) {
         const int i = base + t;
         bool stop = i >= A.T - 1;
-        if (!stop) stop = A.drafts[(size_t)req * (A.T - 1) + i] != ld_dev(&A.out_argmax[req * A.T + i]);
+        if (!stop) {
+          const u64* wp = &rowtok[(size_t)req * A.T + i];
+          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+          u64 w;
+          for (;;) {
+            w = ld_dev(wp);
+            if ((w & 0xFFFFFFFF00000000ull) == tag || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+          stop = (w & 0xFFFFFFFF00000000ull) != tag || dr[i] != (int32_t)(uint32_t)w;
+        }
         const unsigned long long mb2 = __ballot(stop);
         if (mb2) {
           nacc += __ffsll((long long)mb2) - 1;
@@ -424,10 +446,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
         }
         nacc += WAVE;
       }
-      if (t == 0) {
-        A.out_accept[req] = nacc;
-        st_dev(&reqdone[req], 0u);
-      }
+      if (t == 0) A.out_accept[req] = nacc;
     }
   }
   VS_TR_FLUSH(A);
@@ -440,7 +459,7 @@ using namespace vs;
 extern "C" size_t vs_verify_workspace_bytes(int B, int T, int V) {
   (void)V;
   size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
-  return 16 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
+  return 8 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
 }
 
 extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t ld, int vocab_valid,
@@ -500,15 +519,21 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   a.out_lp = out_logprob;
   a.ws = (char*)ws;
   a.trace = g_trace;
-  const size_t grid = (size_t)R * G;
-  if (grid > 0x7FFFFFFF) return fail(VS_EINVAL, "vs_verify_greedy: grid too large");
-  if (dtype == VS_F32)
-    hipLaunchKernelGGL(vs_verify_kernel<VS_F32>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
-  else if (dtype == VS_BF16)
-    hipLaunchKernelGGL(vs_verify_kernel<VS_BF16>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(vs_verify_kernel<VS_F16>, dim3((unsigned)grid), dim3(VNT), 0, (hipStream_t)stream, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "vs_verify_greedy: launch");
+  // the call's tag: a process-wide counter (0 skipped), so no word a previous call left can pass for this call's
+  static std::atomic<uint32_t> calls{0};
+  uint32_t tag = calls.fetch_add(1u) + 1u;
+  if (tag == 0) tag = calls.fetch_add(1u) + 1u;
+  a.tag = tag;
+  // rows per launch: all of a launch's workgroups resident at once (finishers wait for their row's workgroups)
+  const int cap = per_cu * dv->cus;
+  int rpl = cap / G;
+  if (rpl < 1) rpl = 1;
+  for (int r0 = 0; r0 < R; r0 += rpl) {
+    const int n = (R - r0) < rpl ? (R - r0) : rpl;
+    a.row0 = r0;
+    void* kargs[] = {&a};
+    const hipError_t e = hipLaunchKernel(kfn, dim3((unsigned)(n * G)), dim3(VNT), kargs, 0, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "vs_verify_greedy: launch");
+  }
   return VS_OK;
 }
