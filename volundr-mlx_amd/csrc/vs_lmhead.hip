@@ -1,6 +1,7 @@
 // vs_lmhead.hip - the bf16 lm_head GEMM with the greedy-verify epilogue fused in, for gfx950: logits are never
 // written to HBM; each workgroup reduces its slice of the vocabulary to per-position (first-max key, max, sum-exp)
-// partials, and the last workgroup to finish merges them into argmax, accept length and logprob.
+// partials; up to 32 positions, workgroup p merges position p from tagged partials (no atomics, no second launch),
+// beyond that a second launch merges them, into argmax, accept length and logprob.
 //
 // Reference: logits = lm_head(h) in bf16 (volundr-mlx/volundr.py:958-968, bf16 weight [vocab_size, hidden]; spec
 // verify's head call, spec/verify.py:223), then tok = argmax(logits[:, :vv]) and nacc = sum(cumprod(inp[1:] ==
@@ -35,7 +36,7 @@ constexpr int LNW = LNT / WAVE;     // waves per workgroup
 constexpr int KS = 32;              // k per MFMA
 constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
 constexpr int LPMAX = 2048;         // workgroups per launch
-constexpr size_t LWS_HEAD = 256;    // workspace head: the arrival counter (zero between calls)
+constexpr size_t LWS_HEAD = 256;    // workspace head (unused, kept for the layout)
 constexpr int LMPW = 4;             // positions one wave of the merging workgroup reduces at a time
 
 // Workgroup partials, position-major and one array per field ([R][P] each), so that the merge's lanes, which walk
@@ -53,20 +54,31 @@ __device__ __forceinline__ LParts lparts(char* ws, int R) {
   return q;
 }
 
+// merge_in partials: five 64-bit words per (position, workgroup), [R][P] at the workspace's partial area, each
+// the call's tag (high half) over 32 bits of payload (first-max key high/low, maximum, sum-exp high/low); a 64-bit
+// store is single-copy atomic, so a word that shows the tag holds this call's payload.
+constexpr int LTW = 8;  // words per partial slot (5 used)
+__device__ __forceinline__ u64* ltparts(char* ws) { return (u64*)(ws + LWS_HEAD); }
+// Wall-clock bound (100 MHz ticks, 100 ms) on a merging workgroup's wait for the other workgroups' partials: every
+// workgroup of the launch is resident on an otherwise idle device (one per CU), so it is reached only if other
+// work held CUs for that long; the position then reports token -1 (no draft matches it) and logprob NaN.
+constexpr uint64_t LWAIT_TICKS = 10000000;
+
 struct LHArgs {
   const uint16_t* h;  // [R, ldh] bf16
   int64_t ldh;
   const uint16_t* W;  // [N, ldw] bf16
   int64_t ldw;
   int N, vv, K, B, T, R, ntiles;
-  int merge_in;  // the last workgroup merges the partials (else vs_lmhead_merge_kernel does, one per position)
+  int merge_in;  // workgroup p merges position p from tagged partials (else vs_lmhead_merge_kernel does)
+  uint32_t tag;  // merge_in: the call's tag (never 0)
   const int32_t* drafts;  // [B, T-1]
   int32_t* out_argmax;    // [R]
   int32_t* out_accept;    // [B]
   float* out_lp;          // [R] or null
   uint16_t* out_logits;   // [R, ldo] bf16 or null
   int64_t ldo;
-  char* ws;  // [LWS_HEAD bytes: the arrival counters] then the workgroup partials (LParts); sampling: LSParts
+  char* ws;  // [LWS_HEAD bytes] then the workgroup partials (LParts, or tagged words when merge_in); sampling: LSParts
   const vs_row_params* params;  // sampling epilogue: one row per position
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
@@ -287,7 +299,6 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   const int nchunks = K / KC;
   const int t0 = (int)((long long)wg * A.ntiles / P), t1 = (int)((long long)(wg + 1) * A.ntiles / P);
   const int rounds = (t1 - t0 + LNW * NTW - 1) / (LNW * NTW);
-  uint32_t* arrivals = (uint32_t*)A.ws;
   const LParts parts = lparts(A.ws, A.R);
   __shared__ uint32_t last_flag;
   VS_TR_DECL(A);
@@ -295,8 +306,10 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   // accept lengths start at T-1 (every draft accepted); the merge lowers them to the first mismatch. A coherent
   // store: the merging workgroup may run on another XCD, and workgroup 0 arrives (after waiting for this store)
   // before the merge starts.
-  if (!SAMPLE && wg == 0)
+  if (!SAMPLE && wg == 0) {
     for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
+    publish_wait();  // complete before this workgroup's partials (stored much later) can release a merge
+  }
   if constexpr (SAMPLE) {
     if (t < 16) {
       int vl = 0, c = LS_UNSUPPORTED;
@@ -620,6 +633,15 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       q.mf[ix] = m;
       q.se[ix] = s;
       q.nfin[ix] = nf;
+    } else if (A.merge_in) {
+      u64* w = ltparts(A.ws) + ((size_t)t * P + wg) * LTW;
+      const u64 tg = (u64)A.tag << 32;
+      const u64 sb = (u64)__double_as_longlong(s);
+      st_dev(&w[0], tg | (k >> 32));
+      st_dev(&w[1], tg | (k & 0xFFFFFFFFull));
+      st_dev(&w[2], tg | (u64)__float_as_uint(m));
+      st_dev(&w[3], tg | (sb >> 32));
+      st_dev(&w[4], tg | (sb & 0xFFFFFFFFull));
     } else {
       const size_t ix = (size_t)t * LPMAX + wg;
       st_dev(&parts.amkey[ix], k);
@@ -656,123 +678,86 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     return;
   }
   VS_TR(A, 20);
-  if (!A.merge_in) {
+  if (!A.merge_in || wg >= R) {
     VS_TR_FLUSH(A);
     return;
   }
-  // The last workgroup to arrive merges every position's P partials (no second launch): wave w takes positions
-  // w, w + LNW, ..., LMPW of them at a time, each lane P / 64 partials of each, every load in flight at once;
-  // first-max argmax, logprob, and the accept length as the first mismatching draft position
-  // (specdec.py:327: nacc = the leading matches).
-  // Arrival in two levels, so that no counter takes more than P / 8 + 8 atomics (hundreds of same-address atomics
-  // from every CU serialise at the coherent level): the workgroups of one XCD (blockIdx % 8) count on their own
-  // counter, the last of each XCD on the top counter.
+  // Workgroup p merges position p (no atomics): thread i reloads workgroup i's partial until its five words show
+  // the call's tag, then the block takes the first-max key, the maximum, and the sum-exp rescaled to it; the
+  // accept length is lowered to the first mismatching draft position (specdec.py:327) by one atomicMin per
+  // mismatching position.
+  __syncthreads();  // the workgroup reduction above is done with rk / rm / rs
   {
-    const int xcd = wg & 7;
-    const uint32_t nx = (uint32_t)((P - xcd + 7) / 8);  // workgroups of this XCD
-    if (block_arrive(arrivals + 1 + xcd, &last_flag) != nx - 1) {
-      VS_TR_FLUSH(A);
-      return;
+    const int p = wg;
+    const u64 tg = (u64)A.tag << 32;
+    u64 k = 0;
+    float m = -__builtin_inff();
+    double sv = 0.0;
+    int ok = 1;
+    if (t < P) {
+      const u64* w = ltparts(A.ws) + ((size_t)p * P + t) * LTW;
+      const uint64_t c0 = __builtin_amdgcn_s_memrealtime();
+      u64 v[5];
+      for (;;) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) v[i] = ld_dev(&w[i]);
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) all = all && (v[i] & 0xFFFFFFFF00000000ull) == tg;
+        if (all) break;
+        if (__builtin_amdgcn_s_memrealtime() - c0 > LWAIT_TICKS) {
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      k = (v[0] << 32) | (v[1] & 0xFFFFFFFFull);
+      m = __uint_as_float((uint32_t)v[2]);
+      sv = __longlong_as_double((long long)((v[3] << 32) | (v[4] & 0xFFFFFFFFull)));
     }
-    const uint32_t nlevels = (uint32_t)(P < 8 ? P : 8);
-    if (block_arrive(arrivals, &last_flag) != nlevels - 1) {
-      VS_TR_FLUSH(A);
-      return;
+    VS_TR(A, 21);
+    const u64 kw = wave_max(k);
+    const float mw = wave_max(m);
+    const int okw = __all(ok) ? 1 : 0;
+    if (ln == 0) {
+      rk[wv][0] = kw;
+      rm[wv][0] = mw;
+      last_flag = 1;
+    }
+    __syncthreads();
+    if (ln == 0 && !okw) last_flag = 0;  // any wave's failure clears it (benign race: all write 0)
+    u64 K0 = rk[0][0];
+    float M = rm[0][0];
+#pragma unroll
+    for (int q = 1; q < LNW; ++q) {
+      K0 = rk[q][0] > K0 ? rk[q][0] : K0;
+      M = rm[q][0] > M ? rm[q][0] : M;
+    }
+    const float L2E = 1.44269504088896340736f;
+    const double sw =
+        wave_sum((sv > 0.0 && is_finite(M)) ? sv * (double)__builtin_amdgcn_exp2f((m - M) * L2E) : 0.0);
+    if (ln == 0) rs[wv][0] = sw;
+    __syncthreads();
+    if (t == 0) {
+      double S = 0.0;
+#pragma unroll
+      for (int q = 0; q < LNW; ++q) S += rs[q][0];
+      VS_TR(A, 24);
+      const bool good = last_flag != 0;
+      const float xj = am_is_nan(K0) ? __builtin_nanf("") : key_value(K0);
+      const int32_t tok = good ? (int32_t)key_index(K0) : -1;
+      A.out_argmax[p] = tok;
+      // log(S) = log1p(S - 1): S >= 1 (the maximum's own term), so the float log keeps its relative accuracy also
+      // when one token dominates (S - 1 tiny)
+      if (A.out_lp)
+        A.out_lp[p] = !good ? __builtin_nanf("")
+                            : (is_finite(xj) && S > 0.0)
+                                  ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0))))
+                                  : 0.0f;
+      const int b = p / A.T, tp = p % A.T;
+      if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
     }
   }
-  VS_TR(A, 21);
-  constexpr int LPL = LPMAX / WAVE;  // partials per lane at most
-  for (int p0 = wv; p0 < R; p0 += LNW * LMPW) {
-    u64 kk[LMPW][LPL / 8];
-    float mm[LMPW][LPL / 8];
-    double ss[LMPW][LPL / 8];
-    const int per = (P + WAVE - 1) / WAVE;  // partials per lane
-    // up to LPL / 8 = 4 partials per lane are held per position (P <= 256 here; larger P loops below)
-    u64 kb[LMPW];
-    float mb[LMPW];
-    double sb[LMPW];
-#pragma unroll
-    for (int q = 0; q < LMPW; ++q) {
-      kb[q] = 0;
-      mb[q] = -__builtin_inff();
-      sb[q] = 0.0;
-    }
-    for (int u0 = 0; u0 < per; u0 += LPL / 8) {
-#pragma unroll
-      for (int q = 0; q < LMPW; ++q) {
-        const int pos = p0 + q * LNW;
-#pragma unroll
-        for (int u = 0; u < LPL / 8; ++u) {
-          const int i = (u0 + u) * WAVE + ln;
-          const bool in = pos < R && u0 + u < per && i < P;
-          // unconditional loads from a clamped (valid) address, masked afterwards: a coherent load cannot be
-          // speculated, so a guarded one would become a branch and serialise the round trips
-          const size_t ix = (size_t)(pos < R ? pos : 0) * LPMAX + (in ? i : 0);
-          const u64 k0 = ld_dev(&parts.amkey[ix]);
-          const float m0 = ld_dev(&parts.mf[ix]);
-          const double s0 = ld_dev(&parts.se[ix]);
-          kk[q][u] = in ? k0 : (u64)0;
-          mm[q][u] = in ? m0 : -__builtin_inff();
-          ss[q][u] = in ? s0 : 0.0;
-        }
-      }
-#ifdef VS_TRACE
-      publish_wait();
-      VS_TR(A, 23);
-#endif
-      // the row maximum first (one wave max), then every partial sum rescaled to it once: no pairwise merges
-#pragma unroll
-      for (int q = 0; q < LMPW; ++q) {
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int u = 0; u < LPL / 8; ++u) {
-          kb[q] = kk[q][u] > kb[q] ? kk[q][u] : kb[q];
-          mx = mm[q][u] > mx ? mm[q][u] : mx;
-        }
-        mx = wave_max(mx);
-        const float mt = mx > mb[q] ? mx : mb[q];  // the running maximum over the batches of partials
-        const float L2E = 1.44269504088896340736f;
-        double acc = sb[q] > 0.0 && is_finite(mt) ? sb[q] * (double)__builtin_amdgcn_exp2f((mb[q] - mt) * L2E) : 0.0;
-#pragma unroll
-        for (int u = 0; u < LPL / 8; ++u)
-          acc += (ss[q][u] > 0.0 && is_finite(mt)) ? ss[q][u] * (double)__builtin_amdgcn_exp2f((mm[q][u] - mt) * L2E)
-                                                   : 0.0;
-        mb[q] = mt;
-        sb[q] = acc;
-      }
-    }
-    VS_TR(A, 24);
-    // the reductions of the LMPW positions, then lane q finishes position q (its outputs in parallel)
-    u64 kf = 0;
-    float mf = 0.0f;
-    double sf = 0.0;
-#pragma unroll
-    for (int q = 0; q < LMPW; ++q) {
-      const u64 k = wave_max(kb[q]);
-      const double sm = wave_sum(sb[q]);
-      kf = ln == q ? k : kf;
-      mf = ln == q ? mb[q] : mf;  // mb is already the same in every lane
-      sf = ln == q ? sm : sf;
-    }
-    VS_TR(A, 25);
-    {
-      const int pos = p0 + ln * LNW;
-      if (ln < LMPW && pos < R) {
-        const float xj = am_is_nan(kf) ? __builtin_nanf("") : key_value(kf);
-        const int32_t tok = (int32_t)key_index(kf);
-        A.out_argmax[pos] = tok;
-        // log(s) = log1p(s - 1): s >= 1 (the maximum's own term), so the float log keeps its relative accuracy
-        // also when one token dominates (s - 1 tiny)
-        if (A.out_lp)
-          A.out_lp[pos] = (is_finite(xj) && sf > 0.0)
-                              ? (float)((double)xj - ((double)mf + (double)log1pf((float)(sf - 1.0))))
-                              : 0.0f;
-        const int b = pos / A.T, tp = pos % A.T;
-        if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
-      }
-    }
-  }
-  if (t < 9) st_dev(arrivals + t, 0u);  // zero again for the next call on this workspace
   VS_TR(A, 22);
   VS_TR_FLUSH(A);
 }
@@ -842,8 +827,7 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
   }
 }
 
-// Positions up to which the last workgroup merges them itself (beyond, the merge's serial work in one workgroup
-// outweighs a second launch).
+// Positions up to which the launch's own workgroups merge them (beyond, a second launch does).
 constexpr int LMERGE_IN = 32;
 
 template <int NTT, int NTW, int KC>
@@ -959,7 +943,7 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   a.T = T;
   a.R = (int)R;
   a.ntiles = (N + 15) / 16;
-  a.merge_in = R <= LMERGE_IN;
+  a.tag = next_call_tag();
   a.drafts = drafts;
   a.out_argmax = out_argmax;
   a.out_accept = out_accept;
@@ -971,6 +955,7 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   int P = dv->cus;  // one workgroup per CU, each over a contiguous range of vocabulary tiles
   if (P > a.ntiles) P = a.ntiles;
   if (P > LPMAX) P = LPMAX;
+  a.merge_in = R <= LMERGE_IN && R <= P && P <= LNT;  // one merging workgroup per position, one thread per partial
   const int ntt = (int)((R + 15) / 16);
   switch (ntt) {
     case 1: return kc512 ? lmhead_launch<1, 4, 512>(a, P, (hipStream_t)stream)

@@ -15,8 +15,6 @@
 #include "vs_common.h"
 #include "vs_host.h"
 
-#include <atomic>
-
 #pragma clang fp contract(off)
 
 namespace vs {
@@ -519,11 +517,7 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   a.out_lp = out_logprob;
   a.ws = (char*)ws;
   a.trace = g_trace;
-  // the call's tag: a process-wide counter (0 skipped), so no word a previous call left can pass for this call's
-  static std::atomic<uint32_t> calls{0};
-  uint32_t tag = calls.fetch_add(1u) + 1u;
-  if (tag == 0) tag = calls.fetch_add(1u) + 1u;
-  a.tag = tag;
+  a.tag = next_call_tag();
   // rows per launch: all of a launch's workgroups resident at once (finishers wait for their row's workgroups)
   const int cap = per_cu * dv->cus;
   int rpl = cap / G;
