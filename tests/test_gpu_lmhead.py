@@ -78,6 +78,17 @@ def test_lmhead_verify_shapes(dev, B, T):
     _check(o, got, h, w, drafts, B, T, vv)
 
 
+@pytest.mark.parametrize("B,T,N", [(4, 17, 900), (1, 17, 200)])
+def test_lmhead_fewer_workgroups_than_positions(dev, B, T, N):
+    """A vocabulary of fewer 16-row tiles than positions gives fewer workgroups than positions, so a second launch
+    merges the partials instead of one workgroup per position."""
+    K = 1024
+    vv = N - 7
+    h, w, drafts = _case(B * 1000 + N, B, T, K, N, scale=4.0)
+    o, got = _run(dev, h, w, drafts, B, T, vv)
+    _check(o, got, h, w, drafts, B, T, vv)
+
+
 def test_lmhead_hidden_5120_and_exact_ties(dev):
     B, T, K, N = 1, 17, 5120, 20000
     h, w, drafts = _case(7, B, T, K, N, scale=4.0)

@@ -1,7 +1,7 @@
 // vs_lmhead.hip - the bf16 lm_head GEMM with the greedy-verify epilogue fused in, for gfx950: logits are never
 // written to HBM; each workgroup reduces its slice of the vocabulary to per-position (first-max key, max, sum-exp)
-// partials; up to 32 positions, workgroup p merges position p from tagged partials (no atomics, no second launch),
-// beyond that a second launch merges them, into argmax, accept length and logprob.
+// partials; workgroup p merges position p from tagged partials (no atomics, no second launch; a second launch
+// merges them when the vocabulary gives fewer workgroups than positions), into argmax, accept length and logprob.
 //
 // Reference: logits = lm_head(h) in bf16 (volundr-mlx/volundr.py:958-968, bf16 weight [vocab_size, hidden]; spec
 // verify's head call, spec/verify.py:223), then tok = argmax(logits[:, :vv]) and nacc = sum(cumprod(inp[1:] ==
@@ -828,7 +828,7 @@ __global__ __launch_bounds__(MNT) void vs_lmhead_merge_kernel(LHArgs A, int P) {
 }
 
 // Positions up to which the launch's own workgroups merge them (beyond, a second launch does).
-constexpr int LMERGE_IN = 32;
+constexpr int LMERGE_IN = LRMAX;
 
 template <int NTT, int NTW, int KC>
 static int lmhead_launch(const LHArgs& a, int P, hipStream_t stream) {
