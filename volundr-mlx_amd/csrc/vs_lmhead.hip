@@ -304,8 +304,8 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   VS_TR_DECL(A);
   VS_TR(A, 0);
   // accept lengths start at T-1 (every draft accepted); the merge lowers them to the first mismatch. A coherent
-  // store: the merging workgroup may run on another XCD, and workgroup 0 arrives (after waiting for this store)
-  // before the merge starts.
+  // store, waited for: the merging workgroups run on other XCDs, and each merges only after it has seen workgroup
+  // 0's partials, so every atomicMin follows it (a second merge launch follows it anyway).
   if (!SAMPLE && wg == 0) {
     for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
     publish_wait();  // complete before this workgroup's partials (stored much later) can release a merge

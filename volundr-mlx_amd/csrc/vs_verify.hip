@@ -24,7 +24,7 @@ constexpr int VNW = VNT / WAVE;
 constexpr int VNV_MAX = 64;  // 16-byte loads per lane (streamed, not held)
 constexpr int VNF = 8;       // 16-byte loads per lane held in VGPRs by the fast path
 constexpr int VGMAX = 64;
-constexpr int VRMAX = 8192;  // rows (B*T) per call: the counters live at fixed offsets so any call finds them zero
+constexpr int VRMAX = 8192;  // rows (B*T) per call: the slots of the row-token area
 
 // A workgroup's partial: five 64-bit words, each the call's tag (high half) over 32 bits of payload: the first-max
 // key (high, low), the finite maximum's bits, sum-exp's float64 bits (high, low). A 64-bit store is single-copy
@@ -481,7 +481,7 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   int gmin = (vocab_valid + chmax - 1) / chmax;
   if (gmin > VGMAX) return fail(VS_EINVAL, "vs_verify_greedy: vocab_valid too large");
   // About NVT 16-byte loads per lane (measured best on MI355X: less work per workgroup
-  // adds merge and arrival overhead, more lengthens each workgroup's chain), but never more workgroups than are
+  // adds merge overhead, more lengthens each workgroup's chain), but never more workgroups than are
   // resident at once (a second wave would start only after the first finished).
   constexpr int NVT = 6;
   const void* kfn = dtype == VS_F32 ? (const void*)vs_verify_kernel<VS_F32>
