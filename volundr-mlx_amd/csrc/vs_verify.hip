@@ -34,9 +34,10 @@ struct VPart {
 };
 static_assert(sizeof(VPart) == 64, "VPart layout");
 constexpr int VPW = 5;  // words in use
-// Wall-clock bound (100 MHz ticks, 2 ms) on a finisher's wait; reached only if the device stopped running the
-// launch's other workgroups (the row then reports token -1, which no draft matches).
-constexpr uint64_t VWAIT_TICKS = 200000;
+// Wall-clock bound (100 MHz ticks, 100 ms) on a finisher's wait: a launch's workgroups are all resident on an
+// otherwise idle device, so it is reached only if other work held CUs for that long; the row then reports token -1
+// (which no draft matches).
+constexpr uint64_t VWAIT_TICKS = 10000000;
 
 struct VerifyArgs {
   const void* logits;
