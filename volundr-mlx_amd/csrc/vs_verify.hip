@@ -402,6 +402,12 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     }
     VS_TR(A, 3);
     const u64 bam = wave_max(k);
+    const int req = row / A.T, tp = row - req * A.T;
+    const int32_t tok = bam ? (int32_t)key_index(bam) : -1;
+    if (t == 0) {  // the token first: the request's finisher waits for it, not for the logprob
+      if (tp < A.T - 1) st_dev(&rowtok[row], tag | (u64)(uint32_t)tok);
+      A.out_argmax[row] = tok;
+    }
     const float M = wave_max(mm);
     // the rescaling factors and the logarithm in float (the logprob's tolerance is 1e-5 relative): v_exp_f32 of
     // (m - M) log2 e, and log(S) = log1p(S - 1) with S >= 1 (it holds the maximum's own term), which keeps the float
@@ -409,44 +415,40 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     const float L2E = 1.44269504088896340736f;
     const double S =
         wave_sum((e > 0.0 && is_finite(M)) ? e * (double)__builtin_amdgcn_exp2f((mm - M) * L2E) : 0.0);
-    const int req = row / A.T, tp = row - req * A.T;
-    const int32_t tok = bam ? (int32_t)key_index(bam) : -1;
-    if (t == 0) {
+    if (t == 0 && A.out_lp) {
       const float xj = am_is_nan(bam) ? __builtin_nanf("") : key_value(bam);
-      if (A.out_lp)
-        A.out_lp[row] =
-            (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f;
-      A.out_argmax[row] = tok;
-      if (tp < A.T - 1) st_dev(&rowtok[row], tag | (u64)(uint32_t)tok);
+      A.out_lp[row] =
+          (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f;
     }
-    // the request's last row: its accept length (specdec.py:327), the other rows' tokens reloaded until they show
-    // the tag, 64 positions per ballot, stopping at the first mismatch
-    if (tp == A.T - 1) {
-      const int32_t* dr = A.drafts + (size_t)req * (A.T - 1);
-      int nacc = 0;
-      for (int base = 0; base < A.T - 1; base += WAVE) {
-        const int i = base + t;
-        bool stop = i >= A.T - 1;
-        if (!stop) {
-          const u64* wp = &rowtok[(size_t)req * A.T + i];
-          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-          u64 w;
-          for (;;) {
-            w = ld_dev(wp);
-            if ((w & 0xFFFFFFFF00000000ull) == tag || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
-            __builtin_amdgcn_s_sleep(1);
-          }
-          stop = (w & 0xFFFFFFFF00000000ull) != tag || dr[i] != (int32_t)(uint32_t)w;
+  } else if (t < 2 * WAVE && row % A.T == A.T - 1) {
+    // the request's last row: its accept length (specdec.py:327), computed by the finisher's second wave while the
+    // first merges the row (row T - 1 has no draft of its own): the other rows' tokens reloaded until they show the
+    // tag, 64 positions per ballot, stopping at the first mismatch
+    const int req = row / A.T, ln = t - WAVE;
+    const int32_t* dr = A.drafts + (size_t)req * (A.T - 1);
+    int nacc = 0;
+    for (int base = 0; base < A.T - 1; base += WAVE) {
+      const int i = base + ln;
+      bool stop = i >= A.T - 1;
+      if (!stop) {
+        const u64* wp = &rowtok[(size_t)req * A.T + i];
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        u64 w;
+        for (;;) {
+          w = ld_dev(wp);
+          if ((w & 0xFFFFFFFF00000000ull) == tag || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
+          __builtin_amdgcn_s_sleep(1);
         }
-        const unsigned long long mb2 = __ballot(stop);
-        if (mb2) {
-          nacc += __ffsll((long long)mb2) - 1;
-          break;
-        }
-        nacc += WAVE;
+        stop = (w & 0xFFFFFFFF00000000ull) != tag || dr[i] != (int32_t)(uint32_t)w;
       }
-      if (t == 0) A.out_accept[req] = nacc;
+      const unsigned long long mb2 = __ballot(stop);
+      if (mb2) {
+        nacc += __ffsll((long long)mb2) - 1;
+        break;
+      }
+      nacc += WAVE;
     }
+    if (ln == 0) A.out_accept[req] = nacc;
   }
   VS_TR_FLUSH(A);
 }
