@@ -300,7 +300,6 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   const int t0 = (int)((long long)wg * A.ntiles / P), t1 = (int)((long long)(wg + 1) * A.ntiles / P);
   const int rounds = (t1 - t0 + LNW * NTW - 1) / (LNW * NTW);
   const LParts parts = lparts(A.ws, A.R);
-  __shared__ uint32_t last_flag;
   VS_TR_DECL(A);
   VS_TR(A, 0);
   // accept lengths start at T-1 (every draft accepted); the merge lowers them to the first mismatch. A coherent
@@ -719,43 +718,45 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     const u64 kw = wave_max(k);
     const float mw = wave_max(m);
     const int okw = __all(ok) ? 1 : 0;
+    __shared__ int okf[LNW];
     if (ln == 0) {
       rk[wv][0] = kw;
       rm[wv][0] = mw;
-      last_flag = 1;
+      okf[wv] = okw;
     }
     __syncthreads();
-    if (ln == 0 && !okw) last_flag = 0;  // any wave's failure clears it (benign race: all write 0)
     u64 K0 = rk[0][0];
     float M = rm[0][0];
+    bool good = okf[0] != 0;
 #pragma unroll
     for (int q = 1; q < LNW; ++q) {
       K0 = rk[q][0] > K0 ? rk[q][0] : K0;
       M = rm[q][0] > M ? rm[q][0] : M;
+      good = good && okf[q] != 0;
+    }
+    if (t == 0) {  // the token and the accept length first (their stores complete while the logprob is computed)
+      const int32_t tok = good ? (int32_t)key_index(K0) : -1;
+      A.out_argmax[p] = tok;
+      const int b = p / A.T, tp = p % A.T;
+      if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
     }
     const float L2E = 1.44269504088896340736f;
     const double sw =
         wave_sum((sv > 0.0 && is_finite(M)) ? sv * (double)__builtin_amdgcn_exp2f((m - M) * L2E) : 0.0);
     if (ln == 0) rs[wv][0] = sw;
     __syncthreads();
-    if (t == 0) {
+    if (t == 0 && A.out_lp) {
       double S = 0.0;
 #pragma unroll
       for (int q = 0; q < LNW; ++q) S += rs[q][0];
       VS_TR(A, 24);
-      const bool good = last_flag != 0;
       const float xj = am_is_nan(K0) ? __builtin_nanf("") : key_value(K0);
-      const int32_t tok = good ? (int32_t)key_index(K0) : -1;
-      A.out_argmax[p] = tok;
       // log(S) = log1p(S - 1): S >= 1 (the maximum's own term), so the float log keeps its relative accuracy also
       // when one token dominates (S - 1 tiny)
-      if (A.out_lp)
-        A.out_lp[p] = !good ? __builtin_nanf("")
-                            : (is_finite(xj) && S > 0.0)
-                                  ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0))))
-                                  : 0.0f;
-      const int b = p / A.T, tp = p % A.T;
-      if (tp < A.T - 1 && A.drafts[(size_t)b * (A.T - 1) + tp] != tok) atomicMin(&A.out_accept[b], tp);
+      A.out_lp[p] = !good ? __builtin_nanf("")
+                          : (is_finite(xj) && S > 0.0)
+                                ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0))))
+                                : 0.0f;
     }
   }
   VS_TR(A, 22);
