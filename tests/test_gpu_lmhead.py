@@ -78,10 +78,12 @@ def test_lmhead_verify_shapes(dev, B, T):
     _check(o, got, h, w, drafts, B, T, vv)
 
 
-@pytest.mark.parametrize("B,T,N", [(4, 17, 900), (1, 17, 200)])
+@pytest.mark.parametrize("B,T,N", [(4, 17, 900), (1, 17, 200), (1, 17, 600), (1, 17, 5003)])
 def test_lmhead_fewer_workgroups_than_positions(dev, B, T, N):
     """A vocabulary of fewer 16-row tiles than positions gives fewer workgroups than positions, so a second launch
-    merges the partials instead of one workgroup per position."""
+    merges the partials instead of one workgroup per position (N = 900 at 68 positions, N = 200 at 17); N = 600
+    merges in the launch with 38 workgroups, between calls with 256 on the same workspace (every partial slot
+    belongs to one position and one workgroup, whatever the grid)."""
     K = 1024
     vv = N - 7
     h, w, drafts = _case(B * 1000 + N, B, T, K, N, scale=4.0)

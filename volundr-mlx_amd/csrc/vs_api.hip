@@ -1,7 +1,6 @@
 // vs_api.hip - library-wide C entry points: error text, workspace zeroing, version; cached device properties.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -15,13 +14,6 @@ unsigned long long* g_trace = nullptr;
 unsigned g_spin_limit = 0;
 thread_local int g_cooperative = 0;
 unsigned g_debug = 0;
-
-uint32_t next_call_tag() {
-  static std::atomic<uint32_t> calls{0};
-  uint32_t tag = calls.fetch_add(1u) + 1u;
-  if (tag == 0) tag = calls.fetch_add(1u) + 1u;
-  return tag;
-}
 
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(int code, const std::string& msg) {

@@ -26,10 +26,6 @@ extern thread_local int g_cooperative;
 // VS_DEBUG_* testing flags (set by vs_set_debug).
 extern unsigned g_debug;
 
-// A process-wide call counter (never 0): kernels that exchange tagged words between workgroups take it as the
-// call's tag, so no word an earlier call left can pass for the current call's.
-uint32_t next_call_tag();
-
 // Phase-timestamp buffer of development builds (VS_TRACE); always null in the shipped library.
 extern unsigned long long* g_trace;
 

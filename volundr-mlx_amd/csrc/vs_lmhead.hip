@@ -36,7 +36,7 @@ constexpr int LNW = LNT / WAVE;     // waves per workgroup
 constexpr int KS = 32;              // k per MFMA
 constexpr int LRMAX = 80;           // positions per call (5 tiles of 16)
 constexpr int LPMAX = 2048;         // workgroups per launch
-constexpr size_t LWS_HEAD = 256;    // workspace head (unused, kept for the layout)
+constexpr size_t LWS_HEAD = 256;    // workspace head (unused)
 constexpr int LMPW = 4;             // positions one wave of the merging workgroup reduces at a time
 
 // Workgroup partials, position-major and one array per field ([R][P] each), so that the merge's lanes, which walk
@@ -54,9 +54,12 @@ __device__ __forceinline__ LParts lparts(char* ws, int R) {
   return q;
 }
 
-// merge_in partials: five 64-bit words per (position, workgroup), [R][P] at the workspace's partial area, each
-// the call's tag (high half) over 32 bits of payload (first-max key high/low, maximum, sum-exp high/low); a 64-bit
-// store is single-copy atomic, so a word that shows the tag holds this call's payload.
+// merge_in partials: five 64-bit words per (position, workgroup), [R][LNT] at the workspace's partial area (slot
+// (p, wg) is only ever written by workgroup wg for position p, whatever the grid size of the call), each
+// the tag (high half) over 32 bits of payload (first-max key high/low, maximum, sum-exp high/low); a 64-bit store
+// is single-copy atomic, so a word that shows the tag holds this call's payload. Tag = the slot's epoch (word 7)
+// + 1; the merging workgroup advances it once it has read the slot, and the writer reads it before it stores, so
+// that calls, and a captured graph's replays, tag their words apart whatever shapes they have.
 constexpr int LTW = 8;  // words per partial slot (5 used)
 __device__ __forceinline__ u64* ltparts(char* ws) { return (u64*)(ws + LWS_HEAD); }
 // Wall-clock bound (100 MHz ticks, 100 ms) on a merging workgroup's wait for the other workgroups' partials: every
@@ -71,7 +74,6 @@ struct LHArgs {
   int64_t ldw;
   int N, vv, K, B, T, R, ntiles;
   int merge_in;  // workgroup p merges position p from tagged partials (else vs_lmhead_merge_kernel does)
-  uint32_t tag;  // merge_in: the call's tag (never 0)
   const int32_t* drafts;  // [B, T-1]
   int32_t* out_argmax;    // [R]
   int32_t* out_accept;    // [B]
@@ -309,6 +311,9 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
     publish_wait();  // complete before this workgroup's partials (stored much later) can release a merge
   }
+  // merge_in: the epoch of this workgroup's slot for position t (this thread stores the partial), read now
+  const uint32_t ep_t =
+      (!SAMPLE && A.merge_in && t < R) ? (uint32_t)ld_dev(ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW + 7) : 0u;
   if constexpr (SAMPLE) {
     if (t < 16) {
       int vl = 0, c = LS_UNSUPPORTED;
@@ -633,8 +638,8 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       q.se[ix] = s;
       q.nfin[ix] = nf;
     } else if (A.merge_in) {
-      u64* w = ltparts(A.ws) + ((size_t)t * P + wg) * LTW;
-      const u64 tg = (u64)A.tag << 32;
+      u64* w = ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW;
+      const u64 tg = (u64)(ep_t + 1u) << 32;
       const u64 sb = (u64)__double_as_longlong(s);
       st_dev(&w[0], tg | (k >> 32));
       st_dev(&w[1], tg | (k & 0xFFFFFFFFull));
@@ -688,13 +693,14 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   __syncthreads();  // the workgroup reduction above is done with rk / rm / rs
   {
     const int p = wg;
-    const u64 tg = (u64)A.tag << 32;
     u64 k = 0;
     float m = -__builtin_inff();
     double sv = 0.0;
     int ok = 1;
     if (t < P) {
-      const u64* w = ltparts(A.ws) + ((size_t)p * P + t) * LTW;
+      u64* w = ltparts(A.ws) + ((size_t)p * LNT + t) * LTW;
+      const uint32_t se = (uint32_t)ld_dev(&w[7]);  // the slot's epoch: only this thread changes it
+      const u64 tg = (u64)(se + 1u) << 32;
       const uint64_t c0 = __builtin_amdgcn_s_memrealtime();
       u64 v[5];
       for (;;) {
@@ -710,6 +716,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
         }
         __builtin_amdgcn_s_sleep(2);
       }
+      w[7] = se + 1u;  // read in this call (a plain store: read by later calls only)
       k = (v[0] << 32) | (v[1] & 0xFFFFFFFFull);
       m = __uint_as_float((uint32_t)v[2]);
       sv = __longlong_as_double((long long)((v[3] << 32) | (v[4] & 0xFFFFFFFFull)));
@@ -944,7 +951,6 @@ extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W
   a.T = T;
   a.R = (int)R;
   a.ntiles = (N + 15) / 16;
-  a.tag = next_call_tag();
   a.drafts = drafts;
   a.out_argmax = out_argmax;
   a.out_accept = out_accept;

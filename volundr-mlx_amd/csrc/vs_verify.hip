@@ -7,10 +7,13 @@
 //
 // Each (b, t) row is split into G chunks, one 256-thread workgroup each, so B*T = 17..68 rows still fill the
 // 256 CUs. A workgroup reads its chunk once with 16-byte loads into VGPRs, reduces (first-max key, finite max) with
-// wave64 reductions, then sum(exp(x - max)). No atomics: every word a workgroup publishes carries the call's tag
-// (a host counter), the row's last workgroup (g = G - 1) reloads the row's G partials until each shows the tag and
-// merges them, and the finisher of a request's last row reloads the request's other tokens the same way and
-// computes the accept length. A launch holds only as many rows as the device keeps resident at once, so every
+// wave64 reductions, then sum(exp(x - max)). No atomics: every word a workgroup publishes carries a tag, an epoch
+// + 1 read from the workspace; the row's last workgroup (g = G - 1) reloads the row's G partials until each shows
+// the tag and merges them, and the finisher of a request's last row reloads the request's other tokens the same
+// way and computes the accept length. Each slot's epoch is advanced only by its reader, after it has read the slot
+// in the call (its writers read the epoch before they store), and a slot is only ever written for one row (partial
+// slot (row, g), token slot row), so no word a previous call or graph replay left can pass for the current one's,
+// whatever shapes the calls had. A launch holds only as many rows as the device keeps resident at once, so every
 // workgroup a finisher waits for is running or done.
 #include "vs_common.h"
 #include "vs_host.h"
@@ -26,12 +29,13 @@ constexpr int VNF = 8;       // 16-byte loads per lane held in VGPRs by the fast
 constexpr int VGMAX = 64;
 constexpr int VRMAX = 8192;  // rows (B*T) per call: the slots of the row-token area
 
-// A workgroup's partial: five 64-bit words, each the call's tag (high half) over 32 bits of payload: the first-max
-// key (high, low), the finite maximum's bits, sum-exp's float64 bits (high, low). A 64-bit store is single-copy
-// atomic, so a word that shows the current tag holds the current payload.
+// A workgroup's partial slot: five 64-bit words, each the tag (high half) over 32 bits of payload: the first-max
+// key (high, low), the finite maximum's bits, sum-exp's float64 bits (high, low); word 7 is the slot's epoch, and
+// tag = epoch + 1. A 64-bit store is single-copy atomic, so a word that shows the tag holds this call's payload.
 struct VPart {
   u64 w[8];
 };
+constexpr int VEPW = 7;  // the epoch word
 static_assert(sizeof(VPart) == 64, "VPart layout");
 constexpr int VPW = 5;  // words in use
 // Wall-clock bound (100 MHz ticks, 100 ms) on a finisher's wait: a launch's workgroups are all resident on an
@@ -48,9 +52,8 @@ struct VerifyArgs {
   int32_t* out_argmax;
   int32_t* out_accept;
   float* out_lp;
-  int row0;       // first row of this launch
-  uint32_t tag;   // the call's tag (never 0), shared by its launches
-  char* ws;  // [VRMAX] row tokens (tag | token) | [R*G] VPart
+  int row0;  // first row of this launch
+  char* ws;  // [VRMAX] token slots (tag | token, epoch) | [R][VGMAX] VPart
   unsigned long long* trace;  // development builds only (VS_TRACE); null otherwise
 };
 
@@ -151,9 +154,25 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   const int nb = gridDim.x, b = blockIdx.x;
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int row = A.row0 + l / G, g = l % G;
-  u64* rowtok = (u64*)A.ws;
-  VPart* parts = (VPart*)(A.ws + 8 * VRMAX);
-  const u64 tag = (u64)A.tag << 32;
+  u64* rowtok = (u64*)A.ws;  // token slot r: words 2r (tag | token) and 2r + 1 (epoch)
+  VPart* parts = (VPart*)(A.ws + 16 * VRMAX) + (size_t)row * VGMAX;  // slot g: written by this row's workgroup g only
+  // Epochs: each slot's epoch is advanced only by its reader, after it has read the slot in the call; its writer
+  // reads it before it stores (so both use the same value), and the tag is epoch + 1 (never the 0 of a zeroed
+  // workspace). Each workgroup reads its own partial slot's epoch, the row's finisher also its token slot's, and the
+  // second wave of a request's last-row finisher the request's first 64 token slots'. They are loaded right after
+  // the logits (issued after them, so that the waits for the logits do not wait for these); every epoch sits in its
+  // own slot, so no address is read by many workgroups at once.
+  const int req = row / A.T, tp = row - req * A.T;
+  uint32_t ep = 0, tep = 0;
+  u64 qep = 0;
+  auto load_epochs = [&]() {
+    ep = (uint32_t)ld_dev(&parts[g].w[VEPW]);
+    if (g == G - 1) {
+      tep = (uint32_t)ld_dev(&rowtok[2 * (size_t)row + 1]);
+      if (tp == A.T - 1 && t >= WAVE && t < 2 * WAVE && t - WAVE < A.T - 1)
+        qep = ld_dev(&rowtok[2 * ((size_t)req * A.T + (t - WAVE)) + 1]);
+    }
+  };
 
   const int lo = g * A.CH;
   const int hi = min(A.vv, lo + A.CH);
@@ -176,6 +195,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       base = (u < A.NV && base < hi) ? base : lo;  // clamped into the row: the values are masked below
       rv[u] = A.vec_ok ? *(const uint4*)(rowp + (int64_t)base * (DT == VS_F32 ? 4 : 2)) : make_uint4(0, 0, 0, 0);
     }
+    load_epochs();
     // a vector that is not whole inside the chunk (the row's last, or any when unaligned) is assembled element by
     // element, -inf past the end, so both passes below read registers only
 #pragma unroll
@@ -295,6 +315,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   };
   uint4 cur[U], nxt[U];
   load(cur, 0);
+  load_epochs();
   for (int j0 = 0; j0 < A.NV; j0 += U) {
     if (j0 + U < A.NV) load(nxt, j0 + U);  // the next batch is in flight while this one is reduced
 #pragma unroll
@@ -358,7 +379,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
 #pragma unroll
       for (int w = 0; w < VNW; ++w)
         sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)__builtin_amdgcn_exp2f((redf[w] - mb) * L2E) : 0.0;
-      VPart* pp = parts + (size_t)row * G + g;
+      VPart* pp = parts + g;
+      const u64 tag = (u64)(ep + 1u) << 32;
       const u64 sbits = (u64)__double_as_longlong(sb);
       st_dev(&pp->w[0], tag | (kb >> 32));
       st_dev(&pp->w[1], tag | (kb & 0xFFFFFFFFull));
@@ -372,6 +394,8 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     VS_TR_FLUSH(A);
     return;
   }
+  // this row's token slot: the request's finisher advances its epoch after it has read the token
+  const u64 qtag = (u64)(tep + 1u) << 32;
   // the row's finisher: merge the G partials in one wave (G <= 64), each reloaded until all its words show the tag
   if (t < WAVE) {
     u64 k = 0;
@@ -379,18 +403,21 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     double e = 0.0;
     bool ok = true;
     if (t < G) {
-      const VPart* pp = parts + (size_t)row * G + t;
+      VPart* pp = parts + t;
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       u64 w[VPW];
+      const uint32_t se = (uint32_t)ld_dev(&pp->w[VEPW]);  // the slot's epoch: only this lane changes it
+      const u64 stag = (u64)(se + 1u) << 32;
       for (;;) {
 #pragma unroll
         for (int i = 0; i < VPW; ++i) w[i] = ld_dev(&pp->w[i]);
         ok = true;
 #pragma unroll
-        for (int i = 0; i < VPW; ++i) ok = ok && (w[i] & 0xFFFFFFFF00000000ull) == tag;
+        for (int i = 0; i < VPW; ++i) ok = ok && (w[i] & 0xFFFFFFFF00000000ull) == stag;
         if (ok || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
         __builtin_amdgcn_s_sleep(1);
       }
+      pp->w[VEPW] = se + 1u;  // read in this call (a plain store: read by later calls only)
       k = (w[0] << 32) | (w[1] & 0xFFFFFFFFull);
       mm = __uint_as_float((uint32_t)w[2]);
       e = __longlong_as_double((long long)((w[3] << 32) | (w[4] & 0xFFFFFFFFull)));
@@ -402,10 +429,9 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
     }
     VS_TR(A, 3);
     const u64 bam = wave_max(k);
-    const int req = row / A.T, tp = row - req * A.T;
     const int32_t tok = bam ? (int32_t)key_index(bam) : -1;
     if (t == 0) {  // the token first: the request's finisher waits for it, not for the logprob
-      if (tp < A.T - 1) st_dev(&rowtok[row], tag | (u64)(uint32_t)tok);
+      if (tp < A.T - 1) st_dev(&rowtok[2 * (size_t)row], qtag | (u64)(uint32_t)tok);
       A.out_argmax[row] = tok;
     }
     const float M = wave_max(mm);
@@ -420,33 +446,42 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
       A.out_lp[row] =
           (is_finite(xj) && S > 0.0) ? (float)((double)xj - ((double)M + (double)log1pf((float)(S - 1.0)))) : 0.0f;
     }
-  } else if (t < 2 * WAVE && row % A.T == A.T - 1) {
+  } else if (t < 2 * WAVE && tp == A.T - 1) {
     // the request's last row: its accept length (specdec.py:327), computed by the finisher's second wave while the
     // first merges the row (row T - 1 has no draft of its own): the other rows' tokens reloaded until they show the
-    // tag, 64 positions per ballot, stopping at the first mismatch
-    const int req = row / A.T, ln = t - WAVE;
+    // tag, 64 positions per ballot, the accept length at the first mismatch
+    const int ln = t - WAVE;
     const int32_t* dr = A.drafts + (size_t)req * (A.T - 1);
     int nacc = 0;
+    bool found = false;
     for (int base = 0; base < A.T - 1; base += WAVE) {
       const int i = base + ln;
       bool stop = i >= A.T - 1;
       if (!stop) {
-        const u64* wp = &rowtok[(size_t)req * A.T + i];
+        const size_t ti = (size_t)req * A.T + i;
+        const uint32_t te = (uint32_t)(base == 0 ? qep : ld_dev(&rowtok[2 * ti + 1]));
+        const u64 ttag = (u64)(te + 1u) << 32;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         u64 w;
         for (;;) {
-          w = ld_dev(wp);
-          if ((w & 0xFFFFFFFF00000000ull) == tag || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
+          w = ld_dev(&rowtok[2 * ti]);
+          if ((w & 0xFFFFFFFF00000000ull) == ttag || __builtin_amdgcn_s_memrealtime() - t0 > VWAIT_TICKS) break;
           __builtin_amdgcn_s_sleep(1);
         }
-        stop = (w & 0xFFFFFFFF00000000ull) != tag || dr[i] != (int32_t)(uint32_t)w;
+        rowtok[2 * ti + 1] = te + 1u;  // read in this call (a plain store: read by later calls only)
+        stop = (w & 0xFFFFFFFF00000000ull) != ttag || dr[i] != (int32_t)(uint32_t)w;
       }
+      // every token slot is read (and its epoch advanced), also past the first mismatch: a slot left unread would
+      // keep an epoch whose tag this call's token carries
       const unsigned long long mb2 = __ballot(stop);
-      if (mb2) {
-        nacc += __ffsll((long long)mb2) - 1;
-        break;
+      if (!found) {
+        if (mb2) {
+          nacc += __ffsll((long long)mb2) - 1;
+          found = true;
+        } else {
+          nacc += WAVE;
+        }
       }
-      nacc += WAVE;
     }
     if (ln == 0) A.out_accept[req] = nacc;
   }
@@ -460,7 +495,7 @@ using namespace vs;
 extern "C" size_t vs_verify_workspace_bytes(int B, int T, int V) {
   (void)V;
   size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
-  return 8 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;
+  return 16 * (size_t)VRMAX + sizeof(VPart) * R * VGMAX;  // token slots, partial slots
 }
 
 extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int V, int64_t ld, int vocab_valid,
@@ -520,7 +555,6 @@ extern "C" int vs_verify_greedy(const void* logits, int dtype, int B, int T, int
   a.out_lp = out_logprob;
   a.ws = (char*)ws;
   a.trace = g_trace;
-  a.tag = next_call_tag();
   // rows per launch: all of a launch's workgroups resident at once (finishers wait for their row's workgroups)
   const int cap = per_cu * dv->cus;
   int rpl = cap / G;
