@@ -311,9 +311,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     for (int b = t; b < A.B; b += LNT) st_dev(&A.out_accept[b], A.T - 1);
     publish_wait();  // complete before this workgroup's partials (stored much later) can release a merge
   }
-  // merge_in: the epoch of this workgroup's slot for position t (this thread stores the partial), read now
-  const uint32_t ep_t =
-      (!SAMPLE && A.merge_in && t < R) ? (uint32_t)ld_dev(ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW + 7) : 0u;
+
   if constexpr (SAMPLE) {
     if (t < 16) {
       int vl = 0, c = LS_UNSUPPORTED;
@@ -414,6 +412,10 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     wb[j][0] = *(const uint4*)(wbase + wo0[j]);
     wb[j][1] = *(const uint4*)(wbase + wo1[j]);
   }
+  // merge_in: the epoch of this workgroup's slot for position t (this thread stores the partial), loaded after the
+  // first weights (so that their waits do not wait for it)
+  const uint32_t ep_t =
+      (!SAMPLE && A.merge_in && t < R) ? (uint32_t)ld_dev(ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW + 7) : 0u;
   __syncthreads();  // the padded rows are zeroed
   LH_HSTORE(0)
   __syncthreads();
