@@ -108,7 +108,7 @@ def test_nonfinite_across_workgroups(dev, dtype):
     assert np.all(np.abs(g[0, fin] - lp[0, fin]) <= 1e-5 * np.abs(lp[0, fin]) + 1e-10), (g[0, fin], lp[0, fin])
 
 
-@pytest.mark.parametrize("T", [2, 32, 33, 34, 40])
+@pytest.mark.parametrize("T", [2, 32, 33, 34, 40, 65, 70])
 def test_accept_lengths_around_the_packed_limit(dev, T):
     """Blocks of up to 33 positions carry the accept information in one packed word, longer ones take the
     counter-and-reload path: every accept length 0..T-1 on both sides of the limit."""
@@ -149,3 +149,21 @@ def test_repeated_calls_on_one_workspace(dev):
         drafts = np.argmax(x, -1)[:, :-1].astype(np.int32).copy()
         drafts[0, rep % (T - 1)] += 1
         check(dev, x, drafts, V, torch.float32, f"shape {B}x{T}x{V}")
+
+
+def test_long_blocks_accept_lengths(dev):
+    """Blocks of 130 positions: the request's finisher reads its tokens 64 per ballot over three rounds, all of them
+    (also past the first mismatch, whose round decides the accept length); a second call on the same workspace."""
+    rng = np.random.default_rng(31)
+    T, V = 130, 2000
+    want_acc = [0, 63, 64, 100, 129]
+    B = len(want_acc)
+    for rep in range(2):
+        x = rng.standard_normal((B, T, V)).astype(np.float32)
+        tok = np.argmax(x, -1)
+        drafts = tok[:, :-1].astype(np.int32).copy()
+        for b, a in enumerate(want_acc):
+            if a < T - 1:
+                drafts[b, a] = (drafts[b, a] + 1) % V
+        o = check(dev, x, drafts, V, torch.float32, f"T={T} rep {rep}")
+        assert o.accept.cpu().tolist() == want_acc
