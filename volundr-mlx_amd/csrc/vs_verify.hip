@@ -165,8 +165,13 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   const int req = row / A.T, tp = row - req * A.T;
   uint32_t ep = 0, tep = 0;
   u64 qep = 0;
+  // Partial slots: one per wave when the row's waves fit one merging wave (G * VNW <= 64: no workgroup reduction),
+  // else one per workgroup.
+  const bool per_wave = G * VNW <= WAVE;
+  const int nslots = per_wave ? G * VNW : G;
+  VPart* myslot = parts + (per_wave ? g * VNW + t / WAVE : g);
   auto load_epochs = [&]() {
-    ep = (uint32_t)ld_dev(&parts[g].w[VEPW]);
+    ep = (uint32_t)ld_dev(&myslot->w[VEPW]);
     if (g == G - 1) {
       tep = (uint32_t)ld_dev(&rowtok[2 * (size_t)row + 1]);
       if (tp == A.T - 1 && t >= WAVE && t < 2 * WAVE && t - WAVE < A.T - 1)
@@ -353,21 +358,32 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   }
   }
   VS_TR(A, 1);
-  // workgroup merge of the key and the (m, se) pairs: each wave reduces its lanes (max, then the sum rescaled to
-  // the wave's max), one LDS exchange and one barrier, then thread 0 merges the VNW waves
+  // each wave reduces its lanes (the key's maximum, the maximum, then the sum rescaled to it); with a slot per wave
+  // lane 0 publishes the wave's partial, else one LDS exchange and one barrier, then thread 0 merges the VNW waves
+  auto publish = [&](VPart* pp, u64 kb, float mb, double sb) {
+    const u64 tag = (u64)(ep + 1u) << 32;
+    const u64 sbits = (u64)__double_as_longlong(sb);
+    st_dev(&pp->w[0], tag | (kb >> 32));
+    st_dev(&pp->w[1], tag | (kb & 0xFFFFFFFFull));
+    st_dev(&pp->w[2], tag | (u64)__float_as_uint(mb));
+    st_dev(&pp->w[3], tag | (sbits >> 32));
+    st_dev(&pp->w[4], tag | (sbits & 0xFFFFFFFFull));
+  };
   {
     const int wv = t / WAVE;
     const u64 kw = wave_max(am);
     const float mw = wave_max(m);
     const float L2E = 1.44269504088896340736f;
     const double sw = wave_sum((se > 0.0 && is_finite(mw)) ? se * (double)__builtin_amdgcn_exp2f((m - mw) * L2E) : 0.0);
-    if (lane_id() == 0) {
+    if (per_wave) {
+      if (lane_id() == 0) publish(myslot, kw, mw, sw);
+    } else if (lane_id() == 0) {
       red64[wv] = kw;
       redf[wv] = mw;
       redd[wv] = sw;
     }
-    __syncthreads();
-    if (t == 0) {
+    if (!per_wave) __syncthreads();  // uniform
+    if (!per_wave && t == 0) {
       u64 kb = red64[0];
       float mb = redf[0];
 #pragma unroll
@@ -379,14 +395,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
 #pragma unroll
       for (int w = 0; w < VNW; ++w)
         sb += (redd[w] > 0.0 && is_finite(mb)) ? redd[w] * (double)__builtin_amdgcn_exp2f((redf[w] - mb) * L2E) : 0.0;
-      VPart* pp = parts + g;
-      const u64 tag = (u64)(ep + 1u) << 32;
-      const u64 sbits = (u64)__double_as_longlong(sb);
-      st_dev(&pp->w[0], tag | (kb >> 32));
-      st_dev(&pp->w[1], tag | (kb & 0xFFFFFFFFull));
-      st_dev(&pp->w[2], tag | (u64)__float_as_uint(mb));
-      st_dev(&pp->w[3], tag | (sbits >> 32));
-      st_dev(&pp->w[4], tag | (sbits & 0xFFFFFFFFull));
+      publish(myslot, kb, mb, sb);
     }
   }
   VS_TR(A, 2);
@@ -396,13 +405,13 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   }
   // this row's token slot: the request's finisher advances its epoch after it has read the token
   const u64 qtag = (u64)(tep + 1u) << 32;
-  // the row's finisher: merge the G partials in one wave (G <= 64), each reloaded until all its words show the tag
+  // the row's finisher: merge the row's partials in one wave (<= 64), each reloaded until all its words show the tag
   if (t < WAVE) {
     u64 k = 0;
     float mm = -__builtin_inff();
     double e = 0.0;
     bool ok = true;
-    if (t < G) {
+    if (t < nslots) {
       VPart* pp = parts + t;
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       u64 w[VPW];
