@@ -8,11 +8,11 @@
 // Each (b, t) row is split into G chunks, one 256-thread workgroup each, so B*T = 17..68 rows still fill the
 // 256 CUs. A workgroup reads its chunk once with 16-byte loads into VGPRs, reduces (first-max key, finite max) with
 // wave64 reductions, then sum(exp(x - max)). No atomics: every word a workgroup publishes carries a tag, an epoch
-// + 1 read from the workspace; the row's last workgroup (g = G - 1) reloads the row's G partials until each shows
+// + 1 read from the workspace; the row's last workgroup (g = G - 1) reloads the row's partials (one per wave, or per workgroup) until each shows
 // the tag and merges them, and the finisher of a request's last row reloads the request's other tokens the same
 // way and computes the accept length. Each slot's epoch is advanced only by its reader, after it has read the slot
 // in the call (its writers read the epoch before they store), and a slot is only ever written for one row (partial
-// slot (row, g), token slot row), so no word a previous call or graph replay left can pass for the current one's,
+// slot (row, s), token slot row), so no word a previous call or graph replay left can pass for the current one's,
 // whatever shapes the calls had. A launch holds only as many rows as the device keeps resident at once, so every
 // workgroup a finisher waits for is running or done.
 #include "vs_common.h"
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(VNT) void vs_verify_kernel(VerifyArgs A) {
   const int l = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int row = A.row0 + l / G, g = l % G;
   u64* rowtok = (u64*)A.ws;  // token slot r: words 2r (tag | token) and 2r + 1 (epoch)
-  VPart* parts = (VPart*)(A.ws + 16 * VRMAX) + (size_t)row * VGMAX;  // slot g: written by this row's workgroup g only
+  VPart* parts = (VPart*)(A.ws + 16 * VRMAX) + (size_t)row * VGMAX;  // this row's partial slots (written for it only)
   // Epochs: each slot's epoch is advanced only by its reader, after it has read the slot in the call; its writer
   // reads it before it stores (so both use the same value), and the tag is epoch + 1 (never the 0 of a zeroed
   // workspace). Each workgroup reads its own partial slot's epoch, the row's finisher also its token slot's, and the
