@@ -8,9 +8,9 @@
 // Each (b, t) row is split into G chunks, one 256-thread workgroup each, so B*T = 17..68 rows still fill the
 // 256 CUs. A workgroup reads its chunk once with 16-byte loads into VGPRs, reduces (first-max key, finite max) with
 // wave64 reductions, then sum(exp(x - max)). No atomics: every word a workgroup publishes carries a tag, an epoch
-// + 1 read from the workspace; the row's last workgroup (g = G - 1) reloads the row's partials (one per wave, or per workgroup) until each shows
-// the tag and merges them, and the finisher of a request's last row reloads the request's other tokens the same
-// way and computes the accept length. Each slot's epoch is advanced only by its reader, after it has read the slot
+// + 1 read from the workspace; the row's last workgroup (g = G - 1) reloads the row's partials (one per wave, or
+// one per workgroup) until each shows the tag and merges them, and the finisher of a request's last row reloads the
+// request's other tokens the same way and computes the accept length. Each slot's epoch is advanced only by its reader, after it has read the slot
 // in the call (its writers read the epoch before they store), and a slot is only ever written for one row (partial
 // slot (row, s), token slot row), so no word a previous call or graph replay left can pass for the current one's,
 // whatever shapes the calls had. A launch holds only as many rows as the device keeps resident at once, so every
