@@ -61,7 +61,10 @@ __device__ __forceinline__ LParts lparts(char* ws, int R) {
 // + 1; the merging workgroup advances it once it has read the slot, and the writer reads it before it stores, so
 // that calls, and a captured graph's replays, tag their words apart whatever shapes they have.
 constexpr int LTW = 8;  // words per partial slot (5 used)
-__device__ __forceinline__ u64* ltparts(char* ws) { return (u64*)(ws + LWS_HEAD); }
+// (after the position-major arrays of the second-launch merge, so that the two layouts never share words)
+__device__ __forceinline__ u64* ltparts(char* ws, int R) {
+  return (u64*)(ws + LWS_HEAD + (size_t)(8 + 8 + 4) * LPMAX * R);
+}
 // Wall-clock bound (100 MHz ticks, 100 ms) on a merging workgroup's wait for the other workgroups' partials: every
 // workgroup of the launch is resident on an otherwise idle device (one per CU), so it is reached only if other
 // work held CUs for that long; the position then reports token -1 (no draft matches it) and logprob NaN.
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
   // merge_in: the epoch of this workgroup's slot for position t (this thread stores the partial), loaded after the
   // first weights (so that their waits do not wait for it)
   const uint32_t ep_t =
-      (!SAMPLE && A.merge_in && t < R) ? (uint32_t)ld_dev(ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW + 7) : 0u;
+      (!SAMPLE && A.merge_in && t < R) ? (uint32_t)ld_dev(ltparts(A.ws, R) + ((size_t)t * LNT + wg) * LTW + 7) : 0u;
   __syncthreads();  // the padded rows are zeroed
   LH_HSTORE(0)
   __syncthreads();
@@ -640,7 +643,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       q.se[ix] = s;
       q.nfin[ix] = nf;
     } else if (A.merge_in) {
-      u64* w = ltparts(A.ws) + ((size_t)t * LNT + wg) * LTW;
+      u64* w = ltparts(A.ws, R) + ((size_t)t * LNT + wg) * LTW;
       const u64 tg = (u64)(ep_t + 1u) << 32;
       const u64 sb = (u64)__double_as_longlong(s);
       st_dev(&w[0], tg | (k >> 32));
@@ -700,7 +703,7 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
     double sv = 0.0;
     int ok = 1;
     if (t < P) {
-      u64* w = ltparts(A.ws) + ((size_t)p * LNT + t) * LTW;
+      u64* w = ltparts(A.ws, R) + ((size_t)p * LNT + t) * LTW;
       const uint32_t se = (uint32_t)ld_dev(&w[7]);  // the slot's epoch: only this thread changes it
       const u64 tg = (u64)(se + 1u) << 32;
       const uint64_t c0 = __builtin_amdgcn_s_memrealtime();
@@ -913,7 +916,7 @@ extern "C" int vs_lmhead_sample(const void* h, int64_t ldh, const void* W, int64
 
 extern "C" size_t vs_lmhead_workspace_bytes(int B, int T) {
   const size_t R = (B < 1 || T < 1) ? 1 : (size_t)B * T;
-  return LWS_HEAD + (size_t)(8 + 8 + 4) * LPMAX * R;
+  return LWS_HEAD + (size_t)(8 + 8 + 4) * LPMAX * R + (size_t)LTW * 8 * LNT * R;  // arrays, then tagged slots
 }
 
 extern "C" int vs_lmhead_verify_greedy(const void* h, int64_t ldh, const void* W, int64_t ldw, int N, int K,
