@@ -167,3 +167,39 @@ def test_long_blocks_accept_lengths(dev):
                 drafts[b, a] = (drafts[b, a] + 1) % V
         o = check(dev, x, drafts, V, torch.float32, f"T={T} rep {rep}")
         assert o.accept.cpu().tolist() == want_acc
+
+
+def _check_f32_floor(dev, x, drafts, vv, dtype, label):
+    """As check, with the logprob's absolute floor at 2^-22 instead of 1e-10: the kernel sums exp(x - max) in
+    float32 per lane, so a row where one token holds nearly all the mass (logprob near 0) carries the float32
+    rounding of a sum near 1 (the reference's own float32 log-softmax does too)."""
+    B, T, V = x.shape
+    xt = torch.from_numpy(x).to(dev).to(dtype)
+    ref_in = xt.float().cpu().numpy()
+    o = verify_greedy(xt, torch.from_numpy(drafts).to(dev) if T > 1 else None, vv)
+    torch.cuda.synchronize()
+    tok, acc, lp = VR.verify(ref_in, drafts, vv)
+    assert np.array_equal(o.argmax.cpu().numpy(), tok), label
+    assert np.array_equal(o.accept.cpu().numpy(), acc), label
+    g = o.logprobs.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(g - lp) <= 1e-5 * np.abs(lp) + 2.0 ** -22), (label, np.max(np.abs(g - lp)))
+
+
+def test_random_shapes_one_workspace(dev):
+    """60 seeded calls of random shape (B 1-8, T 1-40, V 100-20000, vocab_valid from V/2 to V) and dtype on one
+    workspace, each against the oracle: the exchange slots' epochs keep every call apart from the earlier ones.
+    Some rows are dominated by one token, hence the float32 floor of _check_f32_floor."""
+    rng = np.random.default_rng(123)
+    for it in range(60):
+        B, T, V = int(rng.integers(1, 9)), int(rng.integers(1, 41)), int(rng.integers(100, 20000))
+        vv = int(rng.integers(max(1, V // 2), V + 1))
+        dt = [torch.float32, torch.bfloat16, torch.float16][it % 3]
+        x = (rng.standard_normal((B, T, V)) * rng.uniform(0.5, 4)).astype(np.float32)
+        xt = torch.from_numpy(x).to(dev).to(dt)
+        ref = xt.float().cpu().numpy()
+        drafts = np.argmax(ref[..., :vv], -1)[:, :-1].astype(np.int32).copy() if T > 1 else np.zeros((B, 0), np.int32)
+        for b in range(B):
+            if T > 1 and rng.random() < 0.7:
+                j = int(rng.integers(0, T - 1))
+                drafts[b, j] = (drafts[b, j] + 1) % vv
+        _check_f32_floor(dev, ref, drafts, vv, dt, f"random {it}: B={B} T={T} V={V} vv={vv}")
