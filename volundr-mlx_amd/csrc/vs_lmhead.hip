@@ -709,6 +709,17 @@ __global__ __launch_bounds__(LNT) __attribute__((amdgpu_waves_per_eu(LNT / 256))
       const uint64_t c0 = __builtin_amdgcn_s_memrealtime();
       u64 v[5];
       for (;;) {
+        // one word polled while the workgroup is still streaming (a merging workgroup waits ~10 us for the last
+        // ones, and its reloads share the fabric with their weight reads), then all five
+        v[4] = ld_dev(&w[4]);
+        if ((v[4] & 0xFFFFFFFF00000000ull) != tg) {
+          if (__builtin_amdgcn_s_memrealtime() - c0 > LWAIT_TICKS) {
+            ok = 0;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          continue;
+        }
 #pragma unroll
         for (int i = 0; i < 5; ++i) v[i] = ld_dev(&w[i]);
         bool all = true;
